@@ -1,0 +1,246 @@
+"""MoE-layer decode benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
+
+A step is one MoE-layer decode step (router GEMV, softmax, top-k,
+renormalisation, routed SwiGLU experts, sigmoid-gated shared expert,
+weighted combine) for one batch of synthetic tokens, on weights resident in
+HBM.  The K timed steps cycle through `--replicas` distinct seeded layers
+(each with all E experts) and distinct inputs, so the bytes a step touches
+come from HBM, not from the 256 MB last-level cache.  The steps are
+captured in one HIP graph and replayed; the per-kernel durations come from
+HIP events around each stage in a separate eager pass queued behind a stall
+kernel.  Prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+
+CONFIGS = {
+    # name: (shape key, batch)
+    "qwen3.6-35b-a3b-q4-b1": ("qwen3.6-35b-a3b-q4", 1),
+    "qwen3-next-80b-a3b-q4-b1": ("qwen3-next-80b-a3b-q4", 1),
+    "qwen3.6-35b-a3b-q8-b1": ("qwen3.6-35b-a3b-q8", 1),
+    "qwen3.6-35b-a3b-q8-b4": ("qwen3.6-35b-a3b-q8", 4),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=960)
+    ap.add_argument("--warmup", type=int, default=96)
+    ap.add_argument("--config", default="qwen3.6-35b-a3b-q4-b1", choices=sorted(CONFIGS))
+    ap.add_argument("--replicas", type=int, default=48, help="distinct layers cycled through (MALL defeat)")
+    ap.add_argument("--seed", type=int, default=20261201)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+              "The MoE decode step would shard by experts across GPUs with one all-reduce of the "
+              "[batch, hidden] output; see DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from swiftlet_amd import _lib, moe, synth
+    from swiftlet_amd._lib import check
+
+    if not _lib.LIB_PATH.exists():
+        from swiftlet_amd import build
+        build.build()
+    lib = _lib.load()
+
+    shape_key, batch = CONFIGS[args.config]
+    shape = synth.SHAPES[shape_key]
+    R = args.replicas
+    dev = "cuda"
+    torch.cuda.init()
+    stream = torch.cuda.current_stream()
+    sh = ctypes.c_void_p(stream.cuda_stream)
+
+    # ---- resident weights: R distinct layers, all experts --------------
+    layers = [moe.synth_layer(shape, args.seed, r, dev) for r in range(R)]
+    xs_bits = synth.activations_bf16(args.seed + 7, R * batch, shape.hidden).reshape(R, batch, shape.hidden)
+    xs = torch.from_numpy(xs_bits.view(np.int16)).view(torch.bfloat16).to(dev)
+    wss = [l.new_workspace(batch) for l in layers]
+    outs = torch.empty((R, batch, shape.hidden), dtype=torch.bfloat16, device=dev)
+    ids = torch.empty((R, batch, shape.top_k), dtype=torch.int32, device=dev)
+    wts = torch.empty((R, batch, shape.top_k), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    # prebuilt ctypes argument tuples, one per replica
+    calls = []
+    for r, l in enumerate(layers):
+        calls.append((ctypes.byref(l._c), ctypes.c_void_p(xs[r].data_ptr()), _lib.SWQ_BF16, batch,
+                      ctypes.c_void_p(outs[r].data_ptr()), _lib.SWQ_BF16, ctypes.c_void_p(ids[r].data_ptr()),
+                      ctypes.c_void_p(wts[r].data_ptr()), ctypes.c_void_p(wss[r].data_ptr()), wss[r].numel(), 0))
+
+    def step(i, mask=7):
+        c = calls[i % R]
+        check(lib.swq_moe_decode_stages(*c, mask, sh), "moe_decode")
+
+    # ---- graph of K steps -----------------------------------------------
+    K, W = args.steps, args.warmup
+    for i in range(min(W, R)):
+        step(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for i in range(K):
+            c = calls[i % R]
+            check(lib.swq_moe_decode_stages(*c, 7, cap), "moe_decode (capture)")
+    torch.cuda.synchronize()
+    for _ in range(max(1, (W + K - 1) // K)):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    graph_ms = e0.elapsed_time(e1)
+    us_per_step = graph_ms * 1000.0 / K
+
+    # ---- eager pass with per-stage HIP events (queued behind a stall) ----
+    n_ev = min(K, 4 * R)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n_ev)]
+    check(lib.swq_bench_stall(20000, sh), "stall")  # tens of ms of queue backlog
+    t_eager0 = torch.cuda.Event(enable_timing=True)
+    t_eager1 = torch.cuda.Event(enable_timing=True)
+    t_eager0.record()
+    for i in range(n_ev):
+        ev = evs[i]
+        ev[0].record()
+        step(i, 1)
+        ev[1].record()
+        step(i, 2)
+        ev[2].record()
+        step(i, 4)
+        ev[3].record()
+    t_eager1.record()
+    torch.cuda.synchronize()
+    stage_us = [float(np.mean([evs[i][s].elapsed_time(evs[i][s + 1]) for i in range(n_ev)])) * 1000.0
+                for s in range(3)]
+    eager_us_per_step = t_eager0.elapsed_time(t_eager1) * 1000.0 / n_ev
+    # unique experts per step (batch > 1 reads each distinct expert once)
+    ids_h = ids.cpu().numpy()
+    uniq = [len(np.unique(ids_h[r])) for r in range(R)]
+    mean_uniq = float(np.mean(uniq))
+
+    H, I, Is, E = shape.hidden, shape.inter, shape.shared_inter, shape.experts
+    mb = shape.matrix_bytes
+    eb, rb = shape.expert_bits, shape.router_bits
+    xb = batch * H * 2
+    stage_bytes = [
+        mb(E, H, rb) + mb(1, H, rb) + 2 * mb(Is, H, eb) + xb,    # router + shared gate + shared gate/up
+        mean_uniq * 2 * mb(I, H, eb) + xb,                       # routed gate/up
+        mean_uniq * mb(H, I, eb) + mb(H, Is, eb) + xb,           # routed + shared down, bf16 out
+    ]
+    step_bytes = shape.decode_bytes(mean_uniq, batch)
+    dom = int(np.argmax(stage_us))
+    achieved = stage_bytes[dom] / (stage_us[dom] * 1e-6) / 1e9
+
+    result = {
+        "metric": "us per MoE-layer decode step; achieved HBM GB/s as fraction of peak (1 GPU)",
+        "value": round(us_per_step, 3),
+        "unit": "us/layer-step",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(us_per_step / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4-affine x bf16, fp32 accumulate" if eb == 4 else "q8-affine x bf16, fp32 accumulate",
+        "data": f"synthetic seeded weights (seed {args.seed}), {R} distinct resident layers cycled, bf16 x ~N(0,1)",
+        "config": {"workload": args.config, "hidden": H, "experts": E, "top_k": shape.top_k,
+                   "moe_intermediate": I, "shared_intermediate": Is, "expert_bits": eb,
+                   "router_bits": rb, "group": shape.group, "batch": batch, "replicas": R,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": ["moe_stage1", "moe_stage2", "moe_stage3"][dom],
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": int(stage_bytes[dom]),
+                     "avg_launch_us": round(stage_us[dom], 3)},
+        "stage_us": [round(v, 3) for v in stage_us],
+        "stage_bytes": [int(v) for v in stage_bytes],
+        "step_bytes": int(step_bytes),
+        "step_gbs_wall": round(step_bytes / (us_per_step * 1e-6) / 1e9, 1),
+        "step_gbs_kernels": round(step_bytes / (sum(stage_us) * 1e-6) / 1e9, 1),
+        "eager_us_per_step": round(eager_us_per_step, 3),
+        "unique_experts_per_step": mean_uniq,
+    }
+
+    # ---- CPU baseline: the C restatement of the reference CPU path -------
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args, shape, batch, layers[0], xs_bits[0])
+
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(args, shape, batch, layer0, x0_bits):
+    """oracle/liboracle.so (QwenCPUModel.moeForward restated in C) on layer 0
+    of the same workload, fresh x per step, bounded by --cpu-seconds."""
+    from oracle import cref
+    from swiftlet_amd import moe, synth
+
+    if not cref.LIB.exists():
+        import subprocess
+        subprocess.run(["make", "-C", os.path.join(ROOT, "oracle")], check=True, capture_output=True)
+    arrays = moe.host_layer_arrays(shape, args.seed, 0)
+    c = cref.CMoE(arrays, shape.hidden, shape.experts, shape.top_k, shape.inter, shape.shared_inter,
+                  shape.group, shape.norm_topk_prob)
+    xs = synth.bf16_to_f32(synth.activations_bf16(args.seed + 99, 64 * batch, shape.hidden))
+    res = {}
+    for threads in (1, cref.max_threads()):
+        n, t0 = 0, time.perf_counter()
+        times = []
+        while n < 64 and time.perf_counter() - t0 < args.cpu_seconds / 2:
+            t = time.perf_counter()
+            c.forward(xs[n * batch:(n + 1) * batch], threads)
+            times.append(time.perf_counter() - t)
+            n += 1
+        res[threads] = (float(np.median(times)) * 1e6, n)
+    one_us, one_n = res[1]
+    mt = max(res)
+    return {"value": round(one_us, 1), "unit": "us/layer-step", "cores": 1, "kind": "port",
+            "sample": f"{one_n} decode steps of layer 0 (batch {batch}), median; C restatement of "
+                      f"QwenCPUModel.moeForward, experts dequantised per call",
+            "multithread": {"value": round(res[mt][0], 1), "cores": mt, "steps": res[mt][1]},
+            "cpu": cpu_model(), "nproc": os.cpu_count()}
+
+
+if __name__ == "__main__":
+    main()

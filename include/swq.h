@@ -1,0 +1,186 @@
+/*
+ * swq.h — C ABI of the MI355X (gfx950) MoE decode hot path.
+ *
+ * This is the drop-in boundary for SwiftletCore's quantized-matmul and MoE
+ * layer operator API.  Swift (or any FFI) binds these symbols through a
+ * module.modulemap; Python binds them with ctypes.  Every signature uses
+ * plain pointers and sizes only.
+ *
+ * Conventions
+ *   - Every entry point returns SWQ_OK (0) or a negative SWQ_ERR_* code;
+ *     no C++ exception and no HIP error escapes.  swq_strerror() names it.
+ *   - "device pointer" = memory from hipMalloc (or any HBM allocation) on the
+ *     current HIP device.  Weights are never copied: a swq_qlinear is a
+ *     non-owning view, like GPULinear (MetalShardStore.swift:48-62).
+ *   - `stream` is a hipStream_t passed as void*; NULL means the null stream.
+ *     Stream-ordered entry points return after enqueueing.
+ *   - The hot entry points (swq_encode_gemv, swq_moe_decode,
+ *     swq_moe_prefill) allocate nothing; scratch comes from a caller-owned
+ *     workspace sized by the matching *_workspace_bytes query.
+ *   - A workspace belongs to one stream at a time: two calls that overlap in
+ *     time must use different workspaces.
+ *   - MLX affine format (Checkpoint.swift:168-209): a weight row is
+ *     in_dim*bits/32 uint32 words, codes packed LSB-first; one scale and one
+ *     bias per group_size consecutive inputs; w = scale*q + bias.
+ */
+#ifndef SWQ_H
+#define SWQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+enum {
+    SWQ_OK = 0,
+    SWQ_ERR_INVALID_ARGUMENT = -1,  /* null pointer, non-positive size        */
+    SWQ_ERR_BAD_SHAPE = -2,         /* in_dim % group_size, group % per-word  */
+    SWQ_ERR_UNSUPPORTED_BITS = -3,  /* Checkpoint.Error.unsupportedBits       */
+    SWQ_ERR_UNSUPPORTED_DTYPE = -4, /* scale / activation dtype not 0,1,2     */
+    SWQ_ERR_MISALIGNED = -5,        /* fused path needs 16 B rows, 2/4 B s/b  */
+    SWQ_ERR_WORKSPACE = -6,         /* workspace null or smaller than query   */
+    SWQ_ERR_EXPERT_RANGE = -7,      /* top_k outside [1, num_experts]         */
+    SWQ_ERR_HIP = -8,               /* a HIP runtime call failed              */
+    SWQ_ERR_NO_DEVICE = -9,         /* MetalEngine.Error.noDevice             */
+    SWQ_ERR_LIMIT = -10             /* batch / top_k above compiled maximum   */
+};
+
+/* Scale, bias and activation dtypes.  The values equal
+ * MetalEngine.ScalesType (MetalEngine.swift:69-80): 0 f32, 1 f16, 2 bf16. */
+enum { SWQ_F32 = 0, SWQ_F16 = 1, SWQ_BF16 = 2 };
+
+/* Compiled limits of the fused MoE kernels. */
+enum { SWQ_MAX_BATCH = 16, SWQ_MAX_TOPK = 16 };
+
+/* swq_moe_decode / swq_moe_prefill flags. */
+enum {
+    /* out += moe(x) instead of out = moe(x): the residual add that
+     * weighted_accum fuses (Kernels.metal.txt:463-478).  Needs out_dtype f32. */
+    SWQ_MOE_ACCUMULATE = 1
+};
+
+/* One quantized linear module, optionally a stack of experts.
+ * Replaces GPULinear (MetalShardStore.swift:48-62) plus ExpertStack's
+ * per-expert strides (QwenMetalModel.swift:16-21). */
+typedef struct swq_qlinear {
+    const void *w;           /* packed uint32 codes (device)                  */
+    const void *scales;      /* one per group (device)                        */
+    const void *biases;      /* one per group (device)                        */
+    int64_t w_off;           /* byte offsets added to w / scales / biases     */
+    int64_t s_off;
+    int64_t b_off;
+    int32_t out_dim;         /* rows of one matrix (of one expert if stacked) */
+    int32_t in_dim;          /* logical input dimension                       */
+    int32_t group_size;
+    int32_t bits;            /* 2, 4 or 8                                     */
+    int32_t scales_type;     /* SWQ_F32 / SWQ_F16 / SWQ_BF16                  */
+    int32_t reserved;        /* must be 0                                     */
+    int64_t expert_stride_w;  /* bytes between experts' codes (0: unstacked)  */
+    int64_t expert_stride_sb; /* bytes between experts' scales and biases     */
+} swq_qlinear;
+
+/* One routed-expert SwiGLU MoE layer with a sigmoid-gated shared expert.
+ * Replaces MoEGPU (QwenMetalModel.swift:34-39) + the config fields that
+ * moeForward reads (QwenCPUModel.swift:500-504). */
+typedef struct swq_moe_layer {
+    swq_qlinear router;            /* mlp.gate            [E, H]              */
+    swq_qlinear gate;              /* switch_mlp.gate_proj [E][I, H] stacked  */
+    swq_qlinear up;                /* switch_mlp.up_proj   [E][I, H] stacked  */
+    swq_qlinear down;              /* switch_mlp.down_proj [E][H, I] stacked  */
+    swq_qlinear shared_gate;       /* shared_expert.gate_proj [Is, H]         */
+    swq_qlinear shared_up;         /* shared_expert.up_proj   [Is, H]         */
+    swq_qlinear shared_down;       /* shared_expert.down_proj [H, Is]         */
+    swq_qlinear shared_expert_gate;/* mlp.shared_expert_gate [1, H]           */
+    int32_t hidden;                /* H                                        */
+    int32_t num_experts;           /* E                                        */
+    int32_t top_k;                 /* K                                        */
+    int32_t moe_intermediate;      /* I                                        */
+    int32_t shared_intermediate;   /* Is                                       */
+    int32_t norm_topk_prob;        /* 1: w_k = p_k / sum_topk p (:546-550)     */
+    int32_t has_shared;            /* 0: no shared expert / shared gate        */
+    int32_t reserved;              /* must be 0                                */
+} swq_moe_layer;
+
+/* ---- library ----------------------------------------------------------- */
+
+/* Human-readable name of a status code (never NULL). */
+const char *swq_strerror(int status);
+
+/* ABI version: major*10000 + minor*100 + patch. */
+int swq_version(void);
+
+/* Number of visible HIP devices; SWQ_ERR_NO_DEVICE if none.
+ * Mirrors the MetalEngine() constructor's device check (MetalEngine.swift:22-27). */
+int swq_device_count(int *count);
+
+/* ---- quantized GEMV ---------------------------------------------------- */
+
+/* Blocking, host-memory GEMV: y = W x.  Copies every input to the device and
+ * y back, as MetalEngine.gemvQuantized does (MetalEngine.swift:190-232).
+ * use_fast selects the vectorised kernel (bits 4/8) instead of the scalar
+ * one; both compute the same sum.  Allocates; not for the hot loop. */
+int swq_gemv_quantized(const float *x,
+                       const void *packed, size_t packed_bytes,
+                       const void *scales, size_t scales_bytes,
+                       const void *biases, size_t biases_bytes,
+                       int out_dim, int in_dim, int group_size, int bits,
+                       int scales_type, int use_fast, float *y);
+
+/* Stream-ordered GEMV over a device-resident linear: y[y_off + r] =
+ * sum_i W[r, i] x[x_off + i] for r < rows (rows <= 0: lin->out_dim).
+ * w_extra / s_extra / b_extra advance into a stacked tensor in bytes.
+ * Replaces MetalEngine.encodeGemv (MetalEngine.swift:95-170): picks the
+ * vectorised kernel when rows are 16 B aligned, else the scalar one. */
+int swq_encode_gemv(const swq_qlinear *lin, int rows,
+                    int64_t w_extra, int64_t s_extra, int64_t b_extra,
+                    const float *x, int64_t x_off, float *y, int64_t y_off,
+                    void *stream);
+
+/* buf[dst_off + i] = silu(buf[g_off + i]) * buf[u_off + i], i < count.
+ * Replaces MetalEngine.encodeSiluMul (MetalEngine.swift:172-187). */
+int swq_encode_silu_mul(float *buf, int count, int64_t g_off, int64_t u_off,
+                        int64_t dst_off, void *stream);
+
+/* Materialise rows [row0, row0+rows) of the flattened [.., out, in] weight
+ * as fp32: out[r*in + i] = scale*q + bias (multiply, then add; no FMA).
+ * Replaces Checkpoint.moduleWeightSlice / dequantized (Checkpoint.swift:148-209).
+ * Stacked linears: row r of expert e is flattened row e*out_dim + r. */
+int swq_dequantize(const swq_qlinear *lin, int64_t row0, int64_t rows,
+                   float *out, void *stream);
+
+/* ---- MoE layer decode ------------------------------------------------- */
+
+/* Workspace bytes swq_moe_decode needs for `batch` tokens (0 on bad input). */
+size_t swq_moe_decode_workspace_bytes(const swq_moe_layer *layer, int batch);
+
+/* Prepare a fresh workspace (zeroes its completion counters).  Call once
+ * after allocating it; swq_moe_decode leaves it ready for the next call. */
+int swq_moe_workspace_init(void *ws, size_t ws_bytes, void *stream);
+
+/* One MoE-layer decode step for `batch` independent tokens, entirely on the
+ * device, three kernel launches:
+ *   1. router GEMV + shared-gate GEMV + shared gate/up SwiGLU, then (last
+ *      workgroup) softmax, top-k (ties -> lower expert id), renormalisation;
+ *   2. gate/up SwiGLU of every distinct selected expert, indexed by the
+ *      device-resident top-k ids;
+ *   3. down projections + weighted combine + sigmoid-gated shared expert.
+ * x: [batch, hidden] of x_dtype (SWQ_F32 / SWQ_BF16).  out: [batch, hidden]
+ * of out_dtype (SWQ_F32 / SWQ_BF16).  topk_ids [batch, top_k] int32 and
+ * topk_weights [batch, top_k] f32 receive the routing (either may be NULL).
+ * Replaces QwenMetalModel.moeForward / routerPicks / encodePendingMoE
+ * (QwenMetalModel.swift:609-716, 798-892) with the numerics of
+ * QwenCPUModel.moeForward (QwenCPUModel.swift:500-569). */
+int swq_moe_decode(const swq_moe_layer *layer,
+                   const void *x, int x_dtype, int batch,
+                   void *out, int out_dtype,
+                   int32_t *topk_ids, float *topk_weights,
+                   void *ws, size_t ws_bytes, int flags, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SWQ_H */

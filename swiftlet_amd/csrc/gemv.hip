@@ -1,0 +1,235 @@
+// Quantized GEMV, SwiGLU and dequantisation entry points: the operator
+// layer of MetalEngine (MetalEngine.swift:95-232) and Checkpoint's MLX
+// affine dequantisation (Checkpoint.swift:168-209), on gfx950.
+#include <vector>
+
+#include "internal.hpp"
+#include "tile.hpp"
+
+namespace swq {
+
+constexpr int kGemvThreads = 256;
+constexpr int kGemvRI = 4;
+
+// Vectorised GEMV: 16-byte code chunks, kGemvRI passes of rows per wave.
+template <int BITS, int CPL>
+__global__ __launch_bounds__(kGemvThreads) void gemv_vec_kernel(QMat m, int rows, const float *x, float *y) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const LaneMap lm = lane_map(m.lpr_log2, lane);
+    const int row0 = (blockIdx.x * (kGemvThreads / kWave) + wave) * kGemvRI * lm.rpw;
+    if (row0 >= rows) return;
+    RowTile<BITS, CPL, kGemvRI> rt;
+    load_tile(rt, m, 0, lm, row0, rows);
+    XSlice<BITS, CPL> xs;
+    load_xslice<0>(xs, m, lm, x, 0);
+    float res[kGemvRI];
+    dot_tile(res, rt, xs, lm);
+    if (lm.j == 0) {
+#pragma unroll
+        for (int i = 0; i < kGemvRI; ++i) {
+            const int row = row0 + i * lm.rpw + lm.q;
+            if (row < rows) y[row] = res[i];
+        }
+    }
+}
+
+// Scalar-form GEMV for any alignment and bits in {2, 4, 8}: one wave per
+// row, lanes striding over groups, the factored per-group sum of
+// Kernels.metal.txt:56-75 with byte-addressed loads (:27-37).
+__global__ __launch_bounds__(kGemvThreads) void gemv_scalar_kernel(const uint8_t *w, const uint8_t *s,
+                                                                   const uint8_t *b, int rows, int in,
+                                                                   int group, int bits, int stype,
+                                                                   const float *x, float *y) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kGemvThreads / kWave) + wave;
+    if (row >= rows) return;
+    const int per_word = 32 / bits;
+    const uint32_t mask = (1u << bits) - 1u;
+    const int groups = in / group;
+    const int words_per_group = group / per_word;
+    const int64_t row_bytes = static_cast<int64_t>(in) * bits / 8;
+    const uint8_t *wr = w + static_cast<int64_t>(row) * row_bytes;
+    float acc = 0.f;
+    for (int g = lane; g < groups; g += kWave) {
+        float qdot = 0.f, xsum = 0.f;
+        for (int wi = 0; wi < words_per_group; ++wi) {
+            uint32_t word = load_u32_bytes(wr + static_cast<int64_t>(g * words_per_group + wi) * 4);
+            const float *xx = x + g * group + wi * per_word;
+            for (int j = 0; j < per_word; ++j) {
+                const float xv = xx[j];
+                qdot = fmaf(static_cast<float>(word & mask), xv, qdot);
+                xsum += xv;
+                word >>= bits;
+            }
+        }
+        const int64_t gi = static_cast<int64_t>(row) * groups + g;
+        acc += load_scale_bytes(s, gi, stype) * qdot + load_scale_bytes(b, gi, stype) * xsum;
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+}
+
+// silu_mul of Kernels.metal.txt:114-124: h = g / (1 + exp(-g)) * u.
+__global__ void silu_mul_kernel(float *buf, int count, int64_t g_off, int64_t u_off, int64_t dst_off) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    const float g = buf[g_off + i];
+    buf[dst_off + i] = (g / (1.0f + __expf(-g))) * buf[u_off + i];
+}
+
+// One thread per packed word of rows [row0, row0 + rows) of the flattened
+// [experts * out_dim, in] weight; row r of expert e sits at
+// e*stride_w + r*row_bytes.  w = scale * q then + bias, rounded separately
+// (the two-rounding f32 form of Checkpoint.swift:202).
+__global__ void dequant_kernel(const uint8_t *w, const uint8_t *s, const uint8_t *b, int64_t stride_w,
+                               int64_t stride_sb, int out_dim, int64_t row0, int64_t rows, int in, int group,
+                               int bits, int stype, float *out) {
+    const int per_word = 32 / bits;
+    const int64_t wpr = in / per_word;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= rows * wpr) return;
+    const int64_t r = idx / wpr;
+    const int wi = static_cast<int>(idx - r * wpr);
+    const int64_t flat = row0 + r;
+    const int64_t e = flat / out_dim;
+    const int64_t rr = flat - e * out_dim;
+    const int64_t row_bytes = static_cast<int64_t>(in) * bits / 8;
+    const int gpr = in / group;
+    uint32_t word = load_u32_bytes(w + e * stride_w + rr * row_bytes + static_cast<int64_t>(wi) * 4);
+    const uint8_t *sb = s + e * stride_sb;
+    const uint8_t *bb = b + e * stride_sb;
+    const uint32_t mask = (1u << bits) - 1u;
+    for (int j = 0; j < per_word; ++j) {
+        const int col = wi * per_word + j;
+        const int64_t gi = rr * gpr + col / group;
+        const float sc = load_scale_bytes(sb, gi, stype);
+        const float bi = load_scale_bytes(bb, gi, stype);
+        out[r * in + col] = __fadd_rn(__fmul_rn(sc, static_cast<float>(word & mask)), bi);
+        word >>= bits;
+    }
+}
+
+static int launch_gemv(const swq_qlinear *l, int rows, int64_t w_extra, int64_t s_extra, int64_t b_extra,
+                       const float *x, float *y, bool allow_vec, hipStream_t stream) {
+    const bool x_aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    if (allow_vec && x_aligned && vector_path_ok(l, w_extra, s_extra, b_extra)) {
+        QMat m = make_qmat(l, w_extra, s_extra, b_extra);
+        if (m.cpl <= (m.bits == 4 ? 2 : 4)) {
+            const int rows_per_block = (kGemvThreads / kWave) * kGemvRI * (kWave >> m.lpr_log2);
+            const dim3 grid((rows + rows_per_block - 1) / rows_per_block);
+            if (m.bits == 4) {
+                if (m.cpl == 1) hipLaunchKernelGGL((gemv_vec_kernel<4, 1>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y);
+                else hipLaunchKernelGGL((gemv_vec_kernel<4, 2>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y);
+            } else {
+                if (m.cpl == 1) hipLaunchKernelGGL((gemv_vec_kernel<8, 1>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y);
+                else if (m.cpl == 2) hipLaunchKernelGGL((gemv_vec_kernel<8, 2>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y);
+                else hipLaunchKernelGGL((gemv_vec_kernel<8, 4>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y);
+            }
+            return launch_status();
+        }
+    }
+    const uint8_t *w = static_cast<const uint8_t *>(l->w) + l->w_off + w_extra;
+    const uint8_t *s = static_cast<const uint8_t *>(l->scales) + l->s_off + s_extra;
+    const uint8_t *b = static_cast<const uint8_t *>(l->biases) + l->b_off + b_extra;
+    const dim3 grid((rows + kGemvThreads / kWave - 1) / (kGemvThreads / kWave));
+    hipLaunchKernelGGL(gemv_scalar_kernel, grid, dim3(kGemvThreads), 0, stream, w, s, b, rows, l->in_dim,
+                       l->group_size, l->bits, l->scales_type, x, y);
+    return launch_status();
+}
+
+}  // namespace swq
+
+using namespace swq;
+
+extern "C" int swq_encode_gemv(const swq_qlinear *lin, int rows, int64_t w_extra, int64_t s_extra,
+                               int64_t b_extra, const float *x, int64_t x_off, float *y, int64_t y_off,
+                               void *stream) {
+    int st = check_linear_shape(lin);
+    if (st != SWQ_OK) return st;
+    if (!x || !y || x_off < 0 || y_off < 0 || w_extra < 0 || s_extra < 0 || b_extra < 0) return SWQ_ERR_INVALID_ARGUMENT;
+    const int n = rows > 0 ? rows : lin->out_dim;
+    return launch_gemv(lin, n, w_extra, s_extra, b_extra, x + x_off, y + y_off, true,
+                       static_cast<hipStream_t>(stream));
+}
+
+extern "C" int swq_encode_silu_mul(float *buf, int count, int64_t g_off, int64_t u_off, int64_t dst_off,
+                                   void *stream) {
+    if (!buf || count <= 0 || g_off < 0 || u_off < 0 || dst_off < 0) return SWQ_ERR_INVALID_ARGUMENT;
+    const int tb = 256;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((count + tb - 1) / tb), dim3(tb), 0,
+                       static_cast<hipStream_t>(stream), buf, count, g_off, u_off, dst_off);
+    return launch_status();
+}
+
+extern "C" int swq_dequantize(const swq_qlinear *lin, int64_t row0, int64_t rows, float *out, void *stream) {
+    int st = check_linear_shape(lin);
+    if (st != SWQ_OK) return st;
+    if (!out || row0 < 0 || rows <= 0) return SWQ_ERR_INVALID_ARGUMENT;
+    // an unstacked matrix has out_dim rows; a stack's extent is the caller's
+    if (lin->expert_stride_w == 0 && row0 + rows > lin->out_dim) return SWQ_ERR_BAD_SHAPE;
+    const int per_word = 32 / lin->bits;
+    const int64_t words = rows * (lin->in_dim / per_word);
+    const int tb = 256;
+    const int64_t blocks = (words + tb - 1) / tb;
+    if (blocks > 0x7FFFFFFF) return SWQ_ERR_LIMIT;
+    hipLaunchKernelGGL(dequant_kernel, dim3(static_cast<unsigned>(blocks)), dim3(tb), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint8_t *>(lin->w) + lin->w_off,
+                       static_cast<const uint8_t *>(lin->scales) + lin->s_off,
+                       static_cast<const uint8_t *>(lin->biases) + lin->b_off, lin->expert_stride_w,
+                       lin->expert_stride_sb, lin->out_dim, row0, rows, lin->in_dim, lin->group_size, lin->bits,
+                       lin->scales_type, out);
+    return launch_status();
+}
+
+extern "C" int swq_gemv_quantized(const float *x, const void *packed, size_t packed_bytes, const void *scales,
+                                  size_t scales_bytes, const void *biases, size_t biases_bytes, int out_dim,
+                                  int in_dim, int group_size, int bits, int scales_type, int use_fast, float *y) {
+    if (!x || !packed || !scales || !biases || !y) return SWQ_ERR_INVALID_ARGUMENT;
+    swq_qlinear l{};
+    l.out_dim = out_dim;
+    l.in_dim = in_dim;
+    l.group_size = group_size;
+    l.bits = bits;
+    l.scales_type = scales_type;
+    l.w = packed;
+    l.scales = scales;
+    l.biases = biases;
+    int st = check_linear_shape(&l);
+    if (st != SWQ_OK) return st;
+    const size_t need_w = static_cast<size_t>(out_dim) * in_dim * bits / 8;
+    const size_t need_s = static_cast<size_t>(out_dim) * (in_dim / group_size) * scale_bytes(scales_type);
+    if (packed_bytes < need_w || scales_bytes < need_s || biases_bytes < need_s) return SWQ_ERR_BAD_SHAPE;
+
+    void *dx = nullptr, *dw = nullptr, *ds = nullptr, *db = nullptr, *dy = nullptr;
+    auto release = [&]() {
+        hipFree(dx);
+        hipFree(dw);
+        hipFree(ds);
+        hipFree(db);
+        hipFree(dy);
+    };
+    if (hipMalloc(&dx, static_cast<size_t>(in_dim) * 4) != hipSuccess ||
+        hipMalloc(&dw, need_w) != hipSuccess || hipMalloc(&ds, need_s) != hipSuccess ||
+        hipMalloc(&db, need_s) != hipSuccess || hipMalloc(&dy, static_cast<size_t>(out_dim) * 4) != hipSuccess) {
+        release();
+        return SWQ_ERR_HIP;
+    }
+    st = SWQ_OK;
+    if (hipMemcpy(dx, x, static_cast<size_t>(in_dim) * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(dw, packed, need_w, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(ds, scales, need_s, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(db, biases, need_s, hipMemcpyHostToDevice) != hipSuccess)
+        st = SWQ_ERR_HIP;
+    if (st == SWQ_OK) {
+        l.w = dw;
+        l.scales = ds;
+        l.biases = db;
+        st = launch_gemv(&l, out_dim, 0, 0, 0, static_cast<const float *>(dx), static_cast<float *>(dy),
+                         use_fast != 0, nullptr);
+    }
+    if (st == SWQ_OK && hipDeviceSynchronize() != hipSuccess) st = SWQ_ERR_HIP;
+    if (st == SWQ_OK && hipMemcpy(y, dy, static_cast<size_t>(out_dim) * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        st = SWQ_ERR_HIP;
+    release();
+    return st;
+}

@@ -1,0 +1,112 @@
+"""MoE-layer decode on the device against the oracle (QwenCPUModel.moeForward,
+QwenCPUModel.swift:500-569), at the benchmark shapes and at odd ones.
+
+Bar: expert ids equal the oracle's wherever the router's k-th/(k+1)-th
+logit gap exceeds 1e-3 (f32 summation-order noise of the router GEMV is
+~1e-6 here); combine weights within 1e-5; layer output within 1e-3
+relative L2 of the f32 oracle (the observed error is ~1e-6)."""
+
+import numpy as np
+import pytest
+
+from oracle import moe_ref as R
+from swiftlet_amd import moe, synth
+from tests import helpers
+
+pytestmark = pytest.mark.gpu
+
+REL_L2_BAR = 1e-3
+MARGIN = 1e-3
+
+
+def _run(shape, batch, x_dtype="bf16", out_dtype="f32", seed=helpers.SEED, layer=0, gpu=None):
+    import torch
+    gpu = gpu or moe.synth_layer(shape, seed, layer)
+    xb = synth.activations_bf16(seed + 1000 * layer + batch, batch, shape.hidden)
+    xf = synth.bf16_to_f32(xb)
+    if x_dtype == "bf16":
+        x = helpers.bf16_bits_to_torch(xb)
+    else:
+        x = torch.from_numpy(xf).cuda()
+    odt = torch.float32 if out_dtype == "f32" else torch.bfloat16
+    out, ids, w = gpu.decode(x, out_dtype=odt)
+    torch.cuda.synchronize()
+    return gpu, xf, out, ids.cpu().numpy(), w.cpu().numpy()
+
+
+def _check_against_oracle(shape, xf, out, ids, w, seed=helpers.SEED, layer=0):
+    import torch
+    ref_layer = helpers.ref_layer(shape, seed, layer)
+    ref_out, picks, ref_w = R.moe_forward(xf, ref_layer)
+    margin = R.router_margin(xf, ref_layer)
+    for b in range(xf.shape[0]):
+        ref_ids = [e for e, _ in picks[b]]
+        if margin[b] > MARGIN:
+            assert list(ids[b]) == ref_ids, (b, ids[b], ref_ids)
+            assert np.allclose(w[b], ref_w[b], rtol=1e-5, atol=1e-7)
+    if out.dtype == torch.bfloat16:
+        got = R.bf16_bits_to_f32(helpers.torch_bf16_to_bits(out))
+        ref_b = R.bf16_bits_to_f32(R.f32_to_bf16_bits_rne(ref_out))
+        assert R.rel_l2(got, ref_b) < REL_L2_BAR
+        # bf16 of an f32 output within ~1e-6 of the oracle: at most one ulp apart
+        ulp = np.abs(helpers.torch_bf16_to_bits(out).astype(np.int32)
+                     - R.f32_to_bf16_bits_rne(ref_out).astype(np.int32))
+        assert ulp.max() <= 1
+    else:
+        got = out.cpu().numpy()
+        err = R.rel_l2(got, ref_out)
+        assert err < REL_L2_BAR, err
+        assert err < 1e-5, err  # fp32 accumulation throughout: far inside the bar
+    return ref_out
+
+
+@pytest.mark.parametrize("name,batch", [
+    ("qwen3.6-35b-a3b-q4", 1),
+    ("qwen3-next-80b-a3b-q4", 1),
+    ("qwen3.6-35b-a3b-q8", 1),
+    ("qwen3.6-35b-a3b-q8", 4),
+    ("qwen3.6-35b-a3b-q4", 3),
+])
+def test_moe_decode_matches_oracle(name, batch):
+    shape = synth.SHAPES[name]
+    gpu, xf, out, ids, w = _run(shape, batch)
+    _check_against_oracle(shape, xf, out, ids, w)
+
+
+def test_moe_decode_bf16_out_and_f32_x():
+    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    gpu, xf, out, ids, w = _run(shape, 2, x_dtype="f32", out_dtype="bf16")
+    _check_against_oracle(shape, xf, out, ids, w)
+
+
+def test_moe_decode_deterministic_and_accumulate():
+    import torch
+    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    xb = synth.activations_bf16(5, 1, shape.hidden)
+    x = helpers.bf16_bits_to_torch(xb)
+    ws = gpu.new_workspace(1)
+    o1, i1, w1 = gpu.decode(x, ws=ws)
+    o1, i1, w1 = o1.clone(), i1.clone(), w1.clone()
+    o2, i2, w2 = gpu.decode(x, ws=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(i1, i2) and torch.equal(w1, w2)
+    resid = torch.randn_like(o1)
+    acc = resid.clone()
+    gpu.decode(x, out=acc, ws=ws, accumulate=True)
+    torch.cuda.synchronize()
+    assert torch.allclose(acc, resid + o1, rtol=0, atol=1e-5)
+
+
+@pytest.mark.parametrize("E,K,I,Is,H,bits,norm", [
+    (8, 2, 32, 32, 64, 4, True),      # the tiny model's MoE shape
+    (60, 4, 64, 96, 256, 8, False),   # E not a multiple of 64, norm_topk_prob false
+    (128, 1, 128, 64, 512, 4, True),  # top-1
+    (1024, 16, 64, 64, 128, 4, True), # widest top-k table
+])
+def test_moe_decode_odd_shapes(E, K, I, Is, H, bits, norm):
+    shape = synth.MoEShape("odd", H, E, K, I, Is, expert_bits=bits, router_bits=8,
+                           group=64 if H % 64 == 0 and I % 64 == 0 else 32, norm_topk_prob=norm)
+    for batch in (1, 5):
+        gpu, xf, out, ids, w = _run(shape, batch, seed=77)
+        _check_against_oracle(shape, xf, out, ids, w, seed=77)
