@@ -1,0 +1,261 @@
+"""Whole-model f32 forward of the tiny qwen3_next fixtures — TEST
+INFRASTRUCTURE ONLY.
+
+The reference's only vectors that exercise the MoE math (router softmax,
+top-k, renormalisation, SwiGLU experts, shared expert gate) and the MLX
+affine dequantisation together are mlx's captures of a tiny whole model
+(fixtures/tiny_forward*.safetensors).  Reaching the MoE block requires the
+rest of each decoder layer, so this module restates QwenCPUModel's
+non-MoE ops for that model (qwen3_next, fused-interleaved DeltaNet layout)
+and delegates the MoE block to oracle.moe_ref.moe_forward:
+
+  Checkpoint quant spec / dequant  Checkpoint.swift:31-49, 126-133, 168-209
+  rms_norm                         QwenCPUModel.swift:47-59
+  layer_forward                    QwenCPUModel.swift:259-281
+  attention_forward                QwenCPUModel.swift:285-345
+  apply_rope                       QwenCPUModel.swift:348-367
+  deltanet_forward                 QwenCPUModel.swift:371-496
+  forward / greedy                 QwenCPUModel.swift:208-236
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+from safetensors.numpy import load_file
+
+from . import moe_ref as R
+
+f32 = np.float32
+
+
+class TinyCheckpoint:
+    """Checkpoint(dir:) for a single-file mlx checkpoint."""
+
+    def __init__(self, directory: Path):
+        directory = Path(directory)
+        self.cfg = json.loads((directory / "config.json").read_text())
+        self.t = load_file(str(directory / "model.safetensors"))
+        q = self.cfg.get("quantization") or {}
+        self.default = (q["group_size"], q["bits"]) if "group_size" in q and "bits" in q else None
+        self.overrides = {k: (v["group_size"], v["bits"]) for k, v in q.items()
+                          if isinstance(v, dict) and "group_size" in v and "bits" in v}
+
+    def is_quantized(self, path: str) -> bool:
+        return path + ".scales" in self.t
+
+    def spec(self, path: str):
+        for key, s in self.overrides.items():
+            if path.endswith(key) or key.endswith(path):
+                return s
+        return self.default
+
+    def quantized(self, path: str):
+        """(words, scales, biases, bits, group) of a quantized module."""
+        group, bits = self.spec(path)
+        return (self.t[path + ".weight"], self.t[path + ".scales"], self.t[path + ".biases"], bits, group)
+
+    def module_weight(self, path: str) -> np.ndarray:
+        if self.is_quantized(path):
+            w, s, b, bits, group = self.quantized(path)
+            return R.dequantize(w, s.astype(f32), b.astype(f32), bits, group, R.F32)
+        return self.t[path + ".weight"].astype(f32)
+
+    def tensor(self, name: str) -> np.ndarray:
+        return self.t[name].astype(f32)
+
+
+class _Dense:
+    """Plain f32 matrix (or expert stack) in the QLinear interface the MoE
+    oracle consumes."""
+
+    def __init__(self, w: np.ndarray):
+        self.w = np.asarray(w, f32)
+        self.out_dim, self.in_dim = self.w.shape[-2], self.w.shape[-1]
+
+    def dense(self, expert=None):
+        return self.w if expert is None else self.w[expert]
+
+
+def rms_norm(x: np.ndarray, w, eps: float) -> np.ndarray:
+    """QwenCPUModel.rmsNorm (:47-59), rows over the last axis."""
+    x = np.asarray(x, f32)
+    ss = np.sum(x * x, axis=-1, keepdims=True, dtype=f32)
+    scale = f32(1) / np.sqrt(ss / f32(x.shape[-1]) + f32(eps))
+    return (x * (scale * w) if w is not None else x * scale).astype(f32)
+
+
+class TinyQwen:
+    def __init__(self, directory: Path):
+        self.ck = TinyCheckpoint(directory)
+        c = self.ck.cfg
+        self.c = c
+        self.D = c["hidden_size"]
+        self.eps = c.get("rms_norm_eps", 1e-6)
+        self.L = c["num_hidden_layers"]
+        self.interval = c.get("full_attention_interval", 4)
+        self.embed = self.ck.module_weight("model.embed_tokens")
+        self.lm_head = self.embed if c.get("tie_word_embeddings", False) else self.ck.module_weight("lm_head")
+        self.final_norm = self.ck.tensor("model.norm.weight")
+
+    def is_linear(self, i: int) -> bool:
+        return (i + 1) % self.interval != 0
+
+    # -- MoE ------------------------------------------------------------
+    def moe_layer(self, i: int) -> R.MoELayerRef:
+        """The layer's MoE weights as the oracle's layer object; quantized
+        modules keep their packed form (the experts are dequantised per call)."""
+        p = f"model.layers.{i}.mlp."
+        ck = self.ck
+
+        def lin(path):
+            if ck.is_quantized(path):
+                w, s, b, bits, group = ck.quantized(path)
+                return R.QLinear(w, s.astype(f32), b.astype(f32), bits, group, R.F32)
+            return _Dense(ck.t[path + ".weight"])
+
+        return R.MoELayerRef(
+            router=lin(p + "gate"),
+            gate=lin(p + "switch_mlp.gate_proj"), up=lin(p + "switch_mlp.up_proj"),
+            down=lin(p + "switch_mlp.down_proj"),
+            shared_gate=lin(p + "shared_expert.gate_proj"), shared_up=lin(p + "shared_expert.up_proj"),
+            shared_down=lin(p + "shared_expert.down_proj"), shared_expert_gate=lin(p + "shared_expert_gate"),
+            top_k=self.c["num_experts_per_tok"], norm_topk_prob=bool(self.c.get("norm_topk_prob", False)))
+
+    # -- attention (QwenCPUModel.swift:285-345) ---------------------------
+    def apply_rope(self, x: np.ndarray) -> np.ndarray:
+        c = self.c
+        hd = c["head_dim"]
+        rot = int(hd * c.get("partial_rotary_factor", 0.25))
+        half = rot // 2
+        S = x.shape[0]
+        j = np.arange(half)
+        inv = np.power(f32(c["rope_theta"]), (-(2 * j).astype(f32) / f32(rot)).astype(f32)).astype(f32)
+        ang = (np.arange(S, dtype=f32)[:, None] * inv[None, :]).astype(f32)
+        cs, sn = np.cos(ang).astype(f32)[:, None, :], np.sin(ang).astype(f32)[:, None, :]
+        out = x.copy()
+        a, b = x[..., :half], x[..., half:rot]
+        out[..., :half] = a * cs - b * sn
+        out[..., half:rot] = b * cs + a * sn
+        return out
+
+    def attention_forward(self, x: np.ndarray, i: int) -> np.ndarray:
+        c, ck = self.c, self.ck
+        p = f"model.layers.{i}.self_attn."
+        H, KVH, hd = c["num_attention_heads"], c["num_key_value_heads"], c["head_dim"]
+        S = x.shape[0]
+        q_out = (x @ ck.module_weight(p + "q_proj").T).reshape(S, H, 2 * hd)
+        q, gate = q_out[..., :hd], q_out[..., hd:].reshape(S, H * hd)
+        k = (x @ ck.module_weight(p + "k_proj").T).reshape(S, KVH, hd)
+        v = (x @ ck.module_weight(p + "v_proj").T).reshape(S, KVH, hd)
+        q = rms_norm(q, ck.tensor(p + "q_norm.weight"), self.eps)
+        k = rms_norm(k, ck.tensor(p + "k_norm.weight"), self.eps)
+        q, k = self.apply_rope(q), self.apply_rope(k)
+        scale = f32(1) / np.sqrt(f32(hd))
+        out = np.zeros((S, H, hd), f32)
+        group = H // KVH
+        for h in range(H):
+            kv = h // group
+            for si in range(S):
+                sc = (k[: si + 1, kv, :] @ q[si, h, :]) * scale
+                pr = R.softmax_row(sc)
+                out[si, h] = pr @ v[: si + 1, kv, :]
+        out = out.reshape(S, H * hd) * R.sigmoid(gate)
+        return (out @ ck.module_weight(p + "o_proj").T).astype(f32)
+
+    # -- gated DeltaNet, fused interleaved layout (QwenCPUModel.swift:371-496)
+    def deltanet_forward(self, x: np.ndarray, i: int) -> np.ndarray:
+        c, ck = self.c, self.ck
+        p = f"model.layers.{i}.linear_attn."
+        nk, nv = c["linear_num_key_heads"], c["linear_num_value_heads"]
+        dk, dv = c["linear_key_head_dim"], c["linear_value_head_dim"]
+        rep = nv // nk
+        keyD, valD = nk * dk, nv * dv
+        convD = 2 * keyD + valD
+        Kc = c["linear_conv_kernel_dim"]
+        S = x.shape[0]
+        qkvz = x @ ck.module_weight(p + "in_proj_qkvz").T
+        ba = x @ ck.module_weight(p + "in_proj_ba").T
+        chunk = 2 * dk + 2 * rep * dv
+        mixed = np.zeros((S, convD), f32)
+        z = np.zeros((S, valD), f32)
+        bA = np.zeros((S, nv), f32)
+        aA = np.zeros((S, nv), f32)
+        for hk in range(nk):
+            src = qkvz[:, hk * chunk:(hk + 1) * chunk]
+            mixed[:, hk * dk:(hk + 1) * dk] = src[:, :dk]
+            mixed[:, keyD + hk * dk:keyD + (hk + 1) * dk] = src[:, dk:2 * dk]
+            for ri in range(rep):
+                hv = hk * rep + ri
+                mixed[:, 2 * keyD + hv * dv:2 * keyD + (hv + 1) * dv] = src[:, 2 * dk + ri * dv:2 * dk + (ri + 1) * dv]
+                z[:, hv * dv:(hv + 1) * dv] = src[:, 2 * dk + rep * dv + ri * dv:2 * dk + rep * dv + (ri + 1) * dv]
+            bsrc = ba[:, hk * 2 * rep:(hk + 1) * 2 * rep]
+            bA[:, hk * rep:(hk + 1) * rep] = bsrc[:, :rep]
+            aA[:, hk * rep:(hk + 1) * rep] = bsrc[:, rep:]
+        conv_w = ck.tensor(p + "conv1d.weight").reshape(convD, Kc)
+        padded = np.concatenate([np.zeros((Kc - 1, convD), f32), mixed], axis=0)
+        conv = np.zeros((S, convD), f32)
+        for s in range(S):
+            acc = np.zeros(convD, f32)
+            for j in range(Kc):
+                acc = acc + conv_w[:, j] * padded[s + j]
+            conv[s] = acc
+        conv = R.silu(conv)
+        qh = rms_norm(conv[:, :keyD].reshape(S, nk, dk), None, 1e-6)
+        kh = rms_norm(conv[:, keyD:2 * keyD].reshape(S, nk, dk), None, 1e-6)
+        vh = conv[:, 2 * keyD:].reshape(S, nv, dv)
+        inv = f32(1) / np.sqrt(f32(dk))
+        qh = qh * (inv * inv)
+        kh = kh * inv
+        a_log, dt_bias = ck.tensor(p + "A_log"), ck.tensor(p + "dt_bias")
+        state = np.zeros((nv, dv, dk), f32)
+        out = np.zeros((S, nv, dv), f32)
+        for s in range(S):
+            for hv in range(nv):
+                hk = hv // rep
+                v_ = aA[s, hv] + dt_bias[hv]
+                softplus = v_ if v_ > 20 else np.log1p(np.exp(v_))
+                g = np.exp(-np.exp(a_log[hv]) * softplus).astype(f32)
+                beta = R.sigmoid(bA[s, hv])
+                st = state[hv] * g
+                kv_mem = st @ kh[s, hk]
+                delta = (vh[s, hv] - kv_mem) * beta
+                st = st + np.outer(delta, kh[s, hk])
+                state[hv] = st
+                out[s, hv] = st @ qh[s, hk]
+        normed = rms_norm(out, ck.tensor(p + "norm.weight"), self.eps).reshape(S, valD)
+        normed = normed * R.silu(z)
+        return (normed @ ck.module_weight(p + "out_proj").T).astype(f32)
+
+    # -- layer / model ------------------------------------------------------
+    def layer_forward(self, h: np.ndarray, i: int) -> np.ndarray:
+        """norm -> (DeltaNet | attention) -> residual -> norm -> MoE -> residual."""
+        ck = self.ck
+        p = f"model.layers.{i}."
+        x = rms_norm(h, ck.tensor(p + "input_layernorm.weight"), self.eps)
+        r = self.deltanet_forward(x, i) if self.is_linear(i) else self.attention_forward(x, i)
+        h = (h + r).astype(f32)
+        x2 = rms_norm(h, ck.tensor(p + "post_attention_layernorm.weight"), self.eps)
+        m, _, _ = R.moe_forward(x2, self.moe_layer(i))
+        return (h + m).astype(f32)
+
+    def moe_input(self, h: np.ndarray, i: int) -> np.ndarray:
+        """The MoE block's input inside layer i for layer input h."""
+        ck = self.ck
+        p = f"model.layers.{i}."
+        x = rms_norm(h, ck.tensor(p + "input_layernorm.weight"), self.eps)
+        r = self.deltanet_forward(x, i) if self.is_linear(i) else self.attention_forward(x, i)
+        h = (h + r).astype(f32)
+        return rms_norm(h, ck.tensor(p + "post_attention_layernorm.weight"), self.eps)
+
+    def forward(self, tokens):
+        h = self.embed[np.asarray(tokens)].astype(f32)
+        layers = []
+        for i in range(self.L):
+            h = self.layer_forward(h, i)
+            layers.append(h)
+        hn = rms_norm(h, self.final_norm, self.eps)
+        logits = (hn @ self.lm_head.T).astype(f32)
+        return logits, layers, np.argmax(logits, axis=-1)

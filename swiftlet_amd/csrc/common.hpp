@@ -37,7 +37,7 @@ struct QMat {
     int32_t chunks_per_group;
     int32_t lpr_log2;      // log2(lanes per row) of the vectorised path
     int32_t cpl;           // 16-byte chunks per lane
-    int32_t pad_;
+    int32_t cpg_log2;      // log2(chunks per group)
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t u) {

@@ -12,18 +12,18 @@ constexpr int kGemvThreads = 256;
 constexpr int kGemvRI = 4;
 
 // Vectorised GEMV: 16-byte code chunks, kGemvRI passes of rows per wave.
-template <int BITS, int CPL>
+template <int BITS, int CPL, int ES>
 __global__ __launch_bounds__(kGemvThreads) void gemv_vec_kernel(QMat m, int rows, const float *x, float *y) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const LaneMap lm = lane_map(m.lpr_log2, lane);
     const int row0 = (blockIdx.x * (kGemvThreads / kWave) + wave) * kGemvRI * lm.rpw;
     if (row0 >= rows) return;
-    RowTile<BITS, CPL, kGemvRI> rt;
+    RowTile<BITS, CPL, kGemvRI, ES> rt;
     load_tile(rt, m, 0, lm, row0, rows);
     XSlice<BITS, CPL> xs;
     load_xslice<0>(xs, m, lm, x, 0);
     float res[kGemvRI];
-    dot_tile(res, rt, xs, lm);
+    dot_tile(res, rt, xs, m, lm);
     if (lm.j == 0) {
 #pragma unroll
         for (int i = 0; i < kGemvRI; ++i) {
@@ -84,6 +84,7 @@ __global__ void silu_mul_kernel(float *buf, int count, int64_t g_off, int64_t u_
 __global__ void dequant_kernel(const uint8_t *w, const uint8_t *s, const uint8_t *b, int64_t stride_w,
                                int64_t stride_sb, int out_dim, int64_t row0, int64_t rows, int in, int group,
                                int bits, int stype, float *out) {
+#pragma clang fp contract(off)
     const int per_word = 32 / bits;
     const int64_t wpr = in / per_word;
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -104,7 +105,8 @@ __global__ void dequant_kernel(const uint8_t *w, const uint8_t *s, const uint8_t
         const int64_t gi = rr * gpr + col / group;
         const float sc = load_scale_bytes(sb, gi, stype);
         const float bi = load_scale_bytes(bb, gi, stype);
-        out[r * in + col] = __fadd_rn(__fmul_rn(sc, static_cast<float>(word & mask)), bi);
+        const float prod = sc * static_cast<float>(word & mask);  // contract(off): no fused multiply-add
+        out[r * in + col] = prod + bi;
         word >>= bits;
     }
 }
@@ -117,14 +119,18 @@ static int launch_gemv(const swq_qlinear *l, int rows, int64_t w_extra, int64_t 
         if (m.cpl <= (m.bits == 4 ? 2 : 4)) {
             const int rows_per_block = (kGemvThreads / kWave) * kGemvRI * (kWave >> m.lpr_log2);
             const dim3 grid((rows + rows_per_block - 1) / rows_per_block);
+#define SWQ_GEMV_LAUNCH(B, C, E) \
+    hipLaunchKernelGGL((gemv_vec_kernel<B, C, E>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y)
+            const bool f32s = m.stype == SWQ_F32;
             if (m.bits == 4) {
-                if (m.cpl == 1) hipLaunchKernelGGL((gemv_vec_kernel<4, 1>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y);
-                else hipLaunchKernelGGL((gemv_vec_kernel<4, 2>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y);
+                if (m.cpl == 1) { if (f32s) SWQ_GEMV_LAUNCH(4, 1, 4); else SWQ_GEMV_LAUNCH(4, 1, 2); }
+                else { if (f32s) SWQ_GEMV_LAUNCH(4, 2, 4); else SWQ_GEMV_LAUNCH(4, 2, 2); }
             } else {
-                if (m.cpl == 1) hipLaunchKernelGGL((gemv_vec_kernel<8, 1>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y);
-                else if (m.cpl == 2) hipLaunchKernelGGL((gemv_vec_kernel<8, 2>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y);
-                else hipLaunchKernelGGL((gemv_vec_kernel<8, 4>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y);
+                if (m.cpl == 1) { if (f32s) SWQ_GEMV_LAUNCH(8, 1, 4); else SWQ_GEMV_LAUNCH(8, 1, 2); }
+                else if (m.cpl == 2) { if (f32s) SWQ_GEMV_LAUNCH(8, 2, 4); else SWQ_GEMV_LAUNCH(8, 2, 2); }
+                else { if (f32s) SWQ_GEMV_LAUNCH(8, 4, 4); else SWQ_GEMV_LAUNCH(8, 4, 2); }
             }
+#undef SWQ_GEMV_LAUNCH
             return launch_status();
         }
     }

@@ -46,6 +46,8 @@ inline bool vector_path_ok(const swq_qlinear *l, int64_t w_extra, int64_t s_extr
     if (l->bits != 4 && l->bits != 8) return false;
     if ((static_cast<int64_t>(l->in_dim) * l->bits) % 128 != 0) return false;
     if ((static_cast<int64_t>(l->group_size) * l->bits) % 128 != 0) return false;
+    const int cpg = static_cast<int>(static_cast<int64_t>(l->group_size) * l->bits / 128);
+    if ((cpg & (cpg - 1)) != 0) return false;  // chunks per group: a power of two
     const uintptr_t w = reinterpret_cast<uintptr_t>(l->w) + l->w_off + w_extra;
     if (w % 16 != 0 || l->expert_stride_w % 16 != 0) return false;
     const int sb = scale_bytes(l->scales_type);
@@ -86,6 +88,7 @@ inline QMat make_qmat(const swq_qlinear *l, int64_t w_extra = 0, int64_t s_extra
     if (m.chunks > 0) lane_plan(m.chunks, &lpr_log2, &cpl);
     m.lpr_log2 = lpr_log2;
     m.cpl = cpl;
+    m.cpg_log2 = m.chunks_per_group > 0 ? ilog2_exact(m.chunks_per_group) : 0;
     return m;
 }
 

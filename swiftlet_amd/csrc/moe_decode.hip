@@ -52,23 +52,33 @@ struct MoEArgs {
     int32_t rows3;         // stage-3 rows per workgroup
 };
 
-// Wave-uniform dispatch over (bits, chunks per lane) of a matrix.
-// Wave-uniform dispatch over (bits, chunks per lane) of a matrix.  Rows of
-// up to 2048 inputs: 4-bit rows take one 16-byte chunk per lane, 8-bit rows
-// one or two (the host rejects wider rows with SWQ_ERR_LIMIT).
+// Wave-uniform dispatch over (bits, chunks per lane, scale bytes) of a
+// matrix.  Rows of up to 2048 inputs: 4-bit rows take one 16-byte chunk per
+// lane, 8-bit rows one or two (the host rejects wider rows with
+// SWQ_ERR_LIMIT).
+#define SWQ_DISPATCH_ES(XDT, m, FN, ES, ...)                       \
+    do {                                                           \
+        if ((m).bits == 4) FN<XDT, 4, 1, ES>(__VA_ARGS__);         \
+        else if ((m).cpl == 1) FN<XDT, 8, 1, ES>(__VA_ARGS__);     \
+        else FN<XDT, 8, 2, ES>(__VA_ARGS__);                       \
+    } while (0)
 #define SWQ_DISPATCH(XDT, m, FN, ...)                              \
     do {                                                           \
-        if ((m).bits == 4) FN<XDT, 4, 1>(__VA_ARGS__);             \
-        else if ((m).cpl == 1) FN<XDT, 8, 1>(__VA_ARGS__);         \
-        else FN<XDT, 8, 2>(__VA_ARGS__);                           \
+        if ((m).stype == SWQ_F32) SWQ_DISPATCH_ES(XDT, m, FN, 4, __VA_ARGS__); \
+        else SWQ_DISPATCH_ES(XDT, m, FN, 2, __VA_ARGS__);          \
     } while (0)
 
 // Down projections (stage 3): one chunk per lane, i.e. up to 2048 inputs at
 // 4 bits and 1024 at 8 bits.
 #define SWQ_DISPATCH_DOWN(m, FN, ...)                              \
     do {                                                           \
-        if ((m).bits == 4) FN<0, 4, 1>(__VA_ARGS__);               \
-        else FN<0, 8, 1>(__VA_ARGS__);                             \
+        if ((m).stype == SWQ_F32) {                                \
+            if ((m).bits == 4) FN<0, 4, 1, 4>(__VA_ARGS__);        \
+            else FN<0, 8, 1, 4>(__VA_ARGS__);                      \
+        } else {                                                   \
+            if ((m).bits == 4) FN<0, 4, 1, 2>(__VA_ARGS__);        \
+            else FN<0, 8, 1, 2>(__VA_ARGS__);                      \
+        }                                                          \
     } while (0)
 
 __device__ __forceinline__ void store_coherent(float *p, float v) {
@@ -81,18 +91,18 @@ __device__ __forceinline__ float load_coherent(const float *p) {
 
 // Rows [row0, row0 + kRI*rpw) of one matrix against every token's x;
 // result of (token b, row) goes to out[b*ld + row].
-template <int XDT, int BITS, int CPL>
+template <int XDT, int BITS, int CPL, int ES>
 __device__ __forceinline__ void gemv_rows_tokens(const QMat &m, int row0, int row_end, const void *x,
                                  int H, int B, float *out, int ld, bool coherent, int lane) {
     const LaneMap lm = lane_map(m.lpr_log2, lane);
-    RowTile<BITS, CPL, kRI> rt;
+    RowTile<BITS, CPL, kRI, ES> rt;
     load_tile(rt, m, 0, lm, row0, row_end);
 #pragma unroll 1
     for (int b = 0; b < B; ++b) {
         XSlice<BITS, CPL> xs;
         load_xslice<XDT>(xs, m, lm, x, static_cast<int64_t>(b) * H);
         float res[kRI];
-        dot_tile(res, rt, xs, lm);
+        dot_tile(res, rt, xs, m, lm);
         if (lm.j == 0) {
 #pragma unroll
             for (int i = 0; i < kRI; ++i) {
@@ -108,12 +118,12 @@ __device__ __forceinline__ void gemv_rows_tokens(const QMat &m, int row0, int ro
 
 // SwiGLU rows of one expert: h[dst_p*ld + r] = silu(gate_r . x_b) * (up_r . x_b)
 // for each (token b, destination p) pair.  pairs == nullptr means p = b.
-template <int XDT, int BITS, int CPL>
+template <int XDT, int BITS, int CPL, int ES>
 __device__ __forceinline__ void gateup_rows(const QMat &g, const QMat &u, int64_t expert, int row0, int row_end,
                             const void *x, int H, const int32_t *pairs, int npairs, int K,
                             float *h, int ld, int lane) {
     const LaneMap lm = lane_map(g.lpr_log2, lane);
-    RowTile<BITS, CPL, kRI> tg, tu;
+    RowTile<BITS, CPL, kRI, ES> tg, tu;
     load_tile(tg, g, expert, lm, row0, row_end);
     load_tile(tu, u, expert, lm, row0, row_end);
 #pragma unroll 1
@@ -123,8 +133,8 @@ __device__ __forceinline__ void gateup_rows(const QMat &g, const QMat &u, int64_
         XSlice<BITS, CPL> xs;
         load_xslice<XDT>(xs, g, lm, x, static_cast<int64_t>(b) * H);
         float rg[kRI], ru[kRI];
-        dot_tile(rg, tg, xs, lm);
-        dot_tile(ru, tu, xs, lm);
+        dot_tile(rg, tg, xs, g, lm);
+        dot_tile(ru, tu, xs, u, lm);
         if (lm.j == 0) {
 #pragma unroll
             for (int i = 0; i < kRI; ++i) {
@@ -137,7 +147,7 @@ __device__ __forceinline__ void gateup_rows(const QMat &g, const QMat &u, int64_
 
 // Down rows [row0, row0 + nrows) of one expert for each pair p: the dot of
 // the row with h[p] lands in part[slot_base + pi][row - row0].
-template <int XDT, int BITS, int CPL>
+template <int XDT, int BITS, int CPL, int ES>
 __device__ __forceinline__ void down_rows(const QMat &m, int64_t expert, int row0, int nrows, int row_end,
                           const float *h, int ld, const int32_t *pairs, int npairs,
                           float (*part)[kRows3], int part_base, int lane) {
@@ -146,7 +156,7 @@ __device__ __forceinline__ void down_rows(const QMat &m, int64_t expert, int row
     const int end = min(row0 + nrows, row_end);
 #pragma unroll 1
     for (int t0 = row0; t0 < end; t0 += tile_rows) {
-        RowTile<BITS, CPL, kRI> rt;
+        RowTile<BITS, CPL, kRI, ES> rt;
         load_tile(rt, m, expert, lm, t0, end);
 #pragma unroll 1
         for (int pi = 0; pi < npairs; ++pi) {
@@ -154,7 +164,7 @@ __device__ __forceinline__ void down_rows(const QMat &m, int64_t expert, int row
             XSlice<BITS, CPL> xs;
             load_xslice<0>(xs, m, lm, h, static_cast<int64_t>(p) * ld);
             float res[kRI];
-            dot_tile(res, rt, xs, lm);
+            dot_tile(res, rt, xs, m, lm);
             if (lm.j == 0) {
 #pragma unroll
                 for (int i = 0; i < kRI; ++i) {

@@ -1,0 +1,132 @@
+"""The C ABI without a GPU: libswq.so loads, exports every symbol the headers
+declare, and its host-side validation returns the documented status codes
+before touching a device (SURVEY-listed failure modes: in % group, bits
+outside {2,4,8}, top_k > E, misaligned pointers, short workspace)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from swiftlet_amd import _lib
+from swiftlet_amd._lib import MoELayer, QLinear
+
+ROOT = Path(__file__).resolve().parent.parent
+FAKE = 0x7F0000000000  # a well-aligned address; validation fails before any use
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def declared_functions():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(swq_\w+)\s*\(", text))
+    return sorted(names)
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert "swq_moe_decode" in names and "swq_encode_gemv" in names
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
+
+
+def test_strerror_and_version(lib):
+    assert lib.swq_version() >= 100
+    for code in range(0, -11, -1):
+        s = lib.swq_strerror(code).decode()
+        assert s and s != "unknown status", code
+    assert lib.swq_strerror(-99).decode() == "unknown status"
+
+
+def lin(out_dim, in_dim, bits=4, group=64, stype=_lib.SWQ_F16, stride_w=0, stride_sb=0, base=FAKE):
+    return QLinear(w=base, scales=base + (1 << 30), biases=base + (2 << 30), w_off=0, s_off=0, b_off=0,
+                   out_dim=out_dim, in_dim=in_dim, group_size=group, bits=bits, scales_type=stype,
+                   reserved=0, expert_stride_w=stride_w, expert_stride_sb=stride_sb)
+
+
+def layer(H=2048, E=256, K=8, I=512, Is=512, bits=4, rbits=8, **kw):
+    ew = I * H * bits // 8
+    es = I * (H // 64) * 2
+    d = dict(router=lin(E, H, rbits), gate=lin(I, H, bits, stride_w=ew, stride_sb=es),
+             up=lin(I, H, bits, stride_w=ew, stride_sb=es), down=lin(H, I, bits, stride_w=ew, stride_sb=es),
+             shared_gate=lin(Is, H, bits), shared_up=lin(Is, H, bits), shared_down=lin(H, Is, bits),
+             shared_expert_gate=lin(1, H, rbits), hidden=H, num_experts=E, top_k=K, moe_intermediate=I,
+             shared_intermediate=Is, norm_topk_prob=1, has_shared=1, reserved=0)
+    d.update(kw)
+    return MoELayer(**d)
+
+
+def test_workspace_query(lib):
+    L = layer()
+    n1 = lib.swq_moe_decode_workspace_bytes(ctypes.byref(L), 1)
+    n4 = lib.swq_moe_decode_workspace_bytes(ctypes.byref(L), 4)
+    assert n1 > 8 * 512 * 4 and n4 > n1 and n1 % 256 == 0
+    assert lib.swq_moe_decode_workspace_bytes(ctypes.byref(L), 0) == 0
+    assert lib.swq_moe_decode_workspace_bytes(ctypes.byref(L), 17) == 0  # above SWQ_MAX_BATCH
+
+
+def decode(lib, L, batch=1, ws_bytes=None, x=FAKE, x_dtype=_lib.SWQ_BF16, out_dtype=_lib.SWQ_F32, flags=0, ws=FAKE):
+    if ws_bytes is None:
+        ws_bytes = max(lib.swq_moe_decode_workspace_bytes(ctypes.byref(L), batch), 1 << 20)
+    return lib.swq_moe_decode(ctypes.byref(L), x, x_dtype, batch, FAKE, out_dtype, None, None, ws, ws_bytes,
+                              flags, None)
+
+
+@pytest.mark.parametrize("mutate,code", [
+    (dict(top_k=0), _lib.SWQ_ERR_EXPERT_RANGE),
+    (dict(top_k=300), _lib.SWQ_ERR_EXPERT_RANGE),
+    (dict(top_k=17, num_experts=64, router=lin(64, 2048, 8)), _lib.SWQ_ERR_LIMIT),
+    (dict(reserved=1), _lib.SWQ_ERR_INVALID_ARGUMENT),
+    (dict(router=lin(256, 2048, 3)), _lib.SWQ_ERR_UNSUPPORTED_BITS),
+    (dict(router=lin(256, 2048, 8, group=96)), _lib.SWQ_ERR_BAD_SHAPE),      # in % group != 0
+    (dict(router=lin(256, 2048, 8, stype=7)), _lib.SWQ_ERR_UNSUPPORTED_DTYPE),
+    (dict(router=lin(128, 2048, 8)), _lib.SWQ_ERR_BAD_SHAPE),                # out_dim != E
+    (dict(router=lin(256, 2048, 8, base=FAKE + 4)), _lib.SWQ_ERR_MISALIGNED),
+    (dict(gate=lin(512, 2048, 4, stride_w=0, stride_sb=0)), _lib.SWQ_ERR_INVALID_ARGUMENT),
+    (dict(hidden=4096), _lib.SWQ_ERR_BAD_SHAPE),                             # router in_dim != hidden
+    (dict(hidden=4096, router=lin(256, 4096, 8)), _lib.SWQ_ERR_LIMIT),       # 8-bit rows above 2048
+])
+def test_layer_validation(lib, mutate, code):
+    assert decode(lib, layer(**mutate)) == code
+
+
+def test_call_validation(lib):
+    L = layer()
+    assert decode(lib, L, batch=0) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert decode(lib, L, batch=17) == _lib.SWQ_ERR_LIMIT
+    assert decode(lib, L, ws_bytes=64) == _lib.SWQ_ERR_WORKSPACE
+    assert decode(lib, L, ws=0) == _lib.SWQ_ERR_WORKSPACE
+    assert decode(lib, L, x=0) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert decode(lib, L, x=FAKE + 2) == _lib.SWQ_ERR_MISALIGNED
+    assert decode(lib, L, x_dtype=_lib.SWQ_F16) == _lib.SWQ_ERR_UNSUPPORTED_DTYPE
+    assert decode(lib, L, flags=4) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert decode(lib, L, flags=_lib.SWQ_MOE_ACCUMULATE, out_dtype=_lib.SWQ_BF16) == _lib.SWQ_ERR_UNSUPPORTED_DTYPE
+
+
+def test_gemv_validation(lib):
+    bad = lin(16, 100, 4, group=64)  # in % group != 0
+    assert lib.swq_encode_gemv(ctypes.byref(bad), 0, 0, 0, 0, FAKE, 0, FAKE, 0, None) == _lib.SWQ_ERR_BAD_SHAPE
+    bad = lin(16, 128, 5, group=64)
+    assert lib.swq_encode_gemv(ctypes.byref(bad), 0, 0, 0, 0, FAKE, 0, FAKE, 0, None) == _lib.SWQ_ERR_UNSUPPORTED_BITS
+    ok = lin(16, 128, 4, group=64)
+    assert lib.swq_encode_gemv(ctypes.byref(ok), 0, 0, 0, 0, 0, 0, FAKE, 0, None) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert lib.swq_dequantize(ctypes.byref(ok), 10, 10, FAKE, None) == _lib.SWQ_ERR_BAD_SHAPE  # past out_dim
+    assert lib.swq_encode_silu_mul(FAKE, 0, 0, 0, 0, None) == _lib.SWQ_ERR_INVALID_ARGUMENT
+
+
+def test_no_device_reported(lib):
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a device is visible")
+    n = ctypes.c_int(5)
+    assert lib.swq_device_count(ctypes.byref(n)) == _lib.SWQ_ERR_NO_DEVICE and n.value == 0
+    from swiftlet_amd.engine import HipEngine, NoDevice
+    with pytest.raises(NoDevice):
+        HipEngine()

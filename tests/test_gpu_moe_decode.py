@@ -100,7 +100,7 @@ def test_moe_decode_deterministic_and_accumulate():
 
 @pytest.mark.parametrize("E,K,I,Is,H,bits,norm", [
     (8, 2, 32, 32, 64, 4, True),      # the tiny model's MoE shape
-    (60, 4, 64, 96, 256, 8, False),   # E not a multiple of 64, norm_topk_prob false
+    (60, 4, 64, 128, 256, 8, False),  # E not a multiple of 64, norm_topk_prob false
     (128, 1, 128, 64, 512, 4, True),  # top-1
     (1024, 16, 64, 64, 128, 4, True), # widest top-k table
 ])
