@@ -9,8 +9,8 @@ HBM.  The K timed steps cycle through `--replicas` distinct seeded layers
 (each with all E experts) and distinct inputs, so the bytes a step touches
 come from HBM, not from the 256 MB last-level cache.  The steps are
 captured in one HIP graph and replayed; the per-kernel durations come from
-HIP events around each stage in a separate eager pass queued behind a stall
-kernel.  Prints one JSON line.
+graph replays of each stage on its own, timed with HIP events.  Prints one
+JSON line.
 """
 
 from __future__ import annotations
@@ -133,27 +133,38 @@ def main():
     graph_ms = e0.elapsed_time(e1)
     us_per_step = graph_ms * 1000.0 / K
 
-    # ---- eager pass with per-stage HIP events (queued behind a stall) ----
-    n_ev = min(K, 4 * R)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n_ev)]
-    check(lib.swq_bench_stall(20000, sh), "stall")  # tens of ms of queue backlog
+    # ---- per-kernel durations: graphs of single-stage steps --------------
+    # Each replica's workspace already holds its routing from the replays
+    # above, so a stage on its own reads valid inputs.  The graph's launches
+    # run back to back; HIP events around one replay give the average launch.
+    n_st = min(K, 4 * R)
+    stage_us = []
+    for mask in (1, 2, 4):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for i in range(n_st):
+                c = calls[i % R]
+                check(lib.swq_moe_decode_stages(*c, mask, cap), "moe_decode stage (capture)")
+        g.replay()
+        torch.cuda.synchronize()
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record()
+        g.replay()
+        a1.record()
+        torch.cuda.synchronize()
+        stage_us.append(a0.elapsed_time(a1) * 1000.0 / n_st)
+        del g
+    # eager (no graph) launches of whole steps, for reference
+    check(lib.swq_bench_stall(20000, sh), "stall")
     t_eager0 = torch.cuda.Event(enable_timing=True)
     t_eager1 = torch.cuda.Event(enable_timing=True)
     t_eager0.record()
-    for i in range(n_ev):
-        ev = evs[i]
-        ev[0].record()
-        step(i, 1)
-        ev[1].record()
-        step(i, 2)
-        ev[2].record()
-        step(i, 4)
-        ev[3].record()
+    for i in range(n_st):
+        step(i)
     t_eager1.record()
     torch.cuda.synchronize()
-    stage_us = [float(np.mean([evs[i][s].elapsed_time(evs[i][s + 1]) for i in range(n_ev)])) * 1000.0
-                for s in range(3)]
-    eager_us_per_step = t_eager0.elapsed_time(t_eager1) * 1000.0 / n_ev
+    eager_us_per_step = t_eager0.elapsed_time(t_eager1) * 1000.0 / n_st
     # unique experts per step (batch > 1 reads each distinct expert once)
     ids_h = ids.cpu().numpy()
     uniq = [len(np.unique(ids_h[r])) for r in range(R)]

@@ -38,6 +38,8 @@ struct QMat {
     int32_t lpr_log2;      // log2(lanes per row) of the vectorised path
     int32_t cpl;           // 16-byte chunks per lane
     int32_t cpg_log2;      // log2(chunks per group)
+    int32_t xf;            // activation format: 0 fp32 fma, 1 packed bf16 dot2
+    int32_t pad_;
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t u) {

@@ -9,24 +9,25 @@
 namespace swq {
 
 constexpr int kGemvThreads = 256;
-constexpr int kGemvRI = 4;
 
-// Vectorised GEMV: 16-byte code chunks, kGemvRI passes of rows per wave.
+// Vectorised GEMV: one wave computes a tile of rows (4/CPL passes of 64/LPR
+// rows) over fp32 activations.
 template <int BITS, int CPL, int ES>
 __global__ __launch_bounds__(kGemvThreads) void gemv_vec_kernel(QMat m, int rows, const float *x, float *y) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const LaneMap lm = lane_map(m.lpr_log2, lane);
-    const int row0 = (blockIdx.x * (kGemvThreads / kWave) + wave) * kGemvRI * lm.rpw;
+    const int row0 = (blockIdx.x * (kGemvThreads / kWave) + wave) * RI * lm.rpw;
     if (row0 >= rows) return;
-    RowTile<BITS, CPL, kGemvRI, ES> rt;
+    RowTile<BITS, CPL, ES> rt;
     load_tile(rt, m, 0, lm, row0, rows);
-    XSlice<BITS, CPL> xs;
-    load_xslice<0>(xs, m, lm, x, 0);
-    float res[kGemvRI];
+    XSlice<BITS, CPL, kXF32> xs;
+    load_xslice<SWQ_F32>(xs, m, lm, x, 0);
+    float res[RI];
     dot_tile(res, rt, xs, m, lm);
-    if (lm.j == 0) {
+    if (lm.j == lm.lpr - 1) {
 #pragma unroll
-        for (int i = 0; i < kGemvRI; ++i) {
+        for (int i = 0; i < RI; ++i) {
             const int row = row0 + i * lm.rpw + lm.q;
             if (row < rows) y[row] = res[i];
         }
@@ -116,19 +117,17 @@ static int launch_gemv(const swq_qlinear *l, int rows, int64_t w_extra, int64_t 
     const bool x_aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0;
     if (allow_vec && x_aligned && vector_path_ok(l, w_extra, s_extra, b_extra)) {
         QMat m = make_qmat(l, w_extra, s_extra, b_extra);
-        if (m.cpl <= (m.bits == 4 ? 2 : 4)) {
-            const int rows_per_block = (kGemvThreads / kWave) * kGemvRI * (kWave >> m.lpr_log2);
+        if (plan_fits(m)) {
+            const int rows_per_block = (kGemvThreads / kWave) * (4 / m.cpl) * (kWave >> m.lpr_log2);
             const dim3 grid((rows + rows_per_block - 1) / rows_per_block);
 #define SWQ_GEMV_LAUNCH(B, C, E) \
     hipLaunchKernelGGL((gemv_vec_kernel<B, C, E>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y)
             const bool f32s = m.stype == SWQ_F32;
             if (m.bits == 4) {
-                if (m.cpl == 1) { if (f32s) SWQ_GEMV_LAUNCH(4, 1, 4); else SWQ_GEMV_LAUNCH(4, 1, 2); }
-                else { if (f32s) SWQ_GEMV_LAUNCH(4, 2, 4); else SWQ_GEMV_LAUNCH(4, 2, 2); }
+                if (f32s) SWQ_GEMV_LAUNCH(4, 1, 4); else SWQ_GEMV_LAUNCH(4, 1, 2);
             } else {
                 if (m.cpl == 1) { if (f32s) SWQ_GEMV_LAUNCH(8, 1, 4); else SWQ_GEMV_LAUNCH(8, 1, 2); }
-                else if (m.cpl == 2) { if (f32s) SWQ_GEMV_LAUNCH(8, 2, 4); else SWQ_GEMV_LAUNCH(8, 2, 2); }
-                else { if (f32s) SWQ_GEMV_LAUNCH(8, 4, 4); else SWQ_GEMV_LAUNCH(8, 4, 2); }
+                else { if (f32s) SWQ_GEMV_LAUNCH(8, 2, 4); else SWQ_GEMV_LAUNCH(8, 2, 2); }
             }
 #undef SWQ_GEMV_LAUNCH
             return launch_status();

@@ -57,14 +57,35 @@ inline bool vector_path_ok(const swq_qlinear *l, int64_t w_extra, int64_t s_extr
     return true;
 }
 
-// Lanes per row and chunks per lane of the vectorised path for a row of
-// `chunks` 16-byte chunks: LPR = min(64, next power of two), CPL = the
-// chunks each lane walks.
-inline void lane_plan(int chunks, int *lpr_log2, int *cpl) {
-    int lpr = 1;
-    while (lpr < chunks && lpr < kWave) lpr <<= 1;
-    *lpr_log2 = ilog2_exact(lpr);
-    *cpl = (chunks + lpr - 1) / lpr;
+// Lane plan of the vectorised path: each lane walks `cpl` 16-byte chunks of
+// a row, and LPR = ceil(chunks / cpl) rounded up to a power of two (at most
+// 64) lanes cover the row; lanes past its end idle.
+inline int lpr_log2_for(int chunks, int cpl) {
+    int lanes = (chunks + cpl - 1) / cpl;
+    int l = 0;
+    while ((1 << l) < lanes && l < 6) ++l;
+    return l;
+}
+
+// Activation format and chunks per lane for a matrix read with x of dtype
+// x_dtype: 4-bit codes with bf16 x take packed-bf16 dot products over 4
+// chunks per lane; everything else fp32 fmas over one chunk per lane (two
+// for 8-bit rows wider than 1024).
+inline void plan_qmat(QMat *m, int x_dtype) {
+    if (m->bits == 4 && x_dtype == SWQ_BF16) {
+        m->xf = 1;
+        m->cpl = 4;
+    } else {
+        m->xf = 0;
+        m->cpl = m->chunks > 64 ? 2 : 1;
+    }
+    m->lpr_log2 = lpr_log2_for(m->chunks, m->cpl);
+}
+
+// Largest row (in 16-byte chunks) each plan accepts.
+inline bool plan_fits(const QMat &m) {
+    if (m.xf == 1) return m.chunks <= 4 * kWave;
+    return m.chunks <= m.cpl * kWave && (m.bits == 8 || m.cpl == 1);
 }
 
 inline QMat make_qmat(const swq_qlinear *l, int64_t w_extra = 0, int64_t s_extra = 0,
@@ -84,10 +105,7 @@ inline QMat make_qmat(const swq_qlinear *l, int64_t w_extra = 0, int64_t s_extra
     m.gpr = l->in_dim / l->group_size;
     m.chunks = static_cast<int32_t>(static_cast<int64_t>(l->in_dim) * l->bits / 128);
     m.chunks_per_group = static_cast<int32_t>(static_cast<int64_t>(l->group_size) * l->bits / 128);
-    int lpr_log2 = 0, cpl = 1;
-    if (m.chunks > 0) lane_plan(m.chunks, &lpr_log2, &cpl);
-    m.lpr_log2 = lpr_log2;
-    m.cpl = cpl;
+    plan_qmat(&m, SWQ_F32);
     m.cpg_log2 = m.chunks_per_group > 0 ? ilog2_exact(m.chunks_per_group) : 0;
     return m;
 }

@@ -1,10 +1,10 @@
 // MoE-layer decode step on gfx950: three launches per layer.
 //
-//   stage 1  router GEMV (+ shared-expert gate GEMV + shared gate/up SwiGLU);
-//            the last router workgroup to finish runs softmax, top-k and
-//            renormalisation and builds the distinct-expert list.
-//   stage 2  gate/up SwiGLU of every distinct selected expert, indexed by
-//            the device-resident top-k ids (one launch for all experts).
+//   stage 1  router GEMV, shared-expert gate GEMV, shared gate/up SwiGLU.
+//   stage 2  every workgroup runs softmax, top-k and renormalisation on the
+//            router logits itself (and, for batches, the distinct-expert
+//            list), then the gate/up SwiGLU rows of its expert: one launch for
+//            all selected experts, indexed by device-resident ids.
 //   stage 3  down projections of the selected experts and of the shared
 //            expert, weighted combine in pick order, then the shared term.
 //
@@ -21,7 +21,6 @@
 
 namespace swq {
 
-constexpr int kRI = 4;  // row passes per wave tile
 constexpr int kThreads12 = 256;
 constexpr int kMaxPairs = SWQ_MAX_BATCH * SWQ_MAX_TOPK;
 constexpr int kMaxExperts = 1024;
@@ -33,7 +32,6 @@ struct MoEArgs {
     void *out;
     int32_t *user_ids;
     float *user_w;
-    unsigned *counter;     // [1] router workgroups finished (self-resetting)
     float *logits;         // [B][E]
     float *sg;             // [B] shared gate logit
     float *h_sh;           // [B][Is] shared SwiGLU activations
@@ -52,92 +50,91 @@ struct MoEArgs {
     int32_t rows3;         // stage-3 rows per workgroup
 };
 
-// Wave-uniform dispatch over (bits, chunks per lane, scale bytes) of a
-// matrix.  Rows of up to 2048 inputs: 4-bit rows take one 16-byte chunk per
-// lane, 8-bit rows one or two (the host rejects wider rows with
-// SWQ_ERR_LIMIT).
-#define SWQ_DISPATCH_ES(XDT, m, FN, ES, ...)                       \
-    do {                                                           \
-        if ((m).bits == 4) FN<XDT, 4, 1, ES>(__VA_ARGS__);         \
-        else if ((m).cpl == 1) FN<XDT, 8, 1, ES>(__VA_ARGS__);     \
-        else FN<XDT, 8, 2, ES>(__VA_ARGS__);                       \
+// Wave-uniform dispatch over a matrix's plan (bits, chunks per lane,
+// activation format) and scale bytes.  FN<XDT, BITS, CPL, ES, XF>.
+#define SWQ_DISPATCH_ES(XDT, m, FN, ES, ...)                                \
+    do {                                                                    \
+        if constexpr (XDT == SWQ_BF16) {                                    \
+            if ((m).bits == 4) FN<XDT, 4, 4, ES, kXBF16>(__VA_ARGS__);      \
+            else if ((m).cpl == 1) FN<XDT, 8, 1, ES, kXF32>(__VA_ARGS__);   \
+            else FN<XDT, 8, 2, ES, kXF32>(__VA_ARGS__);                     \
+        } else {                                                            \
+            if ((m).bits == 4) FN<XDT, 4, 1, ES, kXF32>(__VA_ARGS__);       \
+            else if ((m).cpl == 1) FN<XDT, 8, 1, ES, kXF32>(__VA_ARGS__);   \
+            else FN<XDT, 8, 2, ES, kXF32>(__VA_ARGS__);                     \
+        }                                                                   \
     } while (0)
-#define SWQ_DISPATCH(XDT, m, FN, ...)                              \
-    do {                                                           \
+#define SWQ_DISPATCH(XDT, m, FN, ...)                                       \
+    do {                                                                    \
         if ((m).stype == SWQ_F32) SWQ_DISPATCH_ES(XDT, m, FN, 4, __VA_ARGS__); \
-        else SWQ_DISPATCH_ES(XDT, m, FN, 2, __VA_ARGS__);          \
+        else SWQ_DISPATCH_ES(XDT, m, FN, 2, __VA_ARGS__);                   \
     } while (0)
 
-// Down projections (stage 3): one chunk per lane, i.e. up to 2048 inputs at
-// 4 bits and 1024 at 8 bits.
-#define SWQ_DISPATCH_DOWN(m, FN, ...)                              \
-    do {                                                           \
-        if ((m).stype == SWQ_F32) {                                \
-            if ((m).bits == 4) FN<0, 4, 1, 4>(__VA_ARGS__);        \
-            else FN<0, 8, 1, 4>(__VA_ARGS__);                      \
-        } else {                                                   \
-            if ((m).bits == 4) FN<0, 4, 1, 2>(__VA_ARGS__);        \
-            else FN<0, 8, 1, 2>(__VA_ARGS__);                      \
-        }                                                          \
+// Down projections read the fp32 SwiGLU activations: one chunk per lane,
+// i.e. up to 2048 inputs at 4 bits and 1024 at 8 bits.
+#define SWQ_DISPATCH_DOWN(m, FN, ...)                                       \
+    do {                                                                    \
+        if ((m).stype == SWQ_F32) {                                         \
+            if ((m).bits == 4) FN<SWQ_F32, 4, 1, 4, kXF32>(__VA_ARGS__);    \
+            else FN<SWQ_F32, 8, 1, 4, kXF32>(__VA_ARGS__);                  \
+        } else {                                                            \
+            if ((m).bits == 4) FN<SWQ_F32, 4, 1, 2, kXF32>(__VA_ARGS__);    \
+            else FN<SWQ_F32, 8, 1, 2, kXF32>(__VA_ARGS__);                  \
+        }                                                                   \
     } while (0)
 
-__device__ __forceinline__ void store_coherent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// Rows one wave covers in one tile: 4/CPL passes of 64/LPR rows.
+__host__ __device__ __forceinline__ int tile_rows(const QMat &m) { return (4 / m.cpl) * (kWave >> m.lpr_log2); }
 
-__device__ __forceinline__ float load_coherent(const float *p) {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Rows [row0, row0 + kRI*rpw) of one matrix against every token's x;
-// result of (token b, row) goes to out[b*ld + row].
-template <int XDT, int BITS, int CPL, int ES>
+// One tile of rows of one matrix against every token's x; the result of
+// (token b, row) goes to out[b*ld + row].
+template <int XDT, int BITS, int CPL, int ES, int XF>
 __device__ __forceinline__ void gemv_rows_tokens(const QMat &m, int row0, int row_end, const void *x,
-                                 int H, int B, float *out, int ld, bool coherent, int lane) {
+                                                 int H, int B, float *out, int ld, int lane) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
     const LaneMap lm = lane_map(m.lpr_log2, lane);
-    RowTile<BITS, CPL, kRI, ES> rt;
+    RowTile<BITS, CPL, ES> rt;
     load_tile(rt, m, 0, lm, row0, row_end);
 #pragma unroll 1
     for (int b = 0; b < B; ++b) {
-        XSlice<BITS, CPL> xs;
+        XSlice<BITS, CPL, XF> xs;
         load_xslice<XDT>(xs, m, lm, x, static_cast<int64_t>(b) * H);
-        float res[kRI];
+        float res[RI];
         dot_tile(res, rt, xs, m, lm);
-        if (lm.j == 0) {
+        if (lm.j == lm.lpr - 1) {
 #pragma unroll
-            for (int i = 0; i < kRI; ++i) {
+            for (int i = 0; i < RI; ++i) {
                 const int row = row0 + i * lm.rpw + lm.q;
-                if (row < row_end) {
-                    if (coherent) store_coherent(out + b * ld + row, res[i]);
-                    else out[b * ld + row] = res[i];
-                }
+                if (row < row_end) out[b * ld + row] = res[i];
             }
         }
     }
 }
 
-// SwiGLU rows of one expert: h[dst_p*ld + r] = silu(gate_r . x_b) * (up_r . x_b)
-// for each (token b, destination p) pair.  pairs == nullptr means p = b.
-template <int XDT, int BITS, int CPL, int ES>
+// SwiGLU rows of one expert: h[p*ld + r] = silu(gate_r . x_b) * (up_r . x_b)
+// for each (token b, destination p) pair; pairs == nullptr means p = b.
+template <int XDT, int BITS, int CPL, int ES, int XF>
 __device__ __forceinline__ void gateup_rows(const QMat &g, const QMat &u, int64_t expert, int row0, int row_end,
-                            const void *x, int H, const int32_t *pairs, int npairs, int K,
-                            float *h, int ld, int lane) {
+                                            const void *x, int H, const int32_t *pairs, int npairs, int K,
+                                            float *h, int ld, int lane) {
+    if (npairs <= 0) return;
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
     const LaneMap lm = lane_map(g.lpr_log2, lane);
-    RowTile<BITS, CPL, kRI, ES> tg, tu;
+    RowTile<BITS, CPL, ES> tg, tu;
     load_tile(tg, g, expert, lm, row0, row_end);
     load_tile(tu, u, expert, lm, row0, row_end);
 #pragma unroll 1
     for (int pi = 0; pi < npairs; ++pi) {
         const int p = pairs ? pairs[pi] : pi;
         const int b = pairs ? p / K : pi;
-        XSlice<BITS, CPL> xs;
+        XSlice<BITS, CPL, XF> xs;
         load_xslice<XDT>(xs, g, lm, x, static_cast<int64_t>(b) * H);
-        float rg[kRI], ru[kRI];
+        float rg[RI], ru[RI];
         dot_tile(rg, tg, xs, g, lm);
         dot_tile(ru, tu, xs, u, lm);
-        if (lm.j == 0) {
+        if (lm.j == lm.lpr - 1) {
 #pragma unroll
-            for (int i = 0; i < kRI; ++i) {
+            for (int i = 0; i < RI; ++i) {
                 const int row = row0 + i * lm.rpw + lm.q;
                 if (row < row_end) h[static_cast<int64_t>(p) * ld + row] = swiglu(rg[i], ru[i]);
             }
@@ -146,31 +143,83 @@ __device__ __forceinline__ void gateup_rows(const QMat &g, const QMat &u, int64_
 }
 
 // Down rows [row0, row0 + nrows) of one expert for each pair p: the dot of
-// the row with h[p] lands in part[slot_base + pi][row - row0].
-template <int XDT, int BITS, int CPL, int ES>
+// the row with h[p] lands in part[part_base + p][row - row0].
+template <int XDT, int BITS, int CPL, int ES, int XF>
 __device__ __forceinline__ void down_rows(const QMat &m, int64_t expert, int row0, int nrows, int row_end,
-                          const float *h, int ld, const int32_t *pairs, int npairs,
-                          float (*part)[kRows3], int part_base, int lane) {
+                                          const float *h, int ld, const int32_t *pairs, int npairs,
+                                          float (*part)[kRows3], int part_base, int lane) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
     const LaneMap lm = lane_map(m.lpr_log2, lane);
-    const int tile_rows = kRI * lm.rpw;
     const int end = min(row0 + nrows, row_end);
 #pragma unroll 1
-    for (int t0 = row0; t0 < end; t0 += tile_rows) {
-        RowTile<BITS, CPL, kRI, ES> rt;
+    for (int t0 = row0; t0 < end; t0 += RI * lm.rpw) {
+        RowTile<BITS, CPL, ES> rt;
         load_tile(rt, m, expert, lm, t0, end);
 #pragma unroll 1
         for (int pi = 0; pi < npairs; ++pi) {
             const int p = pairs ? pairs[pi] : pi;
-            XSlice<BITS, CPL> xs;
-            load_xslice<0>(xs, m, lm, h, static_cast<int64_t>(p) * ld);
-            float res[kRI];
+            XSlice<BITS, CPL, XF> xs;
+            load_xslice<XDT>(xs, m, lm, h, static_cast<int64_t>(p) * ld);
+            float res[RI];
             dot_tile(res, rt, xs, m, lm);
-            if (lm.j == 0) {
+            if (lm.j == lm.lpr - 1) {
 #pragma unroll
-                for (int i = 0; i < kRI; ++i) {
+                for (int i = 0; i < RI; ++i) {
                     const int row = t0 + i * lm.rpw + lm.q;
                     if (row < end) part[part_base + p][row - row0] = res[i];
                 }
+            }
+        }
+    }
+}
+
+
+// Batch-1 SwiGLU rows of expert e, the pick in slot `slot`.
+template <int XDT, int BITS, int CPL, int ES, int XF>
+__device__ __forceinline__ void gateup_rows_b1(const QMat &g, const QMat &u, int e, int slot, int row0,
+                                               int row_end, const void *x, float *h, int ld, int lane) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
+    const LaneMap lm = lane_map(g.lpr_log2, lane);
+    RowTile<BITS, CPL, ES> tg, tu;
+    load_tile(tg, g, e, lm, row0, row_end);
+    load_tile(tu, u, e, lm, row0, row_end);
+    XSlice<BITS, CPL, XF> xs;
+    load_xslice<XDT>(xs, g, lm, x, 0);
+    float rg[RI], ru[RI];
+    dot_tile(rg, tg, xs, g, lm);
+    dot_tile(ru, tu, xs, u, lm);
+    if (lm.j == lm.lpr - 1) {
+#pragma unroll
+        for (int i = 0; i < RI; ++i) {
+            const int row = row0 + i * lm.rpw + lm.q;
+            if (row < row_end) h[static_cast<int64_t>(slot) * ld + row] = swiglu(rg[i], ru[i]);
+        }
+    }
+}
+
+// Batch-1 down rows [row0, row0 + nrows) of the expert in slot `slot` (or of
+// the shared expert when ids == nullptr) against activations hv.
+template <int XDT, int BITS, int CPL, int ES, int XF>
+__device__ __forceinline__ void down_rows_b1(const QMat &m, const int32_t *ids, int slot, int row0, int nrows,
+                                             int row_end, const float *hv, float (*part)[kRows3], int part_row,
+                                             int lane) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
+    const LaneMap lm = lane_map(m.lpr_log2, lane);
+    const int end = min(row0 + nrows, row_end);
+    XSlice<BITS, CPL, XF> xs;
+    load_xslice<XDT>(xs, m, lm, hv, 0);
+    const int64_t e = ids ? ids[slot] : 0;
+#pragma unroll 1
+    for (int t0 = row0; t0 < end; t0 += RI * lm.rpw) {
+        RowTile<BITS, CPL, ES> rt;
+        load_tile(rt, m, e, lm, t0, end);
+        float res[RI];
+        dot_tile(res, rt, xs, m, lm);
+        if (lm.j == lm.lpr - 1) {
+#pragma unroll
+            for (int i = 0; i < RI; ++i) {
+                const int row = t0 + i * lm.rpw + lm.q;
+                if (row < end) part[part_row][row - row0] = res[i];
             }
         }
     }
@@ -188,31 +237,53 @@ __device__ __forceinline__ float from_orderable(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    for (int off = 32; off > 0; off >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, kWave)));
-    return v;
+// Wave-wide maximum: DPP within each 16-lane row, then the four row maxima
+// through scalar registers.  Every lane receives it.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, true));
 }
 
-// Selection by logit with ties to the lower expert id equals the
-// reference's selection by softmax probability (softmax is monotonic) up to
-// fp32 ties of exp().  Each lane holds experts lane*M .. lane*M+M-1 as
-// 64-bit keys (orderable logit, inverted id), sorted descending; K rounds
-// take the wave-wide maximum head.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = max(v, dpp_u32<0x141>(v));  // row_half_mirror
+    v = max(v, dpp_u32<0x140>(v));  // row_mirror
+    const uint32_t r0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 0));
+    const uint32_t r1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 16));
+    const uint32_t r2 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 32));
+    const uint32_t r3 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 48));
+    return max(max(r0, r1), max(r2, r3));
+}
+
+// Sum over the wave, returned to every lane (the last lane of the DPP scan
+// holds it; readlane broadcasts).
+__device__ __forceinline__ float wave_sum_all(float v) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(segment_reduce(v, 6)), 63));
+}
+
+// Top-k of one token's router logits, one wave.  Selection by logit with
+// ties to the lower expert id equals the reference's selection by softmax
+// probability (QwenCPUModel.swift:508-522; softmax is monotonic) up to fp32
+// ties of exp().  Lane l holds experts l*M .. l*M+M-1 as 64-bit keys
+// (orderable logit, inverted id), sorted descending; each of the K rounds
+// takes the wave-wide maximum head.  Then p_k = exp(l_k - max) / sum_e
+// exp(l_e - max) (:65-71) and w_k = p_k / sum_j p_j when norm (:546-550).
+// Writes ids[k], w[k] (LDS); sel_l is LDS scratch of K floats.
 template <int M>
-__device__ __forceinline__ void topk_token(const MoEArgs &a, int b, int lane, int32_t *sel_e, float *sel_l) {
-    uint64_t key[M];
+__device__ __forceinline__ void topk_token(const float *lrow, int E, int K, int norm, int lane, int32_t *ids,
+                                           float *w, float *sel_l) {
     float lg[M];
+#pragma unroll
+    for (int j = 0; j < M; ++j) lg[j] = lrow[min(lane * M + j, E - 1)];  // every load issued first
+    uint64_t key[M];
 #pragma unroll
     for (int j = 0; j < M; ++j) {
         const int e = lane * M + j;
-        if (e < a.E) {
-            const float l = load_coherent(a.logits + static_cast<int64_t>(b) * a.E + e);
-            lg[j] = l;
-            key[j] = (static_cast<uint64_t>(orderable(l)) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(e));
-        } else {
-            lg[j] = -INFINITY;
-            key[j] = 0;
-        }
+        const bool valid = e < E;
+        key[j] = valid ? (static_cast<uint64_t>(orderable(lg[j])) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(e))
+                       : 0;
+        if (!valid) lg[j] = -INFINITY;
     }
 #pragma unroll
     for (int i = 0; i < M; ++i) {
@@ -225,7 +296,8 @@ __device__ __forceinline__ void topk_token(const MoEArgs &a, int b, int lane, in
             }
         }
     }
-    for (int k = 0; k < a.K; ++k) {
+    float top = 0.f;
+    for (int k = 0; k < K; ++k) {
         const uint32_t hi = static_cast<uint32_t>(key[0] >> 32);
         const uint32_t lo = static_cast<uint32_t>(key[0]);
         const uint32_t mhi = wave_max_u32(hi);
@@ -237,10 +309,12 @@ __device__ __forceinline__ void topk_token(const MoEArgs &a, int b, int lane, in
             const uint32_t mlo = wave_max_u32(hi == mhi ? lo : 0u);
             winner = __ffsll(static_cast<long long>(__ballot(hi == mhi && lo == mlo))) - 1;
         }
-        const uint32_t wlo = static_cast<uint32_t>(__shfl(static_cast<int>(lo), winner, kWave));
+        const uint32_t wlo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo), winner));
+        const float l = from_orderable(mhi);
+        if (k == 0) top = l;
         if (lane == 0) {
-            sel_e[k] = static_cast<int32_t>(0xFFFFFFFFu - wlo);
-            sel_l[k] = from_orderable(mhi);
+            ids[k] = static_cast<int32_t>(0xFFFFFFFFu - wlo);
+            sel_l[k] = l;
         }
         if (lane == winner) {
 #pragma unroll
@@ -248,165 +322,230 @@ __device__ __forceinline__ void topk_token(const MoEArgs &a, int b, int lane, in
             key[M - 1] = 0;
         }
     }
-    // softmax denominator over all experts (max = the first pick's logit)
-    const float m = __shfl(sel_l[0], 0, kWave);
     float part = 0.f;
 #pragma unroll
-    for (int j = 0; j < M; ++j) part += (lane * M + j < a.E) ? expf(lg[j] - m) : 0.f;
-    const float denom = wave_sum(part);
-    if (lane == 0) {
-        // p_k = exp(l_k - m) / sum; w_k = p_k / sum_j p_j in pick order
-        // (QwenCPUModel.swift:546-550)
-        float total = 0.f;
-        for (int k = 0; k < a.K; ++k) total += expf(sel_l[k] - m) / denom;
-        for (int k = 0; k < a.K; ++k) {
-            const float pk = expf(sel_l[k] - m) / denom;
-            const float w = a.norm ? pk / total : pk;
-            const int idx = b * a.K + k;
-            a.ids[idx] = sel_e[k];
-            a.wts[idx] = w;
-            if (a.user_ids) a.user_ids[idx] = sel_e[k];
-            if (a.user_w) a.user_w[idx] = w;
-        }
-    }
+    for (int j = 0; j < M; ++j) part += expf(lg[j] - top);  // -inf padding adds 0
+    const float denom = wave_sum_all(part);
+    const float pk = lane < K ? expf(sel_l[lane] - top) / denom : 0.f;
+    const float total = wave_sum_all(pk);
+    if (lane < K) w[lane] = norm ? pk / total : pk;
 }
 
-// Distinct experts over all (token, pick) pairs p = b*K + k, in order of
-// first appearance; each pair joins its expert's list in pair order.  One
-// thread per pair (P <= blockDim.x), two O(P) passes over the ids in LDS.
-__device__ __forceinline__ void build_unique(const MoEArgs &a, const int32_t *s_ids, int32_t *s_lead, int32_t *s_slot) {
+// The block's routing, in LDS.
+struct Routing {
+    int32_t ids[kMaxPairs];    // [B][K] picks, pair p = b*K + k
+    float w[kMaxPairs];        // combine weights
+    float sel_l[kThreads12 / kWave][SWQ_MAX_TOPK];
+    int32_t lead[kMaxPairs];   // pair leads its expert's list
+    int32_t slot[kMaxPairs];   // distinct slot of a leading pair
+    int32_t uniq_e[kMaxPairs];
+    int32_t uniq_np[kMaxPairs];
+    int32_t pairs[SWQ_MAX_BATCH];  // pairs of this block's slot
+    int32_t n_unique;
+};
+
+// Every token's top-k into r (one wave per token), then for batches the
+// distinct experts in order of first appearance, each with its pairs in pair
+// order (one thread per pair, two O(P) passes).  `my_slot` selects whose pair
+// list lands in r.pairs; with `publish` the block also writes the routing to
+// the workspace (and the caller's outputs) for stage 3.
+__device__ __forceinline__ void route(const MoEArgs &a, Routing &r, int my_slot, bool publish) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int M = (a.E + kWave - 1) / kWave;
+    for (int b = wave; b < a.B; b += kThreads12 / kWave) {
+        const float *lrow = a.logits + static_cast<int64_t>(b) * a.E;
+        int32_t *ids = r.ids + b * a.K;
+        float *w = r.w + b * a.K;
+        if (M <= 1) topk_token<1>(lrow, a.E, a.K, a.norm, lane, ids, w, r.sel_l[wave]);
+        else if (M <= 2) topk_token<2>(lrow, a.E, a.K, a.norm, lane, ids, w, r.sel_l[wave]);
+        else if (M <= 4) topk_token<4>(lrow, a.E, a.K, a.norm, lane, ids, w, r.sel_l[wave]);
+        else if (M <= 8) topk_token<8>(lrow, a.E, a.K, a.norm, lane, ids, w, r.sel_l[wave]);
+        else topk_token<16>(lrow, a.E, a.K, a.norm, lane, ids, w, r.sel_l[wave]);
+    }
+    __syncthreads();
     const int P = a.B * a.K;
     const int p = threadIdx.x;
+    if (publish && p < P) {
+        a.ids[p] = r.ids[p];
+        a.wts[p] = r.w[p];
+        if (a.user_ids) a.user_ids[p] = r.ids[p];
+        if (a.user_w) a.user_w[p] = r.w[p];
+    }
+    if (a.B == 1) {
+        if (p == 0) r.n_unique = a.K;  // a token's picks are distinct
+        __syncthreads();
+        return;
+    }
     int first = p, pos = 0, count = 0;
     if (p < P) {
-        const int e = s_ids[p];
+        const int e = r.ids[p];
         for (int q = 0; q < P; ++q) {
-            const bool same = s_ids[q] == e;
+            const bool same = r.ids[q] == e;
             if (same && q < p) {
                 first = min(first, q);
                 ++pos;
             }
             count += same ? 1 : 0;
         }
-        s_lead[p] = (first == p) ? 1 : 0;
+        r.lead[p] = (first == p) ? 1 : 0;
     }
     __syncthreads();
     if (p < P && first == p) {
         int rank = 0, total = 0;
         for (int q = 0; q < P; ++q) {
-            rank += (q < p) ? s_lead[q] : 0;
-            total += s_lead[q];
+            rank += (q < p) ? r.lead[q] : 0;
+            total += r.lead[q];
         }
-        s_slot[p] = rank;
-        a.uniq_e[rank] = s_ids[p];
-        a.uniq_np[rank] = count;
-        if (p == 0) *a.n_unique = total;
+        r.slot[p] = rank;
+        r.uniq_e[rank] = r.ids[p];
+        r.uniq_np[rank] = count;
+        if (p == 0) r.n_unique = total;
+        if (publish) {
+            a.uniq_e[rank] = r.ids[p];
+            a.uniq_np[rank] = count;
+            if (p == 0) *a.n_unique = total;
+        }
     }
     __syncthreads();
-    if (p < P) a.uniq_pairs[s_slot[first] * a.B + pos] = p;
+    if (p < P) {
+        const int slot = r.slot[first];
+        if (slot == my_slot) r.pairs[pos] = p;
+        if (publish) a.uniq_pairs[slot * a.B + pos] = p;
+    }
+    __syncthreads();
 }
 
-template <int M>
-__device__ __forceinline__ void topk_all(const MoEArgs &a, int32_t (*sel_e)[SWQ_MAX_TOPK], float (*sel_l)[SWQ_MAX_TOPK],
-                         int32_t *s_ids) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int b = wave; b < a.B; b += kThreads12 / kWave) {
-        topk_token<M>(a, b, lane, sel_e[wave], sel_l[wave]);
-        if (lane < a.K) s_ids[b * a.K + lane] = sel_e[wave][lane];
+// Pull this workgroup's share (part `part` of `parts`) of a matrix's codes,
+// scales and biases toward the last-level cache: plain loads whose values are
+// only kept alive.  Stage 3 then reads the down projections from cache.
+__device__ __forceinline__ uint32_t touch_share(const QMat &m, int64_t expert, int part, int parts) {
+    const int64_t wbytes = static_cast<int64_t>(m.rows) * m.row_bytes;
+    const int64_t sbytes = static_cast<int64_t>(m.rows) * m.gpr * (m.stype == SWQ_F32 ? 4 : 2);
+    const uint8_t *w = m.w + expert * m.stride_w;
+    const uint8_t *sc = m.s + expert * m.stride_sb;
+    const uint8_t *bi = m.b + expert * m.stride_sb;
+    const int64_t wshare = (wbytes / parts) & ~static_cast<int64_t>(63);
+    const int64_t sshare = (sbytes / parts) & ~static_cast<int64_t>(63);
+    uint32_t acc = 0;
+    // one 16-byte load per 64 bytes: one per 64-byte segment of each cache line
+    for (int64_t o = static_cast<int64_t>(threadIdx.x) * 64; o < wshare; o += blockDim.x * 64)
+        acc ^= reinterpret_cast<const uint4 *>(w + part * wshare + o)->x;
+    for (int64_t o = static_cast<int64_t>(threadIdx.x) * 64; o < sshare; o += blockDim.x * 64) {
+        acc ^= *reinterpret_cast<const uint32_t *>(sc + part * sshare + o);
+        acc ^= *reinterpret_cast<const uint32_t *>(bi + part * sshare + o);
     }
+    return acc;
 }
+
+__device__ __forceinline__ void keep(uint32_t v) { asm volatile("" ::"v"(v)); }
 
 template <int XDT>
 __global__ __launch_bounds__(kThreads12) void moe_stage1(MoEArgs a) {
-    __shared__ int32_t s_sel_e[kThreads12 / kWave][SWQ_MAX_TOPK];
-    __shared__ float s_sel_l[kThreads12 / kWave][SWQ_MAX_TOPK];
-    __shared__ int32_t s_ids[kMaxPairs];
-    __shared__ int32_t s_lead[kMaxPairs];
-    __shared__ int32_t s_slot[kMaxPairs];
-    __shared__ int s_is_last;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int task = blockIdx.x * (kThreads12 / kWave) + wave;
-
     if (static_cast<int>(blockIdx.x) < a.nr_blocks) {
-        if (task < a.router_tasks) {
-            const int rows_per_task = kRI * (kWave >> a.router.lpr_log2);
-            SWQ_DISPATCH(XDT, a.router, gemv_rows_tokens, a.router, task * rows_per_task, a.E, a.x,
-                         a.H, a.B, a.logits, a.E, true, lane);
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            __threadfence();
-            const unsigned done = atomicAdd(a.counter, 1u);
-            s_is_last = (done == static_cast<unsigned>(a.nr_blocks - 1));
-        }
-        __syncthreads();
-        if (!s_is_last) return;
-        __threadfence();
-        // the last router workgroup: softmax, top-k, renormalisation
-        const int M = (a.E + kWave - 1) / kWave;
-        if (M <= 1) topk_all<1>(a, s_sel_e, s_sel_l, s_ids);
-        else if (M <= 2) topk_all<2>(a, s_sel_e, s_sel_l, s_ids);
-        else if (M <= 4) topk_all<4>(a, s_sel_e, s_sel_l, s_ids);
-        else if (M <= 8) topk_all<8>(a, s_sel_e, s_sel_l, s_ids);
-        else topk_all<16>(a, s_sel_e, s_sel_l, s_ids);
-        __syncthreads();
-        build_unique(a, s_ids, s_lead, s_slot);
-        if (threadIdx.x == 0) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (task < a.router_tasks)
+            SWQ_DISPATCH(XDT, a.router, gemv_rows_tokens, a.router, task * tile_rows(a.router), a.E, a.x,
+                         a.H, a.B, a.logits, a.E, lane);
         return;
     }
-
-    // shared-expert workgroups
-    const int t = task - a.nr_blocks * (kThreads12 / kWave);
+    // shared-expert workgroups; the shared down projection is pulled toward
+    // the cache for stage 3 meanwhile
     if (!a.has_shared) return;
-    if (t == 0) {
-        SWQ_DISPATCH(XDT, a.seg, gemv_rows_tokens, a.seg, 0, 1, a.x, a.H, a.B, a.sg, 1, false, lane);
-    } else if (t - 1 < a.shared_tasks) {
-        const int rows_per_task = kRI * (kWave >> a.sh_gate.lpr_log2);
-        SWQ_DISPATCH(XDT, a.sh_gate, gateup_rows, a.sh_gate, a.sh_up, 0, (t - 1) * rows_per_task, a.Is,
+    const int sb = blockIdx.x - a.nr_blocks;
+    const uint32_t t = touch_share(a.sh_down, 0, sb, gridDim.x - a.nr_blocks);
+    const int st = task - a.nr_blocks * (kThreads12 / kWave);
+    if (st == 0) {
+        SWQ_DISPATCH(XDT, a.seg, gemv_rows_tokens, a.seg, 0, 1, a.x, a.H, a.B, a.sg, 1, lane);
+    } else if (st - 1 < a.shared_tasks) {
+        SWQ_DISPATCH(XDT, a.sh_gate, gateup_rows, a.sh_gate, a.sh_up, 0, (st - 1) * tile_rows(a.sh_gate), a.Is,
                      a.x, a.H, nullptr, a.B, a.K, a.h_sh, a.Is, lane);
     }
+    keep(t);
 }
 
 template <int XDT>
 __global__ __launch_bounds__(kThreads12) void moe_stage2(MoEArgs a) {
+    __shared__ Routing r;
     const int slot = blockIdx.y;
-    if (slot >= *a.n_unique) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int e = a.uniq_e[slot];
-    const int np = a.uniq_np[slot];
-    const int rows_per_task = kRI * (kWave >> a.gate.lpr_log2);
-    const int row0 = (blockIdx.x * (kThreads12 / kWave) + wave) * rows_per_task;
-    if (row0 >= a.I) return;
-    SWQ_DISPATCH(XDT, a.gate, gateup_rows, a.gate, a.up, e, row0, a.I, a.x, a.H,
-                 a.uniq_pairs + slot * a.B, np, a.K, a.h, a.I, lane);
+    route(a, r, slot, blockIdx.x == 0 && blockIdx.y == 0);
+    if (slot >= r.n_unique) return;
+    const int e = a.B == 1 ? r.ids[slot] : r.uniq_e[slot];
+    const uint32_t t = touch_share(a.down, e, blockIdx.x, gridDim.x);
+    const int row0 = (blockIdx.x * (kThreads12 / kWave) + wave) * tile_rows(a.gate);
+    if (row0 < a.I) {
+        if (a.B == 1) {
+            SWQ_DISPATCH(XDT, a.gate, gateup_rows_b1, a.gate, a.up, e, slot, row0, a.I, a.x, a.h, a.I, lane);
+        } else {
+            SWQ_DISPATCH(XDT, a.gate, gateup_rows, a.gate, a.up, e, row0, a.I, a.x, a.H, r.pairs,
+                         r.uniq_np[slot], a.K, a.h, a.I, lane);
+        }
+    }
+    keep(t);
 }
 
-__global__ __launch_bounds__(1024) void moe_stage3(MoEArgs a) {
+constexpr int kStage3MaxWaves = 12;
+
+__global__ __launch_bounds__(kStage3MaxWaves * 64) void moe_stage3(MoEArgs a) {
     __shared__ float part[kMaxPairs + SWQ_MAX_BATCH][kRows3];
+    __shared__ float s_w[kMaxPairs];
+    __shared__ float s_gate[SWQ_MAX_BATCH];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nw = blockDim.x >> 6;
     const int r0 = blockIdx.x * a.rows3;
-    const int nu = *a.n_unique;
-    const int nslots = nu + (a.has_shared ? 1 : 0);
     const int P = a.B * a.K;
+    // combine weights and shared-gate logits: loaded into registers now,
+    // staged in LDS only after the projections, so their latency overlaps.
+    float w_pre[4];  // P <= 4 * blockDim (the host sizes the block 64*min(12, slots))
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned t = threadIdx.x + i * blockDim.x;
+        w_pre[i] = t < static_cast<unsigned>(P) ? a.wts[t] : 0.f;
+    }
+    const float sg_pre = (a.has_shared && threadIdx.x < static_cast<unsigned>(a.B)) ? a.sg[threadIdx.x] : 0.f;
+    if (a.B == 1) {
+        const int nslots = a.K + (a.has_shared ? 1 : 0);
 #pragma unroll 1
-    for (int s = wave; s < nslots; s += nw) {
-        if (s < nu) {
-            SWQ_DISPATCH_DOWN(a.down, down_rows, a.down, a.uniq_e[s], r0, a.rows3, a.H, a.h, a.I,
-                         a.uniq_pairs + s * a.B, a.uniq_np[s], part, 0, lane);
-        } else {
-            SWQ_DISPATCH_DOWN(a.sh_down, down_rows, a.sh_down, 0, r0, a.rows3, a.H, a.h_sh, a.Is,
-                         nullptr, a.B, part, P, lane);
+        for (int s = wave; s < nslots; s += nw) {
+            if (s < a.K) {
+                SWQ_DISPATCH_DOWN(a.down, down_rows_b1, a.down, a.ids, s, r0, a.rows3, a.H,
+                                  a.h + static_cast<int64_t>(s) * a.I, part, s, lane);
+            } else {
+                SWQ_DISPATCH_DOWN(a.sh_down, down_rows_b1, a.sh_down, nullptr, 0, r0, a.rows3, a.H, a.h_sh,
+                                  part, P, lane);
+            }
+        }
+    } else {
+        const int nu = *a.n_unique;
+        const int nslots = nu + (a.has_shared ? 1 : 0);
+#pragma unroll 1
+        for (int s = wave; s < nslots; s += nw) {
+            if (s < nu) {
+                SWQ_DISPATCH_DOWN(a.down, down_rows, a.down, a.uniq_e[s], r0, a.rows3, a.H, a.h, a.I,
+                                  a.uniq_pairs + s * a.B, a.uniq_np[s], part, 0, lane);
+            } else {
+                SWQ_DISPATCH_DOWN(a.sh_down, down_rows, a.sh_down, 0, r0, a.rows3, a.H, a.h_sh, a.Is,
+                                  nullptr, a.B, part, P, lane);
+            }
         }
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned t = threadIdx.x + i * blockDim.x;
+        if (t < static_cast<unsigned>(P)) s_w[t] = w_pre[i];
+    }
+    if (a.has_shared && threadIdx.x < static_cast<unsigned>(a.B)) s_gate[threadIdx.x] = sigmoidf_ref(sg_pre);
     __syncthreads();
     for (int t = threadIdx.x; t < a.B * a.rows3; t += blockDim.x) {
         const int b = t / a.rows3, rr = t - b * a.rows3;
         const int row = r0 + rr;
         if (row >= a.H) continue;
+        // out = sum_k w_k d_k in pick order, then + sigmoid(sg) * shared
+        // (QwenCPUModel.swift:549-566)
         float acc = 0.f;
-        for (int k = 0; k < a.K; ++k) acc += a.wts[b * a.K + k] * part[b * a.K + k][rr];
-        if (a.has_shared) acc += sigmoidf_ref(a.sg[b]) * part[P + b][rr];
+        for (int k = 0; k < a.K; ++k) acc += s_w[b * a.K + k] * part[b * a.K + k][rr];
+        if (a.has_shared) acc += s_gate[b] * part[P + b][rr];
         const int64_t o = static_cast<int64_t>(b) * a.H + row;
         if (a.odt == SWQ_BF16) {
             static_cast<uint16_t *>(a.out)[o] = f32_to_bf16_rne(acc);
@@ -421,7 +560,7 @@ __global__ __launch_bounds__(1024) void moe_stage3(MoEArgs a) {
 // host side
 
 struct WsLayout {
-    size_t counter, logits, sg, h_sh, ids, wts, n_unique, uniq_e, uniq_np, uniq_pairs, h, total;
+    size_t header, logits, sg, h_sh, ids, wts, n_unique, uniq_e, uniq_np, uniq_pairs, h, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
@@ -435,7 +574,7 @@ static WsLayout ws_layout(const swq_moe_layer *l, int B) {
         return o;
     };
     const size_t P = static_cast<size_t>(B) * l->top_k;
-    w.counter = take(256);
+    w.header = take(256);  // reserved; zeroed by swq_moe_workspace_init
     w.logits = take(static_cast<size_t>(B) * l->num_experts * 4);
     w.sg = take(static_cast<size_t>(B) * 4);
     w.h_sh = take(static_cast<size_t>(B) * (l->has_shared ? l->shared_intermediate : 1) * 4);
@@ -450,7 +589,11 @@ static WsLayout ws_layout(const swq_moe_layer *l, int B) {
     return w;
 }
 
-static int check_vec(const swq_qlinear *l, int out_dim, int in_dim, bool stacked, int E, int max_cpl) {
+// A matrix of the layer: shape, format and alignment, and whether its plan
+// fits the compiled kernels when read with activations of dtype x_dtype
+// (reads_h: the fp32 SwiGLU activations of stage 3).
+static int check_vec(const swq_qlinear *l, int out_dim, int in_dim, bool stacked, int E, int x_dtype,
+                     bool reads_h) {
     int st = check_linear_shape(l);
     if (st != SWQ_OK) return st;
     if (l->out_dim != out_dim || l->in_dim != in_dim) return SWQ_ERR_BAD_SHAPE;
@@ -458,34 +601,34 @@ static int check_vec(const swq_qlinear *l, int out_dim, int in_dim, bool stacked
     if ((static_cast<int64_t>(in_dim) * l->bits) % 128 != 0) return SWQ_ERR_BAD_SHAPE;
     if ((static_cast<int64_t>(l->group_size) * l->bits) % 128 != 0) return SWQ_ERR_BAD_SHAPE;
     if (!vector_path_ok(l, 0, 0, 0)) return SWQ_ERR_MISALIGNED;
-    const int chunks = static_cast<int>(static_cast<int64_t>(in_dim) * l->bits / 128);
-    int lpr_log2, cpl;
-    lane_plan(chunks, &lpr_log2, &cpl);
-    if (cpl > max_cpl || (l->bits == 4 && cpl > 1)) return SWQ_ERR_LIMIT;
+    QMat m = make_qmat(l);
+    plan_qmat(&m, reads_h ? SWQ_F32 : x_dtype);
+    if (!plan_fits(m) || (reads_h && m.cpl != 1)) return SWQ_ERR_LIMIT;
     if (stacked && E > 1 && (l->expert_stride_w == 0 || l->expert_stride_sb == 0)) return SWQ_ERR_INVALID_ARGUMENT;
     return SWQ_OK;
 }
 
-static int check_layer(const swq_moe_layer *l, int B) {
+static int check_layer(const swq_moe_layer *l, int B, int x_dtype) {
     if (!l) return SWQ_ERR_INVALID_ARGUMENT;
     if (l->reserved != 0) return SWQ_ERR_INVALID_ARGUMENT;
     if (B <= 0 || l->hidden <= 0 || l->num_experts <= 0 || l->moe_intermediate <= 0) return SWQ_ERR_INVALID_ARGUMENT;
     if (l->top_k <= 0 || l->top_k > l->num_experts) return SWQ_ERR_EXPERT_RANGE;
     if (l->top_k > SWQ_MAX_TOPK || B > SWQ_MAX_BATCH || l->num_experts > kMaxExperts) return SWQ_ERR_LIMIT;
     const int H = l->hidden, E = l->num_experts, I = l->moe_intermediate;
+    const int xd = x_dtype;
     int st;
-    if ((st = check_vec(&l->router, E, H, false, E, 2)) != SWQ_OK) return st;
-    if ((st = check_vec(&l->gate, I, H, true, E, 2)) != SWQ_OK) return st;
-    if ((st = check_vec(&l->up, I, H, true, E, 2)) != SWQ_OK) return st;
-    if ((st = check_vec(&l->down, H, I, true, E, 1)) != SWQ_OK) return st;
+    if ((st = check_vec(&l->router, E, H, false, E, xd, false)) != SWQ_OK) return st;
+    if ((st = check_vec(&l->gate, I, H, true, E, xd, false)) != SWQ_OK) return st;
+    if ((st = check_vec(&l->up, I, H, true, E, xd, false)) != SWQ_OK) return st;
+    if ((st = check_vec(&l->down, H, I, true, E, xd, true)) != SWQ_OK) return st;
     if (l->gate.bits != l->up.bits || l->gate.in_dim != l->up.in_dim) return SWQ_ERR_BAD_SHAPE;
     if (l->has_shared) {
         const int Is = l->shared_intermediate;
         if (Is <= 0) return SWQ_ERR_INVALID_ARGUMENT;
-        if ((st = check_vec(&l->shared_gate, Is, H, false, 1, 2)) != SWQ_OK) return st;
-        if ((st = check_vec(&l->shared_up, Is, H, false, 1, 2)) != SWQ_OK) return st;
-        if ((st = check_vec(&l->shared_down, H, Is, false, 1, 1)) != SWQ_OK) return st;
-        if ((st = check_vec(&l->shared_expert_gate, 1, H, false, 1, 2)) != SWQ_OK) return st;
+        if ((st = check_vec(&l->shared_gate, Is, H, false, 1, xd, false)) != SWQ_OK) return st;
+        if ((st = check_vec(&l->shared_up, Is, H, false, 1, xd, false)) != SWQ_OK) return st;
+        if ((st = check_vec(&l->shared_down, H, Is, false, 1, xd, true)) != SWQ_OK) return st;
+        if ((st = check_vec(&l->shared_expert_gate, 1, H, false, 1, xd, false)) != SWQ_OK) return st;
         if (l->shared_gate.bits != l->shared_up.bits) return SWQ_ERR_BAD_SHAPE;
     }
     return SWQ_OK;
@@ -496,7 +639,7 @@ static int check_layer(const swq_moe_layer *l, int B) {
 using namespace swq;
 
 extern "C" size_t swq_moe_decode_workspace_bytes(const swq_moe_layer *layer, int batch) {
-    if (check_layer(layer, batch) != SWQ_OK) return 0;
+    if (check_layer(layer, batch, SWQ_BF16) != SWQ_OK) return 0;
     return ws_layout(layer, batch).total;
 }
 
@@ -508,10 +651,10 @@ extern "C" int swq_moe_workspace_init(void *ws, size_t ws_bytes, void *stream) {
 extern "C" int swq_moe_decode_stages(const swq_moe_layer *layer, const void *x, int x_dtype, int batch,
                                      void *out, int out_dtype, int32_t *topk_ids, float *topk_weights, void *ws,
                                      size_t ws_bytes, int flags, int stage_mask, void *stream) {
-    int st = check_layer(layer, batch);
+    if (x_dtype != SWQ_F32 && x_dtype != SWQ_BF16) return SWQ_ERR_UNSUPPORTED_DTYPE;
+    int st = check_layer(layer, batch, x_dtype);
     if (st != SWQ_OK) return st;
     if (!x || !out) return SWQ_ERR_INVALID_ARGUMENT;
-    if (x_dtype != SWQ_F32 && x_dtype != SWQ_BF16) return SWQ_ERR_UNSUPPORTED_DTYPE;
     if (out_dtype != SWQ_F32 && out_dtype != SWQ_BF16) return SWQ_ERR_UNSUPPORTED_DTYPE;
     if ((flags & ~SWQ_MOE_ACCUMULATE) != 0) return SWQ_ERR_INVALID_ARGUMENT;
     const bool accumulate = (flags & SWQ_MOE_ACCUMULATE) != 0;
@@ -535,11 +678,18 @@ extern "C" int swq_moe_decode_stages(const swq_moe_layer *layer, const void *x, 
         a.sh_down = make_qmat(&layer->shared_down);
         a.seg = make_qmat(&layer->shared_expert_gate);
     }
+    plan_qmat(&a.router, x_dtype);
+    plan_qmat(&a.gate, x_dtype);
+    plan_qmat(&a.up, x_dtype);
+    plan_qmat(&a.sh_gate, x_dtype);
+    plan_qmat(&a.sh_up, x_dtype);
+    plan_qmat(&a.seg, x_dtype);
+    plan_qmat(&a.down, SWQ_F32);
+    plan_qmat(&a.sh_down, SWQ_F32);
     a.x = x;
     a.out = out;
     a.user_ids = topk_ids;
     a.user_w = topk_weights;
-    a.counter = reinterpret_cast<unsigned *>(wsb + wl.counter);
     a.logits = reinterpret_cast<float *>(wsb + wl.logits);
     a.sg = reinterpret_cast<float *>(wsb + wl.sg);
     a.h_sh = reinterpret_cast<float *>(wsb + wl.h_sh);
@@ -563,18 +713,16 @@ extern "C" int swq_moe_decode_stages(const swq_moe_layer *layer, const void *x, 
     a.has_shared = layer->has_shared ? 1 : 0;
 
     const int waves12 = kThreads12 / kWave;
-    const int router_rows_per_task = kRI * (kWave >> a.router.lpr_log2);
+    const int router_rows_per_task = tile_rows(a.router);
     a.router_tasks = (a.E + router_rows_per_task - 1) / router_rows_per_task;
     a.nr_blocks = (a.router_tasks + waves12 - 1) / waves12;
     int shared_blocks = 0;
     if (a.has_shared) {
-        const int sh_rows_per_task = kRI * (kWave >> a.sh_gate.lpr_log2);
+        const int sh_rows_per_task = tile_rows(a.sh_gate);
         a.shared_tasks = (a.Is + sh_rows_per_task - 1) / sh_rows_per_task;
         shared_blocks = (a.shared_tasks + 1 + waves12 - 1) / waves12;  // +1: shared gate row
     }
-    const int down_rpw = kWave >> a.down.lpr_log2;
-    a.rows3 = min(kRows3, kRI * down_rpw);
-    if (a.rows3 < 1) a.rows3 = 1;
+    a.rows3 = min(kRows3, tile_rows(a.down));
 
     if (stage_mask & ~7) return SWQ_ERR_INVALID_ARGUMENT;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -586,7 +734,7 @@ extern "C" int swq_moe_decode_stages(const swq_moe_layer *layer, const void *x, 
 
     const int P = batch * a.K;
     const int max_slots = min(P, a.E);
-    const int rows2 = kRI * (kWave >> a.gate.lpr_log2) * waves12;
+    const int rows2 = tile_rows(a.gate) * waves12;
     const dim3 grid2((a.I + rows2 - 1) / rows2, max_slots);
     if (stage_mask & 2) {
         if (x_dtype == SWQ_BF16) hipLaunchKernelGGL(moe_stage2<SWQ_BF16>, grid2, dim3(kThreads12), 0, s, a);
@@ -594,7 +742,7 @@ extern "C" int swq_moe_decode_stages(const swq_moe_layer *layer, const void *x, 
         if ((st = launch_status()) != SWQ_OK) return st;
     }
     if (stage_mask & 4) {
-        const int nw3 = min(16, max_slots + a.has_shared);
+        const int nw3 = min(kStage3MaxWaves, max_slots + a.has_shared);
         hipLaunchKernelGGL(moe_stage3, dim3((H + a.rows3 - 1) / a.rows3), dim3(nw3 * kWave), 0, s, a);
         if ((st = launch_status()) != SWQ_OK) return st;
     }

@@ -1,21 +1,35 @@
 // Wave-level row tiles for the vectorised quantized GEMV paths.
 //
-// A wave computes dot products of up to RI*RPW weight rows with activation
-// vectors held in registers.  Lane layout:  lane = q*LPR + j, where LPR
-// ("lanes per row", a power of two <= 64) lanes cover one row and RPW =
-// 64/LPR rows run side by side.  Lane j of a row owns the 16-byte chunks
-// c = j + t*LPR (t < CPL) of that row, and the activations of those chunks.
+// A wave computes dot products of RI*RPW weight rows with activation vectors
+// held in registers.  Lane layout:  lane = q*LPR + j, where LPR ("lanes per
+// row", a power of two <= 64) lanes cover one row and RPW = 64/LPR rows run
+// side by side.  Lane j owns the CPL 16-byte chunks c = j + t*LPR (t < CPL)
+// of its row and the activations of those chunks, so each load instruction
+// reads LPR consecutive chunks per row.  RI = 4/CPL passes, so every lane
+// holds four 16-byte code chunks per tile.
 //
-// Loads are branch-free: row and chunk indices are clamped to valid ones
-// (the caller drops results of rows past the end; chunks past a row's end
-// get zero scale and bias), and scales are kept as raw bits until every load
-// of the tile is in flight.  A conversion or a branch between two loads
-// would make the compiler wait for the first before issuing the second.
+// Two activation formats:
+//   kXF32   fp32 registers; codes go through v_cvt_f32_ubyteN and an fma.
+//   kXBF16  (4-bit codes, bf16 activations) packed bf16 pairs; each nibble
+//           becomes the bf16 value 128+q with one and-or, and v_dot2c_f32_bf16
+//           accumulates two exact products into fp32.  The 128 offset is
+//           removed through the bias: s*q + b = s*(128+q) + (b - 128*s).
+//
+// Loads are branch-free: row and chunk indices are clamped to valid ones (the
+// caller drops results of rows past the end; chunks past a row's end get zero
+// scale and bias), and scales stay raw bits until every load of the tile is
+// in flight.  A conversion or a branch between two loads would make the
+// compiler wait for the first before issuing the second.
 #pragma once
 
 #include "common.hpp"
 
 namespace swq {
+
+constexpr int kXF32 = 0;
+constexpr int kXBF16 = 1;
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 
 struct LaneMap {
     int lpr;     // lanes per row
@@ -35,39 +49,121 @@ __device__ __forceinline__ LaneMap lane_map(int lpr_log2, int lane) {
     return m;
 }
 
-// Activations of this lane's chunks (fp32 registers) plus their sums.
+// ---------------------------------------------------------------------------
+// reductions over the LPR lanes of a row (DPP; the segment's last lane
+// always holds the full sum, and for LPR <= 16 every lane does)
+
+template <int CTRL, int ROW_MASK, bool BOUND_CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, BOUND_CTRL));
+}
+
+__device__ __forceinline__ float segment_reduce(float v, int lpr_log2) {
+    if (lpr_log2 >= 1) v += dpp<0xB1, 0xF, true>(v);    // quad_perm [1,0,3,2]
+    if (lpr_log2 >= 2) v += dpp<0x4E, 0xF, true>(v);    // quad_perm [2,3,0,1]
+    if (lpr_log2 >= 3) v += dpp<0x141, 0xF, true>(v);   // row_half_mirror
+    if (lpr_log2 >= 4) v += dpp<0x140, 0xF, true>(v);   // row_mirror
+    if (lpr_log2 >= 5) v += dpp<0x142, 0xA, false>(v);  // row_bcast:15 into rows 1, 3
+    if (lpr_log2 >= 6) v += dpp<0x143, 0x8, false>(v);  // row_bcast:31 into row 3
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// activations
+
+template <int BITS, int CPL, int XF>
+struct XSlice;
+
 template <int BITS, int CPL>
-struct XSlice {
+struct XSlice<BITS, CPL, kXF32> {
     static constexpr int kCPC = codes_per_chunk<BITS>();
     float v[CPL][kCPC];
     float sum[CPL];
 };
 
-template <int XDT, int BITS, int CPL>
-__device__ __forceinline__ void load_xslice(XSlice<BITS, CPL> &xs, const QMat &m, const LaneMap &lm,
+template <int CPL>
+struct XSlice<4, CPL, kXBF16> {
+    uint32_t p[CPL][16];  // pairs {x[8k+m], x[8k+m+4]} for word k, m = 0..3
+    float sum[CPL];
+};
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                           false);
+}
+
+template <int XDT, int BITS, int CPL, int XF>
+__device__ __forceinline__ void load_xslice(XSlice<BITS, CPL, XF> &xs, const QMat &m, const LaneMap &lm,
                                             const void *x, int64_t x_base) {
     constexpr int kCPC = codes_per_chunk<BITS>();
+    if constexpr (XF == kXF32) {
 #pragma unroll
-    for (int t = 0; t < CPL; ++t) {
-        const int c = min(lm.j + t * lm.lpr, m.chunks - 1);
-        load_x<XDT>(xs.v[t], x, x_base + static_cast<int64_t>(c) * kCPC);
-    }
+        for (int t = 0; t < CPL; ++t) {
+            const int c = min(lm.j + t * lm.lpr, m.chunks - 1);
+            load_x<XDT>(xs.v[t], x, x_base + static_cast<int64_t>(c) * kCPC);
+        }
 #pragma unroll
-    for (int t = 0; t < CPL; ++t) {
-        float s = 0.f;
+        for (int t = 0; t < CPL; ++t) {
+            float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < kCPC; ++i) s += xs.v[t][i];
-        xs.sum[t] = s;
+            for (int i = 0; i < kCPC; ++i) s += xs.v[t][i];
+            xs.sum[t] = s;
+        }
+    } else {
+        static_assert(XDT == 2 && BITS == 4, "packed bf16 activations need bf16 x and 4-bit codes");
+        const uint16_t *xp = static_cast<const uint16_t *>(x) + x_base;
+        uint4 raw[CPL][4];
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) {
+            const int c = min(lm.j + t * lm.lpr, m.chunks - 1);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                raw[t][k] = *reinterpret_cast<const uint4 *>(xp + static_cast<int64_t>(c) * 32 + k * 8);
+        }
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) {
+            float s[4] = {0.f, 0.f, 0.f, 0.f};  // independent chains
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t d0 = raw[t][k].x, d1 = raw[t][k].y, d2 = raw[t][k].z, d3 = raw[t][k].w;
+                xs.p[t][4 * k + 0] = (d0 & 0xFFFFu) | (d2 << 16);
+                xs.p[t][4 * k + 1] = (d0 >> 16) | (d2 & 0xFFFF0000u);
+                xs.p[t][4 * k + 2] = (d1 & 0xFFFFu) | (d3 << 16);
+                xs.p[t][4 * k + 3] = (d1 >> 16) | (d3 & 0xFFFF0000u);
+#pragma unroll
+                for (int mm = 0; mm < 4; ++mm) s[mm] = dot2_bf16(xs.p[t][4 * k + mm], 0x3F803F80u, s[mm]);
+            }
+            xs.sum[t] = (s[0] + s[1]) + (s[2] + s[3]);
+        }
     }
 }
 
+// sum_i (128 + q_i) * x_i over a chunk of 4-bit codes with packed bf16 pairs.
+__device__ __forceinline__ float dot_chunk_q4_bf16(const uint4 w, const uint32_t *xp) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    float a0 = 0.f, a1 = 0.f;  // two independent chains
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t v = ws[k];
+        a0 = dot2_bf16((v & 0x000F000Fu) | 0x43004300u, xp[4 * k + 0], a0);          // {q0, q4}
+        a1 = dot2_bf16(((v >> 4) & 0x000F000Fu) | 0x43004300u, xp[4 * k + 1], a1);   // {q1, q5}
+        a0 = dot2_bf16(((v >> 8) & 0x000F000Fu) | 0x43004300u, xp[4 * k + 2], a0);   // {q2, q6}
+        a1 = dot2_bf16(((v >> 12) & 0x000F000Fu) | 0x43004300u, xp[4 * k + 3], a1);  // {q3, q7}
+    }
+    return a0 + a1;
+}
+
+// ---------------------------------------------------------------------------
+// weights
+
 // Codes plus raw scale/bias bits of RI passes of rows (row0 + i*rpw + q).
 // ES is the byte size of a scale element: 2 (f16, bf16) or 4 (f32).
-template <int BITS, int CPL, int RI, int ES>
+template <int BITS, int CPL, int ES>
 struct RowTile {
-    uint4 w[RI][CPL];
-    uint32_t s[RI][CPL];
-    uint32_t b[RI][CPL];
+    static constexpr int kRI = 4 / CPL;
+    uint4 w[kRI][CPL];
+    uint32_t s[kRI][CPL];
+    uint32_t b[kRI][CPL];
 };
 
 template <int ES>
@@ -87,9 +183,10 @@ __device__ __forceinline__ float scale_value(uint32_t raw, int stype) {
     }
 }
 
-template <int BITS, int CPL, int RI, int ES>
-__device__ __forceinline__ void load_tile(RowTile<BITS, CPL, RI, ES> &rt, const QMat &m, int64_t expert,
+template <int BITS, int CPL, int ES>
+__device__ __forceinline__ void load_tile(RowTile<BITS, CPL, ES> &rt, const QMat &m, int64_t expert,
                                           const LaneMap &lm, int row0, int row_end) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
     const uint8_t *wbase = m.w + expert * m.stride_w;
     const uint8_t *sbase = m.s + expert * m.stride_sb;
     const uint8_t *bbase = m.b + expert * m.stride_sb;
@@ -113,15 +210,16 @@ __device__ __forceinline__ void load_tile(RowTile<BITS, CPL, RI, ES> &rt, const 
     }
 }
 
-// res[i] = full dot product of row (row0 + i*rpw + q) with the activations;
-// every lane of the row's segment receives it.
+// res[i] = full dot product of row (row0 + i*rpw + q) with the activations,
+// valid in the row segment's last lane (j == LPR-1).
 //
 // The empty asm keeps the code unpacking inside the caller's token loop:
-// hoisted out of it, the unpacked codes of a tile (32 floats per chunk)
-// would stay live across the loop and spill.
-template <int BITS, int CPL, int RI, int ES>
-__device__ __forceinline__ void dot_tile(float (&res)[RI], const RowTile<BITS, CPL, RI, ES> &rt,
-                                         const XSlice<BITS, CPL> &xs, const QMat &m, const LaneMap &lm) {
+// hoisted out of it, the unpacked codes of a tile would stay live across the
+// loop and spill.
+template <int BITS, int CPL, int ES, int XF>
+__device__ __forceinline__ void dot_tile(float (&res)[4 / CPL], const RowTile<BITS, CPL, ES> &rt,
+                                         const XSlice<BITS, CPL, XF> &xs, const QMat &m, const LaneMap &lm) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
 #pragma unroll
     for (int i = 0; i < RI; ++i) {
         float acc = 0.f;
@@ -132,14 +230,20 @@ __device__ __forceinline__ void dot_tile(float (&res)[RI], const RowTile<BITS, C
             const bool live = lm.j + t * lm.lpr < m.chunks;
             const float sc = live ? scale_value<ES>(rt.s[i][t], m.stype) : 0.f;
             const float bi = live ? scale_value<ES>(rt.b[i][t], m.stype) : 0.f;
-            const float qd = dot_chunk<BITS>(w, xs.v[t]);
-            acc = fmaf(sc, qd, acc);
-            acc = fmaf(bi, xs.sum[t], acc);
+            if constexpr (XF == kXF32) {
+                const float qd = dot_chunk<BITS>(w, xs.v[t]);
+                acc = fmaf(sc, qd, acc);
+                acc = fmaf(bi, xs.sum[t], acc);
+            } else {
+                const float d = dot_chunk_q4_bf16(w, xs.p[t]);
+                acc = fmaf(sc, d, acc);
+                acc = fmaf(fmaf(-128.f, sc, bi), xs.sum[t], acc);
+            }
         }
         res[i] = acc;
     }
 #pragma unroll
-    for (int i = 0; i < RI; ++i) res[i] = segment_sum(res[i], lm.lpr);
+    for (int i = 0; i < RI; ++i) res[i] = segment_reduce(res[i], lm.lpr_log2);
 }
 
 }  // namespace swq
