@@ -30,6 +30,15 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 
+# HBM bytes per launch from two rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE),
+# each scaled by what the counter reads for a 256 MiB device copy (FETCH x 2.0, WRITE x 1.0);
+# commands and raw figures in profiles/<kernel>_<workload>.md.  Keyed (workload, kernel).
+MEASURED_TRAFFIC = {
+    ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_692_148,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 14_590_849,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 5_743_112,
+}
+
 CONFIGS = {
     # name: (shape key, batch)
     "qwen3.6-35b-a3b-q4-b1": ("qwen3.6-35b-a3b-q4", 1),
@@ -49,6 +58,9 @@ def parse():
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="first run three plain device-to-device copies of MIB MiB, a kernel of known "
+                         "traffic that scales the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -87,6 +99,15 @@ def main():
     torch.cuda.init()
     stream = torch.cuda.current_stream()
     sh = ctypes.c_void_p(stream.cuda_stream)
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     # ---- resident weights: R distinct layers, all experts --------------
     layers = [moe.synth_layer(shape, args.seed, r, dev) for r in range(R)]
@@ -182,6 +203,7 @@ def main():
     step_bytes = shape.decode_bytes(mean_uniq, batch)
     dom = int(np.argmax(stage_us))
     achieved = stage_bytes[dom] / (stage_us[dom] * 1e-6) / 1e9
+    dom_kernel = ["moe_stage1", "moe_stage2", "moe_stage3"][dom]
 
     result = {
         "metric": "us per MoE-layer decode step; achieved HBM GB/s as fraction of peak (1 GPU)",
@@ -200,9 +222,10 @@ def main():
                    "moe_intermediate": I, "shared_intermediate": Is, "expert_bits": eb,
                    "router_bits": rb, "group": shape.group, "batch": batch, "replicas": R,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": ["moe_stage1", "moe_stage2", "moe_stage3"][dom],
+        "roofline": {"bound": "hbm", "kernel": dom_kernel,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": MEASURED_TRAFFIC.get((args.config, dom_kernel)),
                      "algorithmic_bytes_per_launch": int(stage_bytes[dom]),
                      "avg_launch_us": round(stage_us[dom], 3)},
         "stage_us": [round(v, 3) for v in stage_us],
