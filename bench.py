@@ -32,7 +32,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 
 # HBM bytes per launch from two rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE),
 # each scaled by what the counter reads for a 256 MiB device copy (FETCH x 2.0, WRITE x 1.0);
-# commands and raw figures in profiles/<kernel>_<workload>.md.  Keyed (workload, kernel).
+# the runs' commands and raw counts are kept with the kernel-trace summaries.  Keyed (workload, kernel).
 MEASURED_TRAFFIC = {
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_692_148,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 14_590_849,
@@ -80,7 +80,7 @@ def main():
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
               "The MoE decode step would shard by experts across GPUs with one all-reduce of the "
-              "[batch, hidden] output; see DESIGN.md.", file=sys.stderr)
+              "[batch, hidden] output.", file=sys.stderr)
         sys.exit(2)
 
     import torch
