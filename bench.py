@@ -8,9 +8,11 @@ weighted combine) for one batch of synthetic tokens, on weights resident in
 HBM.  The K timed steps cycle through `--replicas` distinct seeded layers
 (each with all E experts) and distinct inputs, so the bytes a step touches
 come from HBM, not from the 256 MB last-level cache.  The steps are
-captured in one HIP graph and replayed; the per-kernel durations come from
-graph replays of each stage on its own, timed with HIP events.  Prints one
-JSON line.
+captured in one HIP graph and replayed.  A batch-1 step is one kernel (the
+single-launch path), so the graph's average step is that kernel's average
+launch; for batches (three launches) the per-kernel durations come from graph
+replays of each stage on its own, timed with HIP events.  Prints one JSON
+line.
 """
 
 from __future__ import annotations
@@ -58,6 +60,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--path", default="auto", choices=("auto", "fused", "staged"),
+                    help="auto: the single launch for batch 1, the three launches otherwise")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run three plain device-to-device copies of MIB MiB, a kernel of known "
                          "traffic that scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -93,6 +97,8 @@ def main():
     lib = _lib.load()
 
     shape_key, batch = CONFIGS[args.config]
+    path = args.path if args.path != "auto" else ("fused" if batch == 1 else "staged")
+    MASK = _lib.SWQ_STAGES_FUSED if path == "fused" else 7
     shape = synth.SHAPES[shape_key]
     R = args.replicas
     dev = "cuda"
@@ -126,7 +132,7 @@ def main():
                       ctypes.c_void_p(outs[r].data_ptr()), _lib.SWQ_BF16, ctypes.c_void_p(ids[r].data_ptr()),
                       ctypes.c_void_p(wts[r].data_ptr()), ctypes.c_void_p(wss[r].data_ptr()), wss[r].numel(), 0))
 
-    def step(i, mask=7):
+    def step(i, mask=MASK):
         c = calls[i % R]
         check(lib.swq_moe_decode_stages(*c, mask, sh), "moe_decode")
 
@@ -140,7 +146,7 @@ def main():
         cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         for i in range(K):
             c = calls[i % R]
-            check(lib.swq_moe_decode_stages(*c, 7, cap), "moe_decode (capture)")
+            check(lib.swq_moe_decode_stages(*c, MASK, cap), "moe_decode (capture)")
     torch.cuda.synchronize()
     for _ in range(max(1, (W + K - 1) // K)):
         graph.replay()
@@ -154,28 +160,32 @@ def main():
     graph_ms = e0.elapsed_time(e1)
     us_per_step = graph_ms * 1000.0 / K
 
-    # ---- per-kernel durations: graphs of single-stage steps --------------
-    # Each replica's workspace already holds its routing from the replays
-    # above, so a stage on its own reads valid inputs.  The graph's launches
-    # run back to back; HIP events around one replay give the average launch.
+    # ---- per-kernel durations ------------------------------------------------
+    # fused: one kernel per step, so the graph's average step is its average
+    # launch.  staged: graphs of single-stage steps (each replica's workspace
+    # already holds its routing from the replays above, so a stage on its own
+    # reads valid inputs); HIP events around one replay give the average launch.
     n_st = min(K, 4 * R)
-    stage_us = []
-    for mask in (1, 2, 4):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-            for i in range(n_st):
-                c = calls[i % R]
-                check(lib.swq_moe_decode_stages(*c, mask, cap), "moe_decode stage (capture)")
-        g.replay()
-        torch.cuda.synchronize()
-        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a0.record()
-        g.replay()
-        a1.record()
-        torch.cuda.synchronize()
-        stage_us.append(a0.elapsed_time(a1) * 1000.0 / n_st)
-        del g
+    if path == "fused":
+        stage_us = [us_per_step]
+    else:
+        stage_us = []
+        for mask in (1, 2, 4):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+                for i in range(n_st):
+                    c = calls[i % R]
+                    check(lib.swq_moe_decode_stages(*c, mask, cap), "moe_decode stage (capture)")
+            g.replay()
+            torch.cuda.synchronize()
+            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a0.record()
+            g.replay()
+            a1.record()
+            torch.cuda.synchronize()
+            stage_us.append(a0.elapsed_time(a1) * 1000.0 / n_st)
+            del g
     # eager (no graph) launches of whole steps, for reference
     check(lib.swq_bench_stall(20000, sh), "stall")
     t_eager0 = torch.cuda.Event(enable_timing=True)
@@ -195,15 +205,20 @@ def main():
     mb = shape.matrix_bytes
     eb, rb = shape.expert_bits, shape.router_bits
     xb = batch * H * 2
-    stage_bytes = [
-        mb(E, H, rb) + mb(1, H, rb) + 2 * mb(Is, H, eb) + xb,    # router + shared gate + shared gate/up
-        mean_uniq * 2 * mb(I, H, eb) + xb,                       # routed gate/up
-        mean_uniq * mb(H, I, eb) + mb(H, Is, eb) + xb,           # routed + shared down, bf16 out
-    ]
     step_bytes = shape.decode_bytes(mean_uniq, batch)
+    if path == "fused":
+        stage_bytes = [step_bytes]
+        kernels = ["moe_fused"]
+    else:
+        stage_bytes = [
+            mb(E, H, rb) + mb(1, H, rb) + 2 * mb(Is, H, eb) + xb,    # router + shared gate + shared gate/up
+            mean_uniq * 2 * mb(I, H, eb) + xb,                       # routed gate/up
+            mean_uniq * mb(H, I, eb) + mb(H, Is, eb) + xb,           # routed + shared down, bf16 out
+        ]
+        kernels = ["moe_stage1", "moe_stage2", "moe_stage3"]
     dom = int(np.argmax(stage_us))
     achieved = stage_bytes[dom] / (stage_us[dom] * 1e-6) / 1e9
-    dom_kernel = ["moe_stage1", "moe_stage2", "moe_stage3"][dom]
+    dom_kernel = kernels[dom]
 
     result = {
         "metric": "us per MoE-layer decode step; achieved HBM GB/s as fraction of peak (1 GPU)",
@@ -228,8 +243,9 @@ def main():
                      "traffic": MEASURED_TRAFFIC.get((args.config, dom_kernel)),
                      "algorithmic_bytes_per_launch": int(stage_bytes[dom]),
                      "avg_launch_us": round(stage_us[dom], 3)},
-        "stage_us": [round(v, 3) for v in stage_us],
-        "stage_bytes": [int(v) for v in stage_bytes],
+        "path": path,
+        "kernel_us": dict(zip(kernels, [round(v, 3) for v in stage_us])),
+        "kernel_bytes": dict(zip(kernels, [int(v) for v in stage_bytes])),
         "step_bytes": int(step_bytes),
         "step_gbs_wall": round(step_bytes / (us_per_step * 1e-6) / 1e9, 1),
         "step_gbs_kernels": round(step_bytes / (sum(stage_us) * 1e-6) / 1e9, 1),

@@ -36,12 +36,21 @@ int swq_synth_u32(uint32_t *dst, int64_t count, uint64_t seed, uint64_t stream, 
 int swq_synth_scales(uint16_t *scales, uint16_t *biases, int64_t count, int bits, uint64_t seed,
                      uint64_t stream, int64_t start, void *hip_stream);
 
-/* swq_moe_decode restricted to the stages in stage_mask (bit 0: router /
- * top-k / shared gate-up, bit 1: routed gate-up, bit 2: down + combine).
- * A stage reads what the earlier stages left in the workspace. */
+/* swq_moe_decode on a chosen path.  stage_mask bits 0-2 run stages of the
+ * three-launch path (bit 0: router + shared gate/up + shared-expert gate,
+ * bit 1: top-k + routed gate/up, bit 2: down + combine); a stage reads what
+ * the earlier stages left in the workspace.  SWQ_STAGES_FUSED runs the
+ * single-launch path, or returns SWQ_ERR_LIMIT when the layer, the batch or
+ * the device cannot take it. */
+enum { SWQ_STAGES_FUSED = 8 };
+
 int swq_moe_decode_stages(const swq_moe_layer *layer, const void *x, int x_dtype, int batch, void *out,
                           int out_dtype, int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes,
                           int flags, int stage_mask, void *stream);
+
+/* Byte offset in the workspace of a 32-bit word that the single-launch path
+ * sets nonzero if one of its bounded waits ran out (0 on bad input). */
+size_t swq_moe_workspace_error_offset(const swq_moe_layer *layer, int batch);
 
 /* One single-wave kernel that sleeps `iterations` times (s_sleep 127, about
  * 8k cycles each) and exits; iterations <= 1000000. */

@@ -25,6 +25,7 @@ SWQ_ERR_LIMIT = -10
 SWQ_F32, SWQ_F16, SWQ_BF16 = 0, 1, 2
 SWQ_MAX_BATCH, SWQ_MAX_TOPK = 16, 16
 SWQ_MOE_ACCUMULATE = 1
+SWQ_STAGES_FUSED = 8  # swq_bench.h: the single-launch path
 
 
 class SwqError(RuntimeError):
@@ -82,6 +83,7 @@ SIGNATURES = {
     "swq_synth_scales": (_I, [_P, _P, _I64, _I, _U64, _U64, _I64, _P]),
     "swq_moe_decode_stages": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _I, _I, _P]),
     "swq_bench_stall": (_I, [_I, _P]),
+    "swq_moe_workspace_error_offset": (_SZ, [_c.POINTER(MoELayer), _I]),
 }
 
 _lib = None

@@ -68,13 +68,13 @@ inline int lpr_log2_for(int chunks, int cpl) {
 }
 
 // Activation format and chunks per lane for a matrix read with x of dtype
-// x_dtype: 4-bit codes with bf16 x take packed-bf16 dot products over 4
-// chunks per lane; everything else fp32 fmas over one chunk per lane (two
+// x_dtype: 4-bit codes with bf16 x take packed-bf16 dot products over 2
+// chunks per lane (rows up to 4096 inputs); everything else fp32 fmas over one chunk per lane (two
 // for 8-bit rows wider than 1024).
 inline void plan_qmat(QMat *m, int x_dtype) {
     if (m->bits == 4 && x_dtype == SWQ_BF16) {
         m->xf = 1;
-        m->cpl = 4;
+        m->cpl = 2;
     } else {
         m->xf = 0;
         m->cpl = m->chunks > 64 ? 2 : 1;
@@ -84,7 +84,7 @@ inline void plan_qmat(QMat *m, int x_dtype) {
 
 // Largest row (in 16-byte chunks) each plan accepts.
 inline bool plan_fits(const QMat &m) {
-    if (m.xf == 1) return m.chunks <= 4 * kWave;
+    if (m.xf == 1) return m.chunks <= 2 * kWave;
     return m.chunks <= m.cpl * kWave && (m.bits == 8 || m.cpl == 1);
 }
 

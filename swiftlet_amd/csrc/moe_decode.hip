@@ -17,13 +17,14 @@
 // never leave the device.
 #include "../../include/swq_bench.h"
 #include "internal.hpp"
+#include "moe_host.hpp"
+#include "route.hpp"
 #include "tile.hpp"
 
 namespace swq {
 
 constexpr int kThreads12 = 256;
 constexpr int kMaxPairs = SWQ_MAX_BATCH * SWQ_MAX_TOPK;
-constexpr int kMaxExperts = 1024;
 constexpr int kRows3 = 16;  // stage-3 rows per workgroup (upper bound)
 
 struct MoEArgs {
@@ -55,7 +56,7 @@ struct MoEArgs {
 #define SWQ_DISPATCH_ES(XDT, m, FN, ES, ...)                                \
     do {                                                                    \
         if constexpr (XDT == SWQ_BF16) {                                    \
-            if ((m).bits == 4) FN<XDT, 4, 4, ES, kXBF16>(__VA_ARGS__);      \
+            if ((m).bits == 4) FN<XDT, 4, 2, ES, kXBF16>(__VA_ARGS__);      \
             else if ((m).cpl == 1) FN<XDT, 8, 1, ES, kXF32>(__VA_ARGS__);   \
             else FN<XDT, 8, 2, ES, kXF32>(__VA_ARGS__);                     \
         } else {                                                            \
@@ -82,9 +83,6 @@ struct MoEArgs {
             else FN<SWQ_F32, 8, 1, 2, kXF32>(__VA_ARGS__);                  \
         }                                                                   \
     } while (0)
-
-// Rows one wave covers in one tile: 4/CPL passes of 64/LPR rows.
-__host__ __device__ __forceinline__ int tile_rows(const QMat &m) { return (4 / m.cpl) * (kWave >> m.lpr_log2); }
 
 // One tile of rows of one matrix against every token's x; the result of
 // (token b, row) goes to out[b*ld + row].
@@ -227,40 +225,6 @@ __device__ __forceinline__ void down_rows_b1(const QMat &m, const int32_t *ids, 
 
 // ---------------------------------------------------------------------------
 // top-k (one wave per token)
-
-__device__ __forceinline__ uint32_t orderable(float f) {
-    const uint32_t u = __float_as_uint(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ float from_orderable(uint32_t k) {
-    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
-}
-
-// Wave-wide maximum: DPP within each 16-lane row, then the four row maxima
-// through scalar registers.  Every lane receives it.
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, true));
-}
-
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
-    v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
-    v = max(v, dpp_u32<0x141>(v));  // row_half_mirror
-    v = max(v, dpp_u32<0x140>(v));  // row_mirror
-    const uint32_t r0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 0));
-    const uint32_t r1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 16));
-    const uint32_t r2 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 32));
-    const uint32_t r3 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 48));
-    return max(max(r0, r1), max(r2, r3));
-}
-
-// Sum over the wave, returned to every lane (the last lane of the DPP scan
-// holds it; readlane broadcasts).
-__device__ __forceinline__ float wave_sum_all(float v) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(segment_reduce(v, 6)), 63));
-}
 
 // Top-k of one token's router logits, one wave.  Selection by logit with
 // ties to the lower expert id equals the reference's selection by softmax
@@ -559,98 +523,31 @@ __global__ __launch_bounds__(kStage3MaxWaves * 64) void moe_stage3(MoEArgs a) {
 // ---------------------------------------------------------------------------
 // host side
 
-struct WsLayout {
-    size_t header, logits, sg, h_sh, ids, wts, n_unique, uniq_e, uniq_np, uniq_pairs, h, total;
-};
-
-static size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
-
-static WsLayout ws_layout(const swq_moe_layer *l, int B) {
-    WsLayout w{};
-    size_t off = 0;
-    auto take = [&](size_t n) {
-        const size_t o = off;
-        off = align256(off + n);
-        return o;
-    };
-    const size_t P = static_cast<size_t>(B) * l->top_k;
-    w.header = take(256);  // reserved; zeroed by swq_moe_workspace_init
-    w.logits = take(static_cast<size_t>(B) * l->num_experts * 4);
-    w.sg = take(static_cast<size_t>(B) * 4);
-    w.h_sh = take(static_cast<size_t>(B) * (l->has_shared ? l->shared_intermediate : 1) * 4);
-    w.ids = take(P * 4);
-    w.wts = take(P * 4);
-    w.n_unique = take(4);
-    w.uniq_e = take(P * 4);
-    w.uniq_np = take(P * 4);
-    w.uniq_pairs = take(P * B * 4);
-    w.h = take(P * l->moe_intermediate * 4);
-    w.total = off;
-    return w;
-}
-
-// A matrix of the layer: shape, format and alignment, and whether its plan
-// fits the compiled kernels when read with activations of dtype x_dtype
-// (reads_h: the fp32 SwiGLU activations of stage 3).
-static int check_vec(const swq_qlinear *l, int out_dim, int in_dim, bool stacked, int E, int x_dtype,
-                     bool reads_h) {
-    int st = check_linear_shape(l);
-    if (st != SWQ_OK) return st;
-    if (l->out_dim != out_dim || l->in_dim != in_dim) return SWQ_ERR_BAD_SHAPE;
-    if (l->bits != 4 && l->bits != 8) return SWQ_ERR_UNSUPPORTED_BITS;
-    if ((static_cast<int64_t>(in_dim) * l->bits) % 128 != 0) return SWQ_ERR_BAD_SHAPE;
-    if ((static_cast<int64_t>(l->group_size) * l->bits) % 128 != 0) return SWQ_ERR_BAD_SHAPE;
-    if (!vector_path_ok(l, 0, 0, 0)) return SWQ_ERR_MISALIGNED;
-    QMat m = make_qmat(l);
-    plan_qmat(&m, reads_h ? SWQ_F32 : x_dtype);
-    if (!plan_fits(m) || (reads_h && m.cpl != 1)) return SWQ_ERR_LIMIT;
-    if (stacked && E > 1 && (l->expert_stride_w == 0 || l->expert_stride_sb == 0)) return SWQ_ERR_INVALID_ARGUMENT;
-    return SWQ_OK;
-}
-
-static int check_layer(const swq_moe_layer *l, int B, int x_dtype) {
-    if (!l) return SWQ_ERR_INVALID_ARGUMENT;
-    if (l->reserved != 0) return SWQ_ERR_INVALID_ARGUMENT;
-    if (B <= 0 || l->hidden <= 0 || l->num_experts <= 0 || l->moe_intermediate <= 0) return SWQ_ERR_INVALID_ARGUMENT;
-    if (l->top_k <= 0 || l->top_k > l->num_experts) return SWQ_ERR_EXPERT_RANGE;
-    if (l->top_k > SWQ_MAX_TOPK || B > SWQ_MAX_BATCH || l->num_experts > kMaxExperts) return SWQ_ERR_LIMIT;
-    const int H = l->hidden, E = l->num_experts, I = l->moe_intermediate;
-    const int xd = x_dtype;
-    int st;
-    if ((st = check_vec(&l->router, E, H, false, E, xd, false)) != SWQ_OK) return st;
-    if ((st = check_vec(&l->gate, I, H, true, E, xd, false)) != SWQ_OK) return st;
-    if ((st = check_vec(&l->up, I, H, true, E, xd, false)) != SWQ_OK) return st;
-    if ((st = check_vec(&l->down, H, I, true, E, xd, true)) != SWQ_OK) return st;
-    if (l->gate.bits != l->up.bits || l->gate.in_dim != l->up.in_dim) return SWQ_ERR_BAD_SHAPE;
-    if (l->has_shared) {
-        const int Is = l->shared_intermediate;
-        if (Is <= 0) return SWQ_ERR_INVALID_ARGUMENT;
-        if ((st = check_vec(&l->shared_gate, Is, H, false, 1, xd, false)) != SWQ_OK) return st;
-        if ((st = check_vec(&l->shared_up, Is, H, false, 1, xd, false)) != SWQ_OK) return st;
-        if ((st = check_vec(&l->shared_down, H, Is, false, 1, xd, true)) != SWQ_OK) return st;
-        if ((st = check_vec(&l->shared_expert_gate, 1, H, false, 1, xd, false)) != SWQ_OK) return st;
-        if (l->shared_gate.bits != l->shared_up.bits) return SWQ_ERR_BAD_SHAPE;
-    }
-    return SWQ_OK;
-}
-
 }  // namespace swq
 
 using namespace swq;
 
 extern "C" size_t swq_moe_decode_workspace_bytes(const swq_moe_layer *layer, int batch) {
     if (check_layer(layer, batch, SWQ_BF16) != SWQ_OK) return 0;
-    return ws_layout(layer, batch).total;
+    return fused_ws_bytes(layer, ws_layout(layer, batch).total);
 }
 
 extern "C" int swq_moe_workspace_init(void *ws, size_t ws_bytes, void *stream) {
     if (!ws || ws_bytes < 256) return SWQ_ERR_WORKSPACE;
-    return hip_status(hipMemsetAsync(ws, 0, 256, static_cast<hipStream_t>(stream)));
+    return hip_status(hipMemsetAsync(ws, 0, ws_bytes, static_cast<hipStream_t>(stream)));
 }
 
-extern "C" int swq_moe_decode_stages(const swq_moe_layer *layer, const void *x, int x_dtype, int batch,
-                                     void *out, int out_dtype, int32_t *topk_ids, float *topk_weights, void *ws,
-                                     size_t ws_bytes, int flags, int stage_mask, void *stream) {
+extern "C" size_t swq_moe_workspace_error_offset(const swq_moe_layer *layer, int batch) {
+    if (check_layer(layer, batch, SWQ_BF16) != SWQ_OK) return 0;
+    return fused_err_offset(layer, ws_layout(layer, batch).total);
+}
+
+// stage_mask: bits 0-2 run the staged kernels' stages; SWQ_STAGES_FUSED
+// runs the single-launch path (SWQ_ERR_LIMIT when this layer, batch or device
+// cannot); 0 picks the single launch when possible, else the three stages.
+static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int batch, void *out,
+                           int out_dtype, int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes,
+                           int flags, int stage_mask, void *stream) {
     if (x_dtype != SWQ_F32 && x_dtype != SWQ_BF16) return SWQ_ERR_UNSUPPORTED_DTYPE;
     int st = check_layer(layer, batch, x_dtype);
     if (st != SWQ_OK) return st;
@@ -724,8 +621,16 @@ extern "C" int swq_moe_decode_stages(const swq_moe_layer *layer, const void *x, 
     }
     a.rows3 = min(kRows3, tile_rows(a.down));
 
-    if (stage_mask & ~7) return SWQ_ERR_INVALID_ARGUMENT;
+    if (stage_mask != SWQ_STAGES_FUSED && (stage_mask & ~7)) return SWQ_ERR_INVALID_ARGUMENT;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (stage_mask == 0 || stage_mask == SWQ_STAGES_FUSED) {
+        bool taken = false;
+        st = fused_decode(layer, x, x_dtype, batch, out, out_dtype, topk_ids, topk_weights, ws, ws_bytes, wl.total,
+                          accumulate, s, &taken);
+        if (st != SWQ_OK || taken) return st;
+        if (stage_mask == SWQ_STAGES_FUSED) return SWQ_ERR_LIMIT;
+        stage_mask = 7;
+    }
     if (stage_mask & 1) {
         if (x_dtype == SWQ_BF16) hipLaunchKernelGGL(moe_stage1<SWQ_BF16>, dim3(a.nr_blocks + shared_blocks), dim3(kThreads12), 0, s, a);
         else hipLaunchKernelGGL(moe_stage1<SWQ_F32>, dim3(a.nr_blocks + shared_blocks), dim3(kThreads12), 0, s, a);
@@ -749,9 +654,17 @@ extern "C" int swq_moe_decode_stages(const swq_moe_layer *layer, const void *x, 
     return SWQ_OK;
 }
 
+extern "C" int swq_moe_decode_stages(const swq_moe_layer *layer, const void *x, int x_dtype, int batch,
+                                     void *out, int out_dtype, int32_t *topk_ids, float *topk_weights, void *ws,
+                                     size_t ws_bytes, int flags, int stage_mask, void *stream) {
+    if (stage_mask == 0) return SWQ_ERR_INVALID_ARGUMENT;
+    return moe_decode_impl(layer, x, x_dtype, batch, out, out_dtype, topk_ids, topk_weights, ws, ws_bytes, flags,
+                           stage_mask, stream);
+}
+
 extern "C" int swq_moe_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int batch, void *out,
                               int out_dtype, int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes,
                               int flags, void *stream) {
-    return swq_moe_decode_stages(layer, x, x_dtype, batch, out, out_dtype, topk_ids, topk_weights, ws, ws_bytes,
-                                 flags, 7, stream);
+    return moe_decode_impl(layer, x, x_dtype, batch, out, out_dtype, topk_ids, topk_weights, ws, ws_bytes, flags, 0,
+                           stream);
 }

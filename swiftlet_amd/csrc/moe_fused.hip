@@ -1,0 +1,747 @@
+// MoE-layer decode step for one token in a single launch on gfx950.
+//
+// One workgroup per CU, launched as an ordinary kernel: on a device with no other work every
+// workgroup is resident at once.  (A cooperative launch would guarantee
+// that, but costs ~18 us more per launch on this device, in graphs too.)
+// If other work delays some workgroups, the waits below only last longer;
+// no workgroup waits on a later one's launch.  The stages hand data to each
+// other through the workspace instead of through kernel boundaries: every value crossing workgroups is stored together with
+// the call's epoch as one 8-byte word, written and read with agent-coherent
+// (relaxed, device-scope) atomics, so a consumer polls the data itself and
+// needs no separate flag, no cache write-back and no fence.  Each XCD has its
+// own L2; device-scope accesses are coherent across them.
+//
+//   phase 1  router rows -> logits (written to one replica per XCD, so the
+//            pollers spread over separate lines); shared-expert gate/up rows
+//            -> SwiGLU activations; shared-expert gate logit (every workgroup,
+//            for its own combine); waves whose down tile belongs to the shared
+//            expert load that tile now.
+//   routing  wave 0 of every workgroup polls its replica of the logits and
+//            runs softmax / top-k / renormalisation itself.
+//   phase 2  routed gate/up rows -> SwiGLU activations; waves with a routed
+//            down tile load it now, before their gate/up rows are done.
+//   phase 3  down tiles: poll the slot's activations, dot, publish partial
+//            sums per (slot, output row).
+//   combine  the last wave of each workgroup polls its rows' partial sums of
+//            every slot, combines them in pick order, adds the gated shared
+//            expert and writes the output.
+//
+// Numerics are those of the staged kernels (QwenCPUModel.moeForward,
+// QwenCPUModel.swift:500-569): the same tiles, the same reduction orders.
+//
+// Epochs: workgroup b keeps gen[b] (written only by itself); every call of a
+// workspace increments all of them, so every workgroup derives the same epoch
+// g = gen[b] + 1 without communicating.  Polls are bounded; a poll that runs
+// out sets the workspace's error word and the workgroup carries on.
+#include "../../include/swq_bench.h"
+#include "moe_host.hpp"
+#include "route.hpp"
+#include "tile.hpp"
+
+namespace swq {
+
+constexpr int kFusedWaves = 8;
+constexpr int kFusedThreads = kFusedWaves * kWave;
+constexpr int kWorkWaves = kFusedWaves - 1;  // waves 0..6 carry tiles, wave 7 combines
+constexpr int kFusedMaxBlocks = 1024;        // gen[] entries kept in step
+constexpr int kReplicas = 8;                 // logit replicas (one per XCD)
+constexpr int kMaxInterFused = 2048;         // activations a down tile reads
+constexpr int kMaxCombineRows = 64;
+constexpr int kMaxBlkSlots = 4;              // slots whose activations one workgroup's down tiles read
+constexpr uint32_t kSpinLimit = 1u << 20;  // polls of ~1 us: about a second
+
+struct FusedArgs {
+    QMat router, gate, up, down, sh_gate, sh_up, sh_down, seg;
+    const void *x;
+    void *out;
+    int32_t *user_ids;
+    float *user_w;
+    uint32_t *gen;       // [kFusedMaxBlocks]
+    uint32_t *err;       // nonzero after a poll ran out
+    uint64_t *logit_x;   // [kReplicas][rep_stride] (logit, epoch)
+    uint64_t *hsh_x;     // [Is] shared SwiGLU activations
+    uint64_t *h_x;       // [K][I] routed SwiGLU activations
+    uint64_t *part_x;    // [K+1][H] down partial sums (slot K: shared expert)
+    int32_t rep_stride;
+    int32_t odt, accumulate;
+    int32_t H, E, K, I, Is, norm, has_shared;
+    int32_t nb;
+    int32_t router_tiles, p1_tiles;  // phase-1 tiles: router rows, then shared gate/up rows
+    int32_t gu_tpe, gu_tiles;        // routed gate/up tiles per expert, in all
+    int32_t dn_tpe, dn_tpe_sh, dn_tiles;  // down tiles per routed slot, for the shared slot, in all
+    int32_t dn_per_blk;              // consecutive down tiles per workgroup
+    int32_t rows_cmb;                // output rows combined per workgroup
+};
+
+// ---------------------------------------------------------------------------
+// kernel arguments
+
+// The compiler loads kernel arguments lazily, each scalar load followed by a
+// wait, so a phase that first touches a matrix descriptor pays a cache-miss
+// round trip per line.  One scalar load per 64-byte line of the argument
+// block, all issued before a single wait, brings the block into the scalar
+// cache up front (reads only).
+// Fifteen lines: the argument block is 897..960 bytes (checked below).
+__device__ __forceinline__ void prefetch_kernargs() {
+    const auto *kp = __builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t d0, d1, d2, d3, d4, d5, d6, d7, d8, d9, d10, d11, d12, d13, d14;
+    asm volatile(
+        "s_load_dword %0, %15, 0x0\n\ts_load_dword %1, %15, 0x40\n\t"
+        "s_load_dword %2, %15, 0x80\n\ts_load_dword %3, %15, 0xc0\n\t"
+        "s_load_dword %4, %15, 0x100\n\ts_load_dword %5, %15, 0x140\n\t"
+        "s_load_dword %6, %15, 0x180\n\ts_load_dword %7, %15, 0x1c0\n\t"
+        "s_load_dword %8, %15, 0x200\n\ts_load_dword %9, %15, 0x240\n\t"
+        "s_load_dword %10, %15, 0x280\n\ts_load_dword %11, %15, 0x2c0\n\t"
+        "s_load_dword %12, %15, 0x300\n\ts_load_dword %13, %15, 0x340\n\t"
+        "s_load_dword %14, %15, 0x380\n\ts_waitcnt lgkmcnt(0)"
+        : "=s"(d0), "=s"(d1), "=s"(d2), "=s"(d3), "=s"(d4), "=s"(d5), "=s"(d6), "=s"(d7), "=s"(d8), "=s"(d9),
+          "=s"(d10), "=s"(d11), "=s"(d12), "=s"(d13), "=s"(d14)
+        : "s"(kp)
+        : "memory");
+}
+
+// ---------------------------------------------------------------------------
+// (value, epoch) words
+
+__device__ __forceinline__ void put_pair(uint64_t *p, float v, uint32_t g) {
+    __hip_atomic_store(p, (static_cast<uint64_t>(g) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t get_pair(uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint32_t get_u32(uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One wave waits until the n words src[(j / seg) * stride + j % seg], j < n,
+// carry epoch g, and leaves their values in dst[(j / seg) * dpitch + j % seg]
+// (LDS; dpitch 0 means seg).  Up to eight loads
+// per lane are in flight per round (512 words); a lane stops loading a word
+// once it is valid.
+constexpr int kPollPerLane = 8;
+
+__device__ __forceinline__ void poll_pairs(uint64_t *src, int n, int seg, int stride, uint32_t g, float *dst,
+                                           int lane, uint32_t *err, int dpitch = 0) {
+    if (dpitch == 0) dpitch = seg;
+    for (int j0 = 0; j0 < n; j0 += kPollPerLane * kWave) {
+        uint64_t *pp[kPollPerLane];
+        float *dd[kPollPerLane];
+        bool pend[kPollPerLane];
+#pragma unroll
+        for (int c = 0; c < kPollPerLane; ++c) {
+            const int j = j0 + c * kWave + lane;
+            pend[c] = j < n;
+            const int jc = min(j, n - 1);
+            const int q = jc / seg;
+            pp[c] = src + static_cast<int64_t>(q) * stride + (jc - q * seg);
+            dd[c] = dst + q * dpitch + (jc - q * seg);
+        }
+        uint32_t it = 0;
+        for (;;) {
+            uint64_t v[kPollPerLane];
+#pragma unroll
+            for (int c = 0; c < kPollPerLane; ++c) v[c] = pend[c] ? get_pair(pp[c]) : 0;
+            bool any = false;
+#pragma unroll
+            for (int c = 0; c < kPollPerLane; ++c) {
+                if (pend[c] && static_cast<uint32_t>(v[c] >> 32) == g) {
+                    *dd[c] = __uint_as_float(static_cast<uint32_t>(v[c]));
+                    pend[c] = false;
+                }
+                any = any || pend[c];
+            }
+            if (__ballot(any) == 0) break;
+            if (++it > kSpinLimit) {
+                if (lane == 0) atomicOr(err, 1u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    // the wave reads dst right after: order its LDS writes before those reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---------------------------------------------------------------------------
+// routing: top-k of the logits in LDS, one wave
+
+// Lane l holds experts l*M .. l*M+M-1, sorted by (logit desc, id asc); each
+// of the K rounds takes the wave-wide maximum head, the lowest lane holding
+// it wins (lower lanes hold lower ids), and the winner pops its head.  Lane k
+// ends up with pick k.  Selection by logit with ties to the lower id equals
+// the reference's selection by probability (QwenCPUModel.swift:508-522)
+// except where two distinct logits give the same fp32 probability.
+// p_k = exp(l_k - max) / sum_e exp(l_e - max) (:65-71); w_k = p_k / sum_j p_j
+// when norm (:546-550).
+template <int M>
+__device__ __forceinline__ void topk_lds(const float *lg_lds, int E, int K, int norm, int lane, int32_t &my_id,
+                                         float &my_w) {
+    float lg[M];
+    uint32_t key[M];
+    int32_t id[M];
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+        const int e = lane * M + j;
+        const float v = lg_lds[min(e, E - 1)];
+        lg[j] = e < E ? v : -INFINITY;
+        key[j] = e < E ? orderable(v) : 0u;
+        id[j] = e;
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+#pragma unroll
+        for (int j = 0; j + 1 < M - i; ++j) {
+            const bool sw = key[j] < key[j + 1];
+            const uint32_t k0 = key[j], k1 = key[j + 1];
+            const int32_t i0 = id[j], i1 = id[j + 1];
+            key[j] = sw ? k1 : k0;
+            key[j + 1] = sw ? k0 : k1;
+            id[j] = sw ? i1 : i0;
+            id[j + 1] = sw ? i0 : i1;
+        }
+    }
+    uint32_t top_key = 0, my_key = 0;
+    my_id = 0;
+    for (int k = 0; k < K; ++k) {
+        const uint32_t gmax = wave_max_u32(key[0]);
+        const uint64_t cand = __ballot(key[0] == gmax);
+        const int winner = cand ? __builtin_ctzll(cand) : 0;
+        const int32_t e = __builtin_amdgcn_readlane(id[0], winner);
+        if (k == 0) top_key = gmax;
+        if (lane == k) {
+            my_id = e;
+            my_key = gmax;
+        }
+        if (lane == winner) {
+#pragma unroll
+            for (int j = 0; j + 1 < M; ++j) {
+                key[j] = key[j + 1];
+                id[j] = id[j + 1];
+            }
+            key[M - 1] = 0;
+        }
+    }
+    const float top = from_orderable(top_key);
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < M; ++j) part += expf(lg[j] - top);  // -inf padding adds 0
+    const float denom = wave_sum_all(part);
+    const float pk = lane < K ? expf(from_orderable(my_key) - top) / denom : 0.f;
+    const float total = wave_sum_all(pk);
+    my_w = norm ? pk / total : pk;
+}
+
+// ---------------------------------------------------------------------------
+// phase-1 jobs (runtime format dispatch; nothing is held across phases)
+
+// Router rows of tile `tile` -> logits, one copy per replica.
+template <int XDT, int BITS, int CPL, int ES, int XF>
+__device__ __forceinline__ void router_job(const FusedArgs &a, int tile, uint32_t g, int lane) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
+    const QMat &m = a.router;
+    const LaneMap lm = lane_map(m.lpr_log2, lane);
+    const int row0 = tile * RI * lm.rpw;
+    RowTile<BITS, CPL, ES> rt;
+    load_tile(rt, m, 0, lm, row0, a.E);
+    XSlice<BITS, CPL, XF> xs;
+    load_xslice<XDT>(xs, m, lm, a.x, 0);
+    float res[RI];
+    dot_tile(res, rt, xs, m, lm);
+    if (lm.j == lm.lpr - 1) {
+#pragma unroll
+        for (int i = 0; i < RI; ++i) {
+            const int row = row0 + i * lm.rpw + lm.q;
+            if (row < a.E) {
+#pragma unroll
+                for (int r = 0; r < kReplicas; ++r) put_pair(a.logit_x + r * a.rep_stride + row, res[i], g);
+            }
+        }
+    }
+}
+
+// Shared-expert gate/up rows of tile `tile` -> silu(g) * u.
+template <int XDT, int BITS, int CPL, int ES, int XF>
+__device__ __forceinline__ void shared_gateup_job(const FusedArgs &a, int tile, uint32_t g, int lane) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
+    const LaneMap lm = lane_map(a.sh_gate.lpr_log2, lane);
+    const int row0 = tile * RI * lm.rpw;
+    RowTile<BITS, CPL, ES> tg, tu;
+    load_tile(tg, a.sh_gate, 0, lm, row0, a.Is);
+    load_tile(tu, a.sh_up, 0, lm, row0, a.Is);
+    XSlice<BITS, CPL, XF> xs;
+    load_xslice<XDT>(xs, a.sh_gate, lm, a.x, 0);
+    float rg[RI], ru[RI];
+    dot_tile(rg, tg, xs, a.sh_gate, lm);
+    dot_tile(ru, tu, xs, a.sh_up, lm);
+    if (lm.j == lm.lpr - 1) {
+#pragma unroll
+        for (int i = 0; i < RI; ++i) {
+            const int row = row0 + i * lm.rpw + lm.q;
+            if (row < a.Is) put_pair(a.hsh_x + row, swiglu(rg[i], ru[i]), g);
+        }
+    }
+}
+
+// The shared-expert gate logit <w_sg, x>, returned to every lane.
+template <int XDT, int BITS, int CPL, int ES, int XF>
+__device__ __forceinline__ void seg_job(const FusedArgs &a, int lane, float &sg) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
+    const LaneMap lm = lane_map(a.seg.lpr_log2, lane);
+    RowTile<BITS, CPL, ES> rt;
+    load_tile(rt, a.seg, 0, lm, 0, 1);
+    XSlice<BITS, CPL, XF> xs;
+    load_xslice<XDT>(xs, a.seg, lm, a.x, 0);
+    float res[RI];
+    dot_tile(res, rt, xs, a.seg, lm);
+    // row 0 is pass 0, row slot 0: the last lane of the first segment
+    sg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(res[0]), lm.lpr - 1));
+}
+
+// Formats with 2-byte scales only (the fused path's precondition).
+#define SWQ_DISPATCH2(XDT, m, FN, ...)                                      \
+    do {                                                                    \
+        if constexpr (XDT == SWQ_BF16) {                                    \
+            if ((m).bits == 4) FN<XDT, 4, 2, 2, kXBF16>(__VA_ARGS__);       \
+            else if ((m).cpl == 1) FN<XDT, 8, 1, 2, kXF32>(__VA_ARGS__);    \
+            else FN<XDT, 8, 2, 2, kXF32>(__VA_ARGS__);                      \
+        } else {                                                            \
+            if ((m).bits == 4) FN<XDT, 4, 1, 2, kXF32>(__VA_ARGS__);        \
+            else if ((m).cpl == 1) FN<XDT, 8, 1, 2, kXF32>(__VA_ARGS__);    \
+            else FN<XDT, 8, 2, 2, kXF32>(__VA_ARGS__);                      \
+        }                                                                   \
+    } while (0)
+
+// fp32 activations of a down tile from LDS (one chunk per lane).
+template <int BITS>
+__device__ __forceinline__ void load_xslice_lds(XSlice<BITS, 1, kXF32> &xs, const QMat &m, const LaneMap &lm,
+                                                const float *h) {
+    constexpr int kCPC = codes_per_chunk<BITS>();
+    const int c = min(lm.j, m.chunks - 1);
+    const float4 *p = reinterpret_cast<const float4 *>(h + c * kCPC);
+#pragma unroll
+    for (int i = 0; i < kCPC / 4; ++i) {
+        const float4 v = p[i];
+        xs.v[0][4 * i] = v.x;
+        xs.v[0][4 * i + 1] = v.y;
+        xs.v[0][4 * i + 2] = v.z;
+        xs.v[0][4 * i + 3] = v.w;
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kCPC; ++i) s += xs.v[0][i];
+    xs.sum[0] = s;
+}
+
+// Waits (bounded) until the LDS counter reaches `target`.
+__device__ __forceinline__ void wait_count(int32_t *c, int target, uint32_t *err, int lane) {
+    uint32_t it = 0;
+    while (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+        if (++it > kSpinLimit) {
+            if (lane == 0) atomicOr(err, 4u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+__device__ __forceinline__ void count_done(int32_t *c, int lane) {
+    if (lane == 0) __hip_atomic_fetch_add(c, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Slot of down tile u: routed slots first, then the shared expert (slot K).
+__device__ __forceinline__ int dn_slot(const FusedArgs &a, int u) {
+    const int routed_dn = a.K * a.dn_tpe;
+    return u < routed_dn ? u / a.dn_tpe : a.K;
+}
+
+// Down tiles first, first + 7, ... below `end` of this wave: wait until the
+// workgroup's fetching wave has the slot's SwiGLU activations in LDS, dot,
+// publish (partial sum, epoch) per output row.  With `held`, dt already holds
+// the first tile.
+template <int DB>
+__device__ __forceinline__ void down_tiles(const FusedArgs &a, int first, int end, int slot_lo, RowTile<DB, 1, 2> &dt,
+                                           bool held, uint32_t g, int lane, const int32_t *s_ids,
+                                           float (*s_hb)[kMaxInterFused], int32_t *s_ready) {
+    constexpr int DRI = RowTile<DB, 1, 2>::kRI;
+    const int routed_dn = a.K * a.dn_tpe;
+#pragma unroll 1
+    for (int u = first; u < end; u += kWorkWaves) {
+        const bool sh = u >= routed_dn;
+        const QMat &m = sh ? a.sh_down : a.down;
+        const LaneMap lm = lane_map(m.lpr_log2, lane);
+        const int slot = sh ? a.K : u / a.dn_tpe;
+        const int row0 = (sh ? u - routed_dn : u - slot * a.dn_tpe) * DRI * lm.rpw;
+        if (!held || u != first) load_tile(dt, m, sh ? 0 : s_ids[slot], lm, row0, a.H);
+        const int idx = slot - slot_lo;
+        uint32_t it = 0;
+        while (__hip_atomic_load(s_ready + idx, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0) {
+            if (++it > kSpinLimit) {
+                if (lane == 0) atomicOr(a.err, 2u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        XSlice<DB, 1, kXF32> xs;
+        load_xslice_lds<DB>(xs, m, lm, s_hb[idx]);
+        float res[DRI];
+        dot_tile(res, dt, xs, m, lm);
+        if (lm.j == lm.lpr - 1) {
+#pragma unroll
+            for (int i = 0; i < DRI; ++i) {
+                const int row = row0 + i * lm.rpw + lm.q;
+                if (row < a.H) put_pair(a.part_x + static_cast<int64_t>(slot) * a.H + row, res[i], g);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// the kernel: XDT activation dtype; GB/GC/GX the routed gate/up format; DB
+// the down projections' bits (routed and shared alike).  Scales are 2 bytes.
+
+template <int XDT, int GB, int GC, int GX, int DB>
+__global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
+    __shared__ float s_logits[kMaxExperts];
+    __shared__ int32_t s_ids[SWQ_MAX_TOPK];
+    __shared__ float s_w[SWQ_MAX_TOPK];
+    __shared__ __attribute__((aligned(16))) float s_hb[kMaxBlkSlots][kMaxInterFused];
+    __shared__ int32_t s_ready[kMaxBlkSlots];
+    // waves of this workgroup done with: [0] phase 1, [1] gate/up, [2] down tiles.
+    // A wave that waits on other workgroups' results starts polling global
+    // memory only once its own workgroup's share of that step is done: polls
+    // issued earlier would only compete with the weight stream.
+    __shared__ int32_t s_cnt[3];
+    __shared__ float s_cmb[(SWQ_MAX_TOPK + 1) * kMaxCombineRows];
+
+    static_assert(sizeof(FusedArgs) > 896 && sizeof(FusedArgs) <= 960, "prefetch_kernargs covers 15 lines");
+    prefetch_kernargs();
+    const int wave = threadIdx.x >> 6;
+    const int b = blockIdx.x, NB = a.nb;
+    // Each phase takes the lane index through an empty asm: its per-lane
+    // address arithmetic then cannot be hoisted to the top of the kernel,
+    // where it would stay live (and spill) across the earlier phases.
+    int lane = threadIdx.x & 63;
+    // the call's epoch; its first use waits for the load
+    const uint32_t g = get_u32(a.gen + b) + 1u;
+
+    // This workgroup's down tiles [dn0, dn1) read the activations of slots
+    // slot_lo .. slot_lo + kMaxBlkSlots - 1 (the host checks the span); wave
+    // w takes dn0 + w, dn0 + w + 7, ...  A wave with no routed gate/up rows
+    // whose first down tile is the shared expert's loads that tile during
+    // phase 1 and holds it; every other wave loads its down tiles after its
+    // gate/up rows, so no code path holds a down tile and a gate/up tile at
+    // once.
+    constexpr int DRI = RowTile<DB, 1, 2>::kRI;
+    const int dn0 = min(b * a.dn_per_blk, a.dn_tiles);
+    const int dn1 = min(dn0 + a.dn_per_blk, a.dn_tiles);
+    const int dn_u = dn0 + wave;
+    const int routed_dn = a.K * a.dn_tpe;
+    const int slot_lo = dn0 < dn1 ? dn_slot(a, dn0) : 0;
+    const int slot_hi = dn0 < dn1 ? dn_slot(a, dn1 - 1) : -1;
+    const bool held = wave < kWorkWaves && dn_u >= routed_dn && dn_u < dn1 && wave * NB + b >= a.gu_tiles;
+    if (threadIdx.x < kMaxBlkSlots) s_ready[threadIdx.x] = 0;
+    if (threadIdx.x < 3) s_cnt[threadIdx.x] = 0;
+    __syncthreads();
+    RowTile<DB, 1, 2> dt;
+    float sg = 0.f;
+
+    // ---- phase 1 ----------------------------------------------------------
+    asm volatile("" : "+v"(lane));
+    if (wave < kWorkWaves) {
+#pragma unroll 1
+        for (int p = (kWorkWaves - 1 - wave) * NB + b; p < a.p1_tiles; p += kWorkWaves * NB) {
+            if (p < a.router_tiles) SWQ_DISPATCH2(XDT, a.router, router_job, a, p, g, lane);
+            else SWQ_DISPATCH2(XDT, a.sh_gate, shared_gateup_job, a, p - a.router_tiles, g, lane);
+        }
+        count_done(&s_cnt[0], lane);
+        asm volatile("" : "+v"(lane));
+        if (held) {
+            const LaneMap lm = lane_map(a.sh_down.lpr_log2, lane);
+            load_tile(dt, a.sh_down, 0, lm, (dn_u - routed_dn) * DRI * lm.rpw, a.H);
+        }
+    } else if (a.has_shared) {
+        SWQ_DISPATCH2(XDT, a.seg, seg_job, a, lane, sg);
+    }
+
+    // ---- routing ------------------------------------------------------------
+    asm volatile("" : "+v"(lane));
+    if (wave == 0) {
+        wait_count(&s_cnt[0], kWorkWaves, a.err, lane);
+        poll_pairs(a.logit_x + (b % kReplicas) * a.rep_stride, a.E, a.E, 0, g, s_logits, lane, a.err);
+        int32_t my_id;
+        float my_w;
+        const int M = (a.E + kWave - 1) / kWave;
+        if (M <= 1) topk_lds<1>(s_logits, a.E, a.K, a.norm, lane, my_id, my_w);
+        else if (M <= 2) topk_lds<2>(s_logits, a.E, a.K, a.norm, lane, my_id, my_w);
+        else if (M <= 4) topk_lds<4>(s_logits, a.E, a.K, a.norm, lane, my_id, my_w);
+        else if (M <= 8) topk_lds<8>(s_logits, a.E, a.K, a.norm, lane, my_id, my_w);
+        else topk_lds<16>(s_logits, a.E, a.K, a.norm, lane, my_id, my_w);
+        if (lane < a.K) {
+            s_ids[lane] = my_id;
+            s_w[lane] = my_w;
+            if (b == 0) {
+                if (a.user_ids) a.user_ids[lane] = my_id;
+                if (a.user_w) a.user_w[lane] = my_w;
+            }
+        }
+    }
+    __syncthreads();
+
+    if (wave < kWorkWaves) {
+        asm volatile("" : "+v"(lane));
+        if (held) {
+            count_done(&s_cnt[1], lane);
+            down_tiles<DB>(a, dn_u, dn1, slot_lo, dt, true, g, lane, s_ids, s_hb, s_ready);
+        } else {
+            // ---- phase 2: routed gate/up ------------------------------------
+            constexpr int GRI = RowTile<GB, GC, 2>::kRI;
+            const LaneMap lm = lane_map(a.gate.lpr_log2, lane);
+#pragma unroll 1
+            for (int t = wave * NB + b; t < a.gu_tiles; t += kWorkWaves * NB) {
+                const int slot = t / a.gu_tpe;
+                const int row0 = (t - slot * a.gu_tpe) * GRI * lm.rpw;
+                const int64_t e = s_ids[slot];
+                RowTile<GB, GC, 2> tg, tu;
+                load_tile(tg, a.gate, e, lm, row0, a.I);
+                load_tile(tu, a.up, e, lm, row0, a.I);
+                XSlice<GB, GC, GX> xs;
+                load_xslice<XDT>(xs, a.gate, lm, a.x, 0);
+                float rg[GRI], ru[GRI];
+                dot_tile(rg, tg, xs, a.gate, lm);
+                dot_tile(ru, tu, xs, a.up, lm);
+                if (lm.j == lm.lpr - 1) {
+#pragma unroll
+                    for (int i = 0; i < GRI; ++i) {
+                        const int row = row0 + i * lm.rpw + lm.q;
+                        if (row < a.I)
+                            put_pair(a.h_x + static_cast<int64_t>(slot) * a.I + row, swiglu(rg[i], ru[i]), g);
+                    }
+                }
+            }
+            count_done(&s_cnt[1], lane);
+            // ---- phase 3: down tiles ------------------------------------------
+            asm volatile("" : "+v"(lane));
+            down_tiles<DB>(a, dn_u, dn1, slot_lo, dt, false, g, lane, s_ids, s_hb, s_ready);
+        }
+        count_done(&s_cnt[2], lane);
+    } else {
+        // ---- fetch: the activations this workgroup's down tiles read ---------
+        asm volatile("" : "+v"(lane));
+        wait_count(&s_cnt[1], kWorkWaves, a.err, lane);
+        if (slot_hi >= slot_lo) {
+            // routed slots are consecutive rows of h_x; the shared slot comes last
+            const int routed_hi = min(slot_hi, a.K - 1);
+            if (routed_hi >= slot_lo)
+                poll_pairs(a.h_x + static_cast<int64_t>(slot_lo) * a.I, (routed_hi - slot_lo + 1) * a.I, a.I,
+                           a.I, g, &s_hb[0][0], lane, a.err, kMaxInterFused);
+            if (slot_hi == a.K)
+                poll_pairs(a.hsh_x, a.Is, a.Is, 0, g, s_hb[a.K - slot_lo], lane, a.err, kMaxInterFused);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane < slot_hi - slot_lo + 1)
+                __hip_atomic_store(s_ready + lane, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        // ---- combine ------------------------------------------------------------
+        const int r0 = b * a.rows_cmb;
+        const int nr = min(a.rows_cmb, a.H - r0);
+        if (nr > 0) {
+            const int slots = a.K + (a.has_shared ? 1 : 0);
+            wait_count(&s_cnt[2], kWorkWaves, a.err, lane);
+            poll_pairs(a.part_x + r0, slots * nr, nr, a.H, g, s_cmb, lane, a.err);
+            const float gate = a.has_shared ? sigmoidf_ref(sg) : 0.f;
+            for (int rr = lane; rr < nr; rr += kWave) {
+                // out = sum_k w_k d_k in pick order, then + sigmoid(sg) * shared
+                // (QwenCPUModel.swift:549-566)
+                float acc = 0.f;
+                for (int k = 0; k < a.K; ++k) acc += s_w[k] * s_cmb[k * nr + rr];
+                if (a.has_shared) acc += gate * s_cmb[a.K * nr + rr];
+                const int row = r0 + rr;
+                if (a.odt == SWQ_BF16) {
+                    static_cast<uint16_t *>(a.out)[row] = f32_to_bf16_rne(acc);
+                } else {
+                    float *out = static_cast<float *>(a.out);
+                    out[row] = a.accumulate ? out[row] + acc : acc;
+                }
+            }
+        }
+        // the next call's epoch: every entry, whatever grid the next call uses
+        if (lane == 0) {
+            for (int i = b; i < kFusedMaxBlocks; i += NB)
+                __hip_atomic_store(a.gen + i, g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+
+struct FusedLayout {
+    size_t gen, err, logit_x, hsh_x, h_x, part_x, total;
+    int rep_stride;
+};
+
+// Placed after the staged path's regions of the same workspace.
+inline FusedLayout fused_layout(const swq_moe_layer *l, size_t base) {
+    FusedLayout f{};
+    size_t off = align256(base);
+    auto take = [&](size_t n) {
+        const size_t o = off;
+        off = align256(off + n);
+        return o;
+    };
+    // replicas 4 KiB apart plus a 256-byte skew, so they sit in different
+    // memory channels
+    const size_t rep_bytes = ((static_cast<size_t>(l->num_experts) * 8 + 4095) & ~static_cast<size_t>(4095)) + 256;
+    f.rep_stride = static_cast<int>(rep_bytes / 8);
+    f.gen = take(kFusedMaxBlocks * 4);
+    f.err = take(4);
+    f.logit_x = take(rep_bytes * kReplicas);
+    f.hsh_x = take(static_cast<size_t>(l->has_shared ? l->shared_intermediate : 1) * 8);
+    f.h_x = take(static_cast<size_t>(l->top_k) * l->moe_intermediate * 8);
+    f.part_x = take(static_cast<size_t>(l->top_k + 1) * l->hidden * 8);
+    f.total = off;
+    return f;
+}
+
+using FusedKernel = void (*)(FusedArgs);
+
+// The instantiation for this layer's formats, or nullptr.
+static FusedKernel fused_kernel_for(const QMat &gate, const QMat &down, int x_dtype) {
+    if (x_dtype == SWQ_BF16) {
+        if (gate.bits == 4 && gate.xf == 1 && gate.cpl == 2 && down.bits == 4) return moe_fused<SWQ_BF16, 4, 2, kXBF16, 4>;
+        if (gate.bits == 8 && gate.cpl == 2 && down.bits == 8) return moe_fused<SWQ_BF16, 8, 2, kXF32, 8>;
+        if (gate.bits == 8 && gate.cpl == 1 && down.bits == 8) return moe_fused<SWQ_BF16, 8, 1, kXF32, 8>;
+    } else {
+        if (gate.bits == 4 && gate.xf == 0 && gate.cpl == 1 && down.bits == 4) return moe_fused<SWQ_F32, 4, 1, kXF32, 4>;
+        if (gate.bits == 8 && gate.cpl == 2 && down.bits == 8) return moe_fused<SWQ_F32, 8, 2, kXF32, 8>;
+        if (gate.bits == 8 && gate.cpl == 1 && down.bits == 8) return moe_fused<SWQ_F32, 8, 1, kXF32, 8>;
+    }
+    return nullptr;
+}
+
+// Workgroups of the fused launch on the current device: one per CU, provided
+// a workgroup fits a CU (so the grid is resident at once on an idle device);
+// 0 if not.  Cached per device and kernel.
+static int fused_blocks(FusedKernel k) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    static FusedKernel cached_k[64];
+    static int cached_n[64];
+    if (cached_k[dev] == k) return cached_n[dev];
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(k), kFusedThreads, 0) !=
+        hipSuccess)
+        return 0;
+    const int n = per_cu >= 1 ? min(cus, kFusedMaxBlocks) : 0;
+    cached_n[dev] = n;
+    cached_k[dev] = k;
+    return n;
+}
+
+// The fused launch's arguments for this layer, or no kernel when the layer,
+// the batch or the device does not take the fused path.
+static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch, FusedArgs *fa, int *nb) {
+    if (batch != 1) return nullptr;
+    const swq_qlinear *mats[8] = {&layer->router, &layer->gate, &layer->up, &layer->down,
+                                  &layer->shared_gate, &layer->shared_up, &layer->shared_down,
+                                  &layer->shared_expert_gate};
+    const int nmats = layer->has_shared ? 8 : 4;
+    for (int i = 0; i < nmats; ++i)
+        if (mats[i]->scales_type == SWQ_F32) return nullptr;
+    FusedArgs a{};
+    a.router = make_qmat(&layer->router);
+    a.gate = make_qmat(&layer->gate);
+    a.up = make_qmat(&layer->up);
+    a.down = make_qmat(&layer->down);
+    plan_qmat(&a.router, x_dtype);
+    plan_qmat(&a.gate, x_dtype);
+    plan_qmat(&a.up, x_dtype);
+    plan_qmat(&a.down, SWQ_F32);
+    if (layer->has_shared) {
+        a.sh_gate = make_qmat(&layer->shared_gate);
+        a.sh_up = make_qmat(&layer->shared_up);
+        a.sh_down = make_qmat(&layer->shared_down);
+        a.seg = make_qmat(&layer->shared_expert_gate);
+        plan_qmat(&a.sh_gate, x_dtype);
+        plan_qmat(&a.sh_up, x_dtype);
+        plan_qmat(&a.seg, x_dtype);
+        plan_qmat(&a.sh_down, SWQ_F32);
+        if (a.sh_down.bits != a.down.bits) return nullptr;
+    }
+    if (layer->moe_intermediate > kMaxInterFused) return nullptr;
+    if (layer->has_shared && layer->shared_intermediate > kMaxInterFused) return nullptr;
+    FusedKernel kern = fused_kernel_for(a.gate, a.down, x_dtype);
+    if (!kern) return nullptr;
+    const int blocks = fused_blocks(kern);
+    if (blocks <= 0) return nullptr;
+    const int H = layer->hidden;
+    a.nb = blocks;
+    a.rows_cmb = (H + blocks - 1) / blocks;
+    if (a.rows_cmb > kMaxCombineRows) return nullptr;
+    a.H = H;
+    a.E = layer->num_experts;
+    a.K = layer->top_k;
+    a.I = layer->moe_intermediate;
+    a.Is = layer->has_shared ? layer->shared_intermediate : 0;
+    a.norm = layer->norm_topk_prob ? 1 : 0;
+    a.has_shared = layer->has_shared ? 1 : 0;
+    a.router_tiles = (a.E + tile_rows(a.router) - 1) / tile_rows(a.router);
+    a.p1_tiles = a.router_tiles + (a.has_shared ? (a.Is + tile_rows(a.sh_gate) - 1) / tile_rows(a.sh_gate) : 0);
+    a.gu_tpe = (a.I + tile_rows(a.gate) - 1) / tile_rows(a.gate);
+    a.gu_tiles = a.K * a.gu_tpe;
+    a.dn_tpe = (H + tile_rows(a.down) - 1) / tile_rows(a.down);
+    a.dn_tpe_sh = a.has_shared ? (H + tile_rows(a.sh_down) - 1) / tile_rows(a.sh_down) : 0;
+    a.dn_tiles = a.K * a.dn_tpe + a.dn_tpe_sh;
+    a.dn_per_blk = (a.dn_tiles + blocks - 1) / blocks;
+    // every workgroup's down tiles must span at most kMaxBlkSlots slots
+    auto slot_of = [&](int u) { return u < a.K * a.dn_tpe ? u / a.dn_tpe : a.K; };
+    for (int blk = 0; blk < blocks; ++blk) {
+        const int u0 = blk * a.dn_per_blk, u1 = min(u0 + a.dn_per_blk, a.dn_tiles);
+        if (u0 < u1 && slot_of(u1 - 1) - slot_of(u0) + 1 > kMaxBlkSlots) return nullptr;
+    }
+    *fa = a;
+    *nb = blocks;
+    return kern;
+}
+
+size_t fused_ws_bytes(const swq_moe_layer *l, size_t base) { return fused_layout(l, base).total; }
+
+int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int batch, void *out, int out_dtype,
+                 int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes, size_t staged_bytes,
+                 bool accumulate, hipStream_t stream, bool *taken) {
+    *taken = false;
+    FusedArgs a;
+    int nb = 0;
+    FusedKernel k = fused_plan(layer, x_dtype, batch, &a, &nb);
+    if (!k) return SWQ_OK;
+    const FusedLayout fl = fused_layout(layer, staged_bytes);
+    if (ws_bytes < fl.total) return SWQ_OK;
+    uint8_t *wsb = static_cast<uint8_t *>(ws);
+    a.x = x;
+    a.out = out;
+    a.user_ids = topk_ids;
+    a.user_w = topk_weights;
+    a.gen = reinterpret_cast<uint32_t *>(wsb + fl.gen);
+    a.err = reinterpret_cast<uint32_t *>(wsb + fl.err);
+    a.logit_x = reinterpret_cast<uint64_t *>(wsb + fl.logit_x);
+    a.hsh_x = reinterpret_cast<uint64_t *>(wsb + fl.hsh_x);
+    a.h_x = reinterpret_cast<uint64_t *>(wsb + fl.h_x);
+    a.part_x = reinterpret_cast<uint64_t *>(wsb + fl.part_x);
+    a.rep_stride = fl.rep_stride;
+    a.odt = out_dtype;
+    a.accumulate = accumulate ? 1 : 0;
+    hipLaunchKernelGGL(k, dim3(nb), dim3(kFusedThreads), 0, stream, a);
+    const int st = launch_status();
+    if (st != SWQ_OK) return st;
+    *taken = true;
+    return SWQ_OK;
+}
+
+size_t fused_err_offset(const swq_moe_layer *l, size_t base) { return fused_layout(l, base).err; }
+
+}  // namespace swq

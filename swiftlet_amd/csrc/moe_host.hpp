@@ -1,0 +1,95 @@
+// Host-side validation and workspace layout of the MoE decode step, shared by
+// the staged and the single-launch paths.
+#pragma once
+
+#include "internal.hpp"
+
+namespace swq {
+
+constexpr int kMaxExperts = 1024;
+
+struct WsLayout {
+    size_t header, logits, sg, h_sh, ids, wts, n_unique, uniq_e, uniq_np, uniq_pairs, h, total;
+};
+
+inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+inline WsLayout ws_layout(const swq_moe_layer *l, int B) {
+    WsLayout w{};
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        const size_t o = off;
+        off = align256(off + n);
+        return o;
+    };
+    const size_t P = static_cast<size_t>(B) * l->top_k;
+    w.header = take(256);  // reserved; zeroed by swq_moe_workspace_init
+    w.logits = take(static_cast<size_t>(B) * l->num_experts * 4);
+    w.sg = take(static_cast<size_t>(B) * 4);
+    w.h_sh = take(static_cast<size_t>(B) * (l->has_shared ? l->shared_intermediate : 1) * 4);
+    w.ids = take(P * 4);
+    w.wts = take(P * 4);
+    w.n_unique = take(4);
+    w.uniq_e = take(P * 4);
+    w.uniq_np = take(P * 4);
+    w.uniq_pairs = take(P * B * 4);
+    w.h = take(P * l->moe_intermediate * 4);
+    w.total = off;
+    return w;
+}
+
+// A matrix of the layer: shape, format and alignment, and whether its plan
+// fits the compiled kernels when read with activations of dtype x_dtype
+// (reads_h: the fp32 SwiGLU activations of stage 3).
+inline int check_vec(const swq_qlinear *l, int out_dim, int in_dim, bool stacked, int E, int x_dtype,
+                     bool reads_h) {
+    int st = check_linear_shape(l);
+    if (st != SWQ_OK) return st;
+    if (l->out_dim != out_dim || l->in_dim != in_dim) return SWQ_ERR_BAD_SHAPE;
+    if (l->bits != 4 && l->bits != 8) return SWQ_ERR_UNSUPPORTED_BITS;
+    if ((static_cast<int64_t>(in_dim) * l->bits) % 128 != 0) return SWQ_ERR_BAD_SHAPE;
+    if ((static_cast<int64_t>(l->group_size) * l->bits) % 128 != 0) return SWQ_ERR_BAD_SHAPE;
+    if (!vector_path_ok(l, 0, 0, 0)) return SWQ_ERR_MISALIGNED;
+    QMat m = make_qmat(l);
+    plan_qmat(&m, reads_h ? SWQ_F32 : x_dtype);
+    if (!plan_fits(m) || (reads_h && m.cpl != 1)) return SWQ_ERR_LIMIT;
+    if (stacked && E > 1 && (l->expert_stride_w == 0 || l->expert_stride_sb == 0)) return SWQ_ERR_INVALID_ARGUMENT;
+    return SWQ_OK;
+}
+
+inline int check_layer(const swq_moe_layer *l, int B, int x_dtype) {
+    if (!l) return SWQ_ERR_INVALID_ARGUMENT;
+    if (l->reserved != 0) return SWQ_ERR_INVALID_ARGUMENT;
+    if (B <= 0 || l->hidden <= 0 || l->num_experts <= 0 || l->moe_intermediate <= 0) return SWQ_ERR_INVALID_ARGUMENT;
+    if (l->top_k <= 0 || l->top_k > l->num_experts) return SWQ_ERR_EXPERT_RANGE;
+    if (l->top_k > SWQ_MAX_TOPK || B > SWQ_MAX_BATCH || l->num_experts > kMaxExperts) return SWQ_ERR_LIMIT;
+    const int H = l->hidden, E = l->num_experts, I = l->moe_intermediate;
+    const int xd = x_dtype;
+    int st;
+    if ((st = check_vec(&l->router, E, H, false, E, xd, false)) != SWQ_OK) return st;
+    if ((st = check_vec(&l->gate, I, H, true, E, xd, false)) != SWQ_OK) return st;
+    if ((st = check_vec(&l->up, I, H, true, E, xd, false)) != SWQ_OK) return st;
+    if ((st = check_vec(&l->down, H, I, true, E, xd, true)) != SWQ_OK) return st;
+    if (l->gate.bits != l->up.bits || l->gate.in_dim != l->up.in_dim) return SWQ_ERR_BAD_SHAPE;
+    if (l->has_shared) {
+        const int Is = l->shared_intermediate;
+        if (Is <= 0) return SWQ_ERR_INVALID_ARGUMENT;
+        if ((st = check_vec(&l->shared_gate, Is, H, false, 1, xd, false)) != SWQ_OK) return st;
+        if ((st = check_vec(&l->shared_up, Is, H, false, 1, xd, false)) != SWQ_OK) return st;
+        if ((st = check_vec(&l->shared_down, H, Is, false, 1, xd, true)) != SWQ_OK) return st;
+        if ((st = check_vec(&l->shared_expert_gate, 1, H, false, 1, xd, false)) != SWQ_OK) return st;
+        if (l->shared_gate.bits != l->shared_up.bits) return SWQ_ERR_BAD_SHAPE;
+    }
+    return SWQ_OK;
+}
+
+// The single-launch path (moe_fused.hip): its workspace regions follow the
+// staged path's `base` bytes.  fused_decode launches it when the layer, the
+// batch and the device allow (*taken), else leaves the work to the caller.
+size_t fused_ws_bytes(const swq_moe_layer *l, size_t base);
+size_t fused_err_offset(const swq_moe_layer *l, size_t base);
+int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int batch, void *out, int out_dtype,
+                 int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes, size_t staged_bytes,
+                 bool accumulate, hipStream_t stream, bool *taken);
+
+}  // namespace swq

@@ -49,6 +49,9 @@ __device__ __forceinline__ LaneMap lane_map(int lpr_log2, int lane) {
     return m;
 }
 
+// Rows one wave covers in one tile: 4/CPL passes of 64/LPR rows.
+__host__ __device__ __forceinline__ int tile_rows(const QMat &m) { return (4 / m.cpl) * (kWave >> m.lpr_log2); }
+
 // ---------------------------------------------------------------------------
 // reductions over the LPR lanes of a row (DPP; the segment's last lane
 // always holds the full sum, and for LPR <= 16 every lane does)

@@ -3,9 +3,9 @@
 ``MoELayerGPU`` holds one layer's device-resident weights (QwenMetalModel's
 MoEGPU, QwenMetalModel.swift:34-39) and runs the decode step with
 ``swq_moe_decode``: router, softmax, top-k, renormalisation, SwiGLU experts,
-sigmoid-gated shared expert and weighted combine, in three launches
-(replacing moeForward / routerPicks / encodePendingMoE,
-QwenMetalModel.swift:609-716, 798-892).
+sigmoid-gated shared expert and weighted combine, in one launch for a single
+token and three for batches (replacing moeForward / routerPicks /
+encodePendingMoE, QwenMetalModel.swift:609-716, 798-892).
 """
 
 from __future__ import annotations
@@ -68,10 +68,19 @@ class MoELayerGPU:
         return ws
 
     # -- decode --------------------------------------------------------
+    def workspace_error(self, ws, batch: int = 1) -> int:
+        """The word the single-launch path sets if one of its bounded waits ran
+        out (0 when every call so far completed normally)."""
+        off = self.lib.swq_moe_workspace_error_offset(ctypes.byref(self._c), batch)
+        return int(ws[off:off + 4].cpu().numpy().view(np.uint32)[0])
+
     def decode(self, x, out=None, out_dtype=None, ws=None, accumulate: bool = False,
-               topk_ids=None, topk_weights=None, stream=None):
+               topk_ids=None, topk_weights=None, stream=None, path: str = "auto"):
         """One decode step for x [B, H] (bf16 or f32 device tensor).
 
+        ``path``: "auto" (swq_moe_decode: one launch when the layer and batch
+        allow, else three), "staged" (the three launches) or "fused" (the
+        single launch; raises SwqError LIMIT when it cannot take the call).
         Returns (out [B, H], topk_ids [B, K] int32, topk_weights [B, K] f32)."""
         torch = _torch()
         if x.dim() == 1:
@@ -88,10 +97,14 @@ class MoELayerGPU:
             topk_ids = torch.empty((B, self.top_k), dtype=torch.int32, device=x.device)
         if topk_weights is None:
             topk_weights = torch.empty((B, self.top_k), dtype=torch.float32, device=x.device)
-        check(self.lib.swq_moe_decode(
-            ctypes.byref(self._c), x.data_ptr(), x_dtype, B, out.data_ptr(), o_dtype,
-            topk_ids.data_ptr(), topk_weights.data_ptr(), ws.data_ptr(), ws.numel(),
-            _lib.SWQ_MOE_ACCUMULATE if accumulate else 0, _stream_handle(stream)), "moe_decode")
+        args = (ctypes.byref(self._c), x.data_ptr(), x_dtype, B, out.data_ptr(), o_dtype,
+                topk_ids.data_ptr(), topk_weights.data_ptr(), ws.data_ptr(), ws.numel(),
+                _lib.SWQ_MOE_ACCUMULATE if accumulate else 0)
+        if path == "auto":
+            check(self.lib.swq_moe_decode(*args, _stream_handle(stream)), "moe_decode")
+        else:
+            mask = {"staged": 7, "fused": _lib.SWQ_STAGES_FUSED}[path]
+            check(self.lib.swq_moe_decode_stages(*args, mask, _stream_handle(stream)), f"moe_decode ({path})")
         return out, topk_ids, topk_weights
 
     def touched_bytes(self, unique_experts: int, batch: int = 1, x_bytes: int = 2,

@@ -110,3 +110,84 @@ def test_moe_decode_odd_shapes(E, K, I, Is, H, bits, norm):
     for batch in (1, 5):
         gpu, xf, out, ids, w = _run(shape, batch, seed=77)
         _check_against_oracle(shape, xf, out, ids, w, seed=77)
+
+
+# ---------------------------------------------------------------------------
+# the single-launch path against the three-launch path: the same tiles and
+# reduction orders, so equal bit for bit
+
+def _pair(gpu, shape, x, out_dtype, ws_f, ws_s):
+    import torch
+    odt = torch.float32 if out_dtype == "f32" else torch.bfloat16
+    of, i_f, w_f = gpu.decode(x, out_dtype=odt, ws=ws_f, path="fused")
+    os_, i_s, w_s = gpu.decode(x, out_dtype=odt, ws=ws_s, path="staged")
+    torch.cuda.synchronize()
+    return (of, i_f, w_f), (os_, i_s, w_s)
+
+
+@pytest.mark.parametrize("name", ["qwen3.6-35b-a3b-q4", "qwen3-next-80b-a3b-q4", "qwen3.6-35b-a3b-q8"])
+@pytest.mark.parametrize("x_dtype,out_dtype", [("bf16", "f32"), ("f32", "bf16")])
+def test_fused_equals_staged(name, x_dtype, out_dtype):
+    import torch
+    shape = synth.SHAPES[name]
+    print(f"fused vs staged: {name} x {x_dtype} out {out_dtype}", flush=True)
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    xb = synth.activations_bf16(helpers.SEED + 11, 1, shape.hidden)
+    x = helpers.bf16_bits_to_torch(xb) if x_dtype == "bf16" else torch.from_numpy(synth.bf16_to_f32(xb)).cuda()
+    ws_f, ws_s = gpu.new_workspace(1), gpu.new_workspace(1)
+    (of, i_f, w_f), (os_, i_s, w_s) = _pair(gpu, shape, x, out_dtype, ws_f, ws_s)
+    assert gpu.workspace_error(ws_f) == 0
+    assert torch.equal(i_f, i_s) and torch.equal(w_f, w_s)
+    assert torch.equal(of, os_)
+    _check_against_oracle(shape, synth.bf16_to_f32(xb), of, i_f.cpu().numpy(), w_f.cpu().numpy())
+
+
+def test_fused_epochs_across_calls():
+    """One workspace, alternating layers and fresh inputs: each call consumes
+    only what it produced itself (stale words of earlier calls carry older
+    epochs), and no bounded wait runs out."""
+    import torch
+    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    layers = [moe.synth_layer(shape, helpers.SEED, r) for r in range(2)]
+    ws = layers[0].new_workspace(1)
+    ws_s = layers[0].new_workspace(1)
+    for i in range(6):
+        gpu = layers[i % 2]
+        print(f"epoch call {i}", flush=True)
+        xb = synth.activations_bf16(helpers.SEED + 100 + i, 1, shape.hidden)
+        x = helpers.bf16_bits_to_torch(xb)
+        (of, i_f, w_f), (os_, i_s, w_s) = _pair(gpu, shape, x, "f32", ws, ws_s)
+        assert torch.equal(i_f, i_s) and torch.equal(w_f, w_s), i
+        assert torch.equal(of, os_), i
+    assert layers[0].workspace_error(ws) == 0
+
+
+@pytest.mark.parametrize("E,K,I,Is,H,bits,norm", [
+    (8, 2, 32, 32, 64, 4, True),
+    (60, 4, 64, 128, 256, 8, False),
+    (1024, 16, 64, 64, 128, 4, True),
+])
+def test_fused_equals_staged_odd_shapes(E, K, I, Is, H, bits, norm):
+    import torch
+    shape = synth.MoEShape("odd", H, E, K, I, Is, expert_bits=bits, router_bits=8,
+                           group=64 if H % 64 == 0 and I % 64 == 0 else 32, norm_topk_prob=norm)
+    print(f"fused vs staged odd: {E},{K},{I},{Is},{H},{bits}", flush=True)
+    gpu = moe.synth_layer(shape, 77, 0)
+    xb = synth.activations_bf16(78, 1, shape.hidden)
+    x = helpers.bf16_bits_to_torch(xb)
+    ws_f, ws_s = gpu.new_workspace(1), gpu.new_workspace(1)
+    (of, i_f, w_f), (os_, i_s, w_s) = _pair(gpu, shape, x, "f32", ws_f, ws_s)
+    assert gpu.workspace_error(ws_f) == 0
+    assert torch.equal(i_f, i_s) and torch.equal(w_f, w_s)
+    assert torch.equal(of, os_)
+
+
+def test_fused_declines_batches():
+    from swiftlet_amd import _lib
+    import torch
+    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    x = helpers.bf16_bits_to_torch(synth.activations_bf16(3, 2, shape.hidden))
+    with pytest.raises(_lib.SwqError) as e:
+        gpu.decode(x, path="fused")
+    assert e.value.code == _lib.SWQ_ERR_LIMIT
