@@ -79,40 +79,43 @@ __device__ __forceinline__ float ubyte(uint32_t v, int n) {
 }
 
 // sum_i q_i * x_i over one 16-byte chunk of 4-bit codes; x holds the 32
-// matching inputs.  Nibble j of word k is input 8k + j.
+// matching inputs.  Nibble j of word k is input 8k + j.  Four independent
+// accumulator chains (one per word), summed pairwise at the end.
 __device__ __forceinline__ float dot_chunk_q4(const uint4 w, const float *x) {
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-    float acc = 0.f;
+    float acc[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const uint32_t lo = ws[k] & 0x0F0F0F0Fu;         // nibbles 0,2,4,6
         const uint32_t hi = (ws[k] >> 4) & 0x0F0F0F0Fu;  // nibbles 1,3,5,7
         const float *xx = x + 8 * k;
-        acc = fmaf(ubyte(lo, 0), xx[0], acc);
-        acc = fmaf(ubyte(hi, 0), xx[1], acc);
-        acc = fmaf(ubyte(lo, 1), xx[2], acc);
-        acc = fmaf(ubyte(hi, 1), xx[3], acc);
-        acc = fmaf(ubyte(lo, 2), xx[4], acc);
-        acc = fmaf(ubyte(hi, 2), xx[5], acc);
-        acc = fmaf(ubyte(lo, 3), xx[6], acc);
-        acc = fmaf(ubyte(hi, 3), xx[7], acc);
+        float a = ubyte(lo, 0) * xx[0];
+        a = fmaf(ubyte(hi, 0), xx[1], a);
+        a = fmaf(ubyte(lo, 1), xx[2], a);
+        a = fmaf(ubyte(hi, 1), xx[3], a);
+        a = fmaf(ubyte(lo, 2), xx[4], a);
+        a = fmaf(ubyte(hi, 2), xx[5], a);
+        a = fmaf(ubyte(lo, 3), xx[6], a);
+        a = fmaf(ubyte(hi, 3), xx[7], a);
+        acc[k] = a;
     }
-    return acc;
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
 }
 
 // Same for 8-bit codes: 16 inputs per chunk, byte j of word k is input 4k+j.
 __device__ __forceinline__ float dot_chunk_q8(const uint4 w, const float *x) {
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-    float acc = 0.f;
+    float acc[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const float *xx = x + 4 * k;
-        acc = fmaf(ubyte(ws[k], 0), xx[0], acc);
-        acc = fmaf(ubyte(ws[k], 1), xx[1], acc);
-        acc = fmaf(ubyte(ws[k], 2), xx[2], acc);
-        acc = fmaf(ubyte(ws[k], 3), xx[3], acc);
+        float a = ubyte(ws[k], 0) * xx[0];
+        a = fmaf(ubyte(ws[k], 1), xx[1], a);
+        a = fmaf(ubyte(ws[k], 2), xx[2], a);
+        a = fmaf(ubyte(ws[k], 3), xx[3], a);
+        acc[k] = a;
     }
-    return acc;
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
 }
 
 template <int BITS>

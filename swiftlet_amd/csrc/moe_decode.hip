@@ -72,14 +72,15 @@ struct MoEArgs {
     } while (0)
 
 // Down projections read the fp32 SwiGLU activations: one chunk per lane,
-// i.e. up to 2048 inputs at 4 bits and 1024 at 8 bits.
+// i.e. up to 2048 inputs at 4 bits and 1024 at 8 bits; 4-bit rows take the
+// split-bf16 dot products.
 #define SWQ_DISPATCH_DOWN(m, FN, ...)                                       \
     do {                                                                    \
         if ((m).stype == SWQ_F32) {                                         \
-            if ((m).bits == 4) FN<SWQ_F32, 4, 1, 4, kXF32>(__VA_ARGS__);    \
+            if ((m).bits == 4) FN<SWQ_F32, 4, 1, 4, kXBF16X2>(__VA_ARGS__); \
             else FN<SWQ_F32, 8, 1, 4, kXF32>(__VA_ARGS__);                  \
         } else {                                                            \
-            if ((m).bits == 4) FN<SWQ_F32, 4, 1, 2, kXF32>(__VA_ARGS__);    \
+            if ((m).bits == 4) FN<SWQ_F32, 4, 1, 2, kXBF16X2>(__VA_ARGS__); \
             else FN<SWQ_F32, 8, 1, 2, kXF32>(__VA_ARGS__);                  \
         }                                                                   \
     } while (0)
@@ -534,6 +535,8 @@ extern "C" size_t swq_moe_decode_workspace_bytes(const swq_moe_layer *layer, int
 
 extern "C" int swq_moe_workspace_init(void *ws, size_t ws_bytes, void *stream) {
     if (!ws || ws_bytes < 256) return SWQ_ERR_WORKSPACE;
+    const int st = fused_probe_device(static_cast<hipStream_t>(stream));
+    if (st != SWQ_OK) return st;
     return hip_status(hipMemsetAsync(ws, 0, ws_bytes, static_cast<hipStream_t>(stream)));
 }
 

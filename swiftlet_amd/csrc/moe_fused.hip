@@ -47,7 +47,6 @@ constexpr int kFusedMaxBlocks = 1024;        // gen[] entries kept in step
 constexpr int kReplicas = 8;                 // logit replicas (one per XCD)
 constexpr int kMaxInterFused = 2048;         // activations a down tile reads
 constexpr int kMaxCombineRows = 64;
-constexpr int kMaxBlkSlots = 4;              // slots whose activations one workgroup's down tiles read
 constexpr uint32_t kSpinLimit = 1u << 20;  // polls of ~1 us: about a second
 
 struct FusedArgs {
@@ -68,8 +67,8 @@ struct FusedArgs {
     int32_t nb;
     int32_t router_tiles, p1_tiles;  // phase-1 tiles: router rows, then shared gate/up rows
     int32_t gu_tpe, gu_tiles;        // routed gate/up tiles per expert, in all
-    int32_t dn_tpe, dn_tpe_sh, dn_tiles;  // down tiles per routed slot, for the shared slot, in all
-    int32_t dn_per_blk;              // consecutive down tiles per workgroup
+    int32_t dn_tpe, dn_tpe_sh;       // down tiles per routed slot, of the shared expert
+    int32_t local;                   // a group's workgroups share an XCD (verified on the host)
     int32_t rows_cmb;                // output rows combined per workgroup
 };
 
@@ -353,65 +352,143 @@ __device__ __forceinline__ void count_done(int32_t *c, int lane) {
     if (lane == 0) __hip_atomic_fetch_add(c, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Slot of down tile u: routed slots first, then the shared expert (slot K).
-__device__ __forceinline__ int dn_slot(const FusedArgs &a, int u) {
-    const int routed_dn = a.K * a.dn_tpe;
-    return u < routed_dn ? u / a.dn_tpe : a.K;
+// LDS activations of one slot.  The fetching wave polls them in as fp32;
+// for 4-bit down rows it then rewrites them as hi/lo bf16 pair words (the
+// kXBF16X2 format), chunk c (32 activations) in words [32c, 32c + 32): its
+// eight 16-byte groups (hi words 0-3, 4-7, 8-11, 12-15, then lo) with group
+// i stored at (i + c) mod 8, so the lanes of a down tile, which read chunk j
+// each, spread over the LDS banks.  One pair per lane and round: the reads
+// of a round all complete before its writes (in-order LDS within a wave).
+__device__ __forceinline__ int x2_word(int c, int grp16, int d) { return 32 * c + 4 * ((grp16 + c) & 7) + d; }
+
+__device__ __forceinline__ void convert_x2_lds(float *buf, int n, int lane) {
+    uint32_t *wbuf = reinterpret_cast<uint32_t *>(buf);
+    const int npairs = n / 2;
+    for (int p0 = 0; p0 < npairs; p0 += 4 * kWave) {
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int p = min(p0 + r * kWave + lane, npairs - 1);
+            const int c = p >> 4, w = p & 15;
+            const int e0 = 32 * c + 8 * (w >> 2) + (w & 3);
+            split_pair(buf[e0], buf[e0 + 4], hi[r], lo[r]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int p = p0 + r * kWave + lane;
+            if (p < npairs) {
+                const int c = p >> 4, w = p & 15;
+                wbuf[x2_word(c, w >> 2, w & 3)] = hi[r];
+                wbuf[x2_word(c, 4 + (w >> 2), w & 3)] = lo[r];
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
 }
 
-// Down tiles first, first + 7, ... below `end` of this wave: wait until the
-// workgroup's fetching wave has the slot's SwiGLU activations in LDS, dot,
-// publish (partial sum, epoch) per output row.  With `held`, dt already holds
-// the first tile.
+// One down tile of matrix m, rows from row0: dot with the activations in LDS
+// (split bf16 pairs and chunk sums for 4-bit rows, fp32 for 8-bit rows),
+// publish (partial sum, epoch) to part_x[slot][row].
 template <int DB>
-__device__ __forceinline__ void down_tiles(const FusedArgs &a, int first, int end, int slot_lo, RowTile<DB, 1, 2> &dt,
-                                           bool held, uint32_t g, int lane, const int32_t *s_ids,
-                                           float (*s_hb)[kMaxInterFused], int32_t *s_ready) {
+__device__ __forceinline__ void down_dot(const FusedArgs &a, const QMat &m, const RowTile<DB, 1, 2> &dt, int row0,
+                                         int slot, const float *h_lds, uint32_t g, int lane) {
     constexpr int DRI = RowTile<DB, 1, 2>::kRI;
-    const int routed_dn = a.K * a.dn_tpe;
-#pragma unroll 1
-    for (int u = first; u < end; u += kWorkWaves) {
-        const bool sh = u >= routed_dn;
-        const QMat &m = sh ? a.sh_down : a.down;
-        const LaneMap lm = lane_map(m.lpr_log2, lane);
-        const int slot = sh ? a.K : u / a.dn_tpe;
-        const int row0 = (sh ? u - routed_dn : u - slot * a.dn_tpe) * DRI * lm.rpw;
-        if (!held || u != first) load_tile(dt, m, sh ? 0 : s_ids[slot], lm, row0, a.H);
-        const int idx = slot - slot_lo;
-        uint32_t it = 0;
-        while (__hip_atomic_load(s_ready + idx, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0) {
-            if (++it > kSpinLimit) {
-                if (lane == 0) atomicOr(a.err, 2u);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        XSlice<DB, 1, kXF32> xs;
-        load_xslice_lds<DB>(xs, m, lm, s_hb[idx]);
-        float res[DRI];
-        dot_tile(res, dt, xs, m, lm);
-        if (lm.j == lm.lpr - 1) {
+    const LaneMap lm = lane_map(m.lpr_log2, lane);
+    float res[DRI];
+    if constexpr (DB == 4) {
+        XSlice<4, 1, kXBF16X2> xs;
+        const int c = min(lm.j, m.chunks - 1);
+        const uint32_t *wb = reinterpret_cast<const uint32_t *>(h_lds);
 #pragma unroll
-            for (int i = 0; i < DRI; ++i) {
-                const int row = row0 + i * lm.rpw + lm.q;
-                if (row < a.H) put_pair(a.part_x + static_cast<int64_t>(slot) * a.H + row, res[i], g);
-            }
+        for (int i = 0; i < 4; ++i) {
+            const uint4 h = *reinterpret_cast<const uint4 *>(wb + x2_word(c, i, 0));
+            const uint4 l = *reinterpret_cast<const uint4 *>(wb + x2_word(c, 4 + i, 0));
+            xs.hi[0][4 * i] = h.x;
+            xs.hi[0][4 * i + 1] = h.y;
+            xs.hi[0][4 * i + 2] = h.z;
+            xs.hi[0][4 * i + 3] = h.w;
+            xs.lo[0][4 * i] = l.x;
+            xs.lo[0][4 * i + 1] = l.y;
+            xs.lo[0][4 * i + 2] = l.z;
+            xs.lo[0][4 * i + 3] = l.w;
+        }
+        xs.sum[0] = pair_sum(xs.hi[0], xs.lo[0]);
+        dot_tile(res, dt, xs, m, lm);
+    } else {
+        XSlice<DB, 1, kXF32> xs;
+        load_xslice_lds<DB>(xs, m, lm, h_lds);
+        dot_tile(res, dt, xs, m, lm);
+    }
+    if (lm.j == lm.lpr - 1) {
+#pragma unroll
+        for (int i = 0; i < DRI; ++i) {
+            const int row = row0 + i * lm.rpw + lm.q;
+            if (row < a.H) put_pair(a.part_x + static_cast<int64_t>(slot) * a.H + row, res[i], g);
         }
     }
+}
+
+// Bounded wait for an LDS flag set by the workgroup's fetching wave.
+__device__ __forceinline__ void wait_ready(int32_t *flag, uint32_t *err, int lane) {
+    uint32_t it = 0;
+    while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0) {
+        if (++it > kSpinLimit) {
+            if (lane == 0) atomicOr(err, 2u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// (value, epoch) word written for readers on this XCD only: a plain store,
+// which stays in the XCD's L2, where their agent-coherent loads find it.
+// Used only when the host has verified that a group's workgroups share an
+// XCD; otherwise the agent-coherent store.
+__device__ __forceinline__ void put_pair_group(uint64_t *p, float v, uint32_t g, int local) {
+    const uint64_t w = (static_cast<uint64_t>(g) << 32) | __float_as_uint(v);
+    if (local) __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
 // the kernel: XDT activation dtype; GB/GC/GX the routed gate/up format; DB
 // the down projections' bits (routed and shared alike).  Scales are 2 bytes.
+//
+// Workgroups form kGroups groups, g = b % kGroups (the hardware hands
+// workgroups to XCDs round robin, so a group sits on one XCD); rank r =
+// b / kGroups.  Group g owns routed slots g, g + kGroups, ...: their gate/up
+// rows, their down tiles and the SwiGLU activations between them.  A down
+// tile is ~360 VALU instructions of one wave at batch 1, so the down tiles
+// are spread over four waves per workgroup.  Waves:
+//   0-3  routed gate/up tiles of the group (wave 0 first routes); then wave 3
+//        takes a share of the group's routed down tiles and wave 1 the shared
+//        expert's down tiles
+//   4-6  phase-1 jobs; then routed down tiles of the group, the first one
+//        loaded right after routing and held until the activations arrive
+//   7    shared-expert gate logit; fetches the activations the workgroup's
+//        down tiles read into LDS; combines its output rows
+
+constexpr int kGroups = 8;
+constexpr int kGuWaves = 4;
+constexpr int kDnShares = 4;           // routed down tiles: waves 4, 5, 6 and 3
+constexpr int kDnLateWave = 3;         // the share taken after gate/up
+constexpr int kShWave = 1, kAuxWave = 7;
+constexpr int kGroupSlots = (SWQ_MAX_TOPK + kGroups - 1) / kGroups;  // routed slots per group
+constexpr int kShBuf = kGroupSlots;                                    // LDS buffer of the shared slot
 
 template <int XDT, int GB, int GC, int GX, int DB>
 __global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
     __shared__ float s_logits[kMaxExperts];
     __shared__ int32_t s_ids[SWQ_MAX_TOPK];
     __shared__ float s_w[SWQ_MAX_TOPK];
-    __shared__ __attribute__((aligned(16))) float s_hb[kMaxBlkSlots][kMaxInterFused];
-    __shared__ int32_t s_ready[kMaxBlkSlots];
-    // waves of this workgroup done with: [0] phase 1, [1] gate/up, [2] down tiles.
+    __shared__ __attribute__((aligned(16))) float s_hb[kGroupSlots + 1][kMaxInterFused];
+    __shared__ int32_t s_ready[kGroupSlots + 1];
+    // waves of this workgroup done with: [0] phase 1, [1] gate/up, [2] down.
     // A wave that waits on other workgroups' results starts polling global
     // memory only once its own workgroup's share of that step is done: polls
     // issued earlier would only compete with the weight stream.
@@ -422,48 +499,31 @@ __global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
     prefetch_kernargs();
     const int wave = threadIdx.x >> 6;
     const int b = blockIdx.x, NB = a.nb;
+    const int grp = b % kGroups, rank = b / kGroups, NPG = NB / kGroups;
     // Each phase takes the lane index through an empty asm: its per-lane
     // address arithmetic then cannot be hoisted to the top of the kernel,
     // where it would stay live (and spill) across the earlier phases.
     int lane = threadIdx.x & 63;
     // the call's epoch; its first use waits for the load
     const uint32_t g = get_u32(a.gen + b) + 1u;
-
-    // This workgroup's down tiles [dn0, dn1) read the activations of slots
-    // slot_lo .. slot_lo + kMaxBlkSlots - 1 (the host checks the span); wave
-    // w takes dn0 + w, dn0 + w + 7, ...  A wave with no routed gate/up rows
-    // whose first down tile is the shared expert's loads that tile during
-    // phase 1 and holds it; every other wave loads its down tiles after its
-    // gate/up rows, so no code path holds a down tile and a gate/up tile at
-    // once.
-    constexpr int DRI = RowTile<DB, 1, 2>::kRI;
-    const int dn0 = min(b * a.dn_per_blk, a.dn_tiles);
-    const int dn1 = min(dn0 + a.dn_per_blk, a.dn_tiles);
-    const int dn_u = dn0 + wave;
-    const int routed_dn = a.K * a.dn_tpe;
-    const int slot_lo = dn0 < dn1 ? dn_slot(a, dn0) : 0;
-    const int slot_hi = dn0 < dn1 ? dn_slot(a, dn1 - 1) : -1;
-    const bool held = wave < kWorkWaves && dn_u >= routed_dn && dn_u < dn1 && wave * NB + b >= a.gu_tiles;
-    if (threadIdx.x < kMaxBlkSlots) s_ready[threadIdx.x] = 0;
+    const int nsg = a.K > grp ? (a.K - grp + kGroups - 1) / kGroups : 0;  // routed slots of the group
+    const bool has_sh_tiles = a.has_shared && b < a.dn_tpe_sh;
+    if (threadIdx.x <= kGroupSlots) s_ready[threadIdx.x] = 0;
     if (threadIdx.x < 3) s_cnt[threadIdx.x] = 0;
     __syncthreads();
-    RowTile<DB, 1, 2> dt;
+    constexpr int DRI = RowTile<DB, 1, 2>::kRI;
+    RowTile<DB, 1, 2> dt0;
     float sg = 0.f;
 
     // ---- phase 1 ----------------------------------------------------------
     asm volatile("" : "+v"(lane));
-    if (wave < kWorkWaves) {
+    if (wave < kAuxWave) {
 #pragma unroll 1
-        for (int p = (kWorkWaves - 1 - wave) * NB + b; p < a.p1_tiles; p += kWorkWaves * NB) {
+        for (int p = (kAuxWave - 1 - wave) * NB + b; p < a.p1_tiles; p += kAuxWave * NB) {
             if (p < a.router_tiles) SWQ_DISPATCH2(XDT, a.router, router_job, a, p, g, lane);
             else SWQ_DISPATCH2(XDT, a.sh_gate, shared_gateup_job, a, p - a.router_tiles, g, lane);
         }
         count_done(&s_cnt[0], lane);
-        asm volatile("" : "+v"(lane));
-        if (held) {
-            const LaneMap lm = lane_map(a.sh_down.lpr_log2, lane);
-            load_tile(dt, a.sh_down, 0, lm, (dn_u - routed_dn) * DRI * lm.rpw, a.H);
-        }
     } else if (a.has_shared) {
         SWQ_DISPATCH2(XDT, a.seg, seg_job, a, lane, sg);
     }
@@ -471,7 +531,7 @@ __global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
     // ---- routing ------------------------------------------------------------
     asm volatile("" : "+v"(lane));
     if (wave == 0) {
-        wait_count(&s_cnt[0], kWorkWaves, a.err, lane);
+        wait_count(&s_cnt[0], kAuxWave, a.err, lane);
         poll_pairs(a.logit_x + (b % kReplicas) * a.rep_stride, a.E, a.E, 0, g, s_logits, lane, a.err);
         int32_t my_id;
         float my_w;
@@ -491,20 +551,33 @@ __global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
         }
     }
     __syncthreads();
+    asm volatile("" : "+v"(lane));
 
-    if (wave < kWorkWaves) {
-        asm volatile("" : "+v"(lane));
-        if (held) {
-            count_done(&s_cnt[1], lane);
-            down_tiles<DB>(a, dn_u, dn1, slot_lo, dt, true, g, lane, s_ids, s_hb, s_ready);
-        } else {
-            // ---- phase 2: routed gate/up ------------------------------------
+    if (wave < kAuxWave) {
+        const int dshare = wave >= kGuWaves ? wave - kGuWaves : (wave == kDnLateWave ? kDnShares - 1 : -1);
+        const LaneMap lmd = lane_map(a.down.lpr_log2, lane);
+        const int nqd = nsg * a.dn_tpe;
+        const int qd0 = rank + NPG * dshare;
+        const bool early = wave >= kGuWaves && dshare >= 0 && qd0 < nqd;
+        if (early) {
+            // ---- the first routed down tile, loaded now and held ------------
+            const int j = qd0 / a.dn_tpe;
+            load_tile(dt0, a.down, s_ids[grp + kGroups * j], lmd, (qd0 - j * a.dn_tpe) * DRI * lmd.rpw, a.H);
+            // Without this the compiler may sink the loads below the waits
+            // that follow (allowed across an acquire), so they would start
+            // only once the activations are in.
+            asm volatile("" ::: "memory");
+        }
+        if (wave < kGuWaves) {
+            // ---- routed gate/up tiles of the group --------------------------
             constexpr int GRI = RowTile<GB, GC, 2>::kRI;
             const LaneMap lm = lane_map(a.gate.lpr_log2, lane);
+            const int nq = nsg * a.gu_tpe;
 #pragma unroll 1
-            for (int t = wave * NB + b; t < a.gu_tiles; t += kWorkWaves * NB) {
-                const int slot = t / a.gu_tpe;
-                const int row0 = (t - slot * a.gu_tpe) * GRI * lm.rpw;
+            for (int q = rank + NPG * wave; q < nq; q += NPG * kGuWaves) {
+                const int j = q / a.gu_tpe;
+                const int slot = grp + kGroups * j;
+                const int row0 = (q - j * a.gu_tpe) * GRI * lm.rpw;
                 const int64_t e = s_ids[slot];
                 RowTile<GB, GC, 2> tg, tu;
                 load_tile(tg, a.gate, e, lm, row0, a.I);
@@ -519,38 +592,62 @@ __global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
                     for (int i = 0; i < GRI; ++i) {
                         const int row = row0 + i * lm.rpw + lm.q;
                         if (row < a.I)
-                            put_pair(a.h_x + static_cast<int64_t>(slot) * a.I + row, swiglu(rg[i], ru[i]), g);
+                            put_pair_group(a.h_x + static_cast<int64_t>(slot) * a.I + row, swiglu(rg[i], ru[i]), g,
+                                           a.local);
                     }
                 }
             }
             count_done(&s_cnt[1], lane);
-            // ---- phase 3: down tiles ------------------------------------------
-            asm volatile("" : "+v"(lane));
-            down_tiles<DB>(a, dn_u, dn1, slot_lo, dt, false, g, lane, s_ids, s_hb, s_ready);
+        }
+        asm volatile("" : "+v"(lane));
+        if (dshare >= 0) {
+            // ---- routed down tiles of the group ---------------------------------
+#pragma unroll 1
+            for (int q = qd0; q < nqd; q += NPG * kDnShares) {
+                const int j = q / a.dn_tpe;
+                const int row0 = (q - j * a.dn_tpe) * DRI * lmd.rpw;
+                if (!(early && q == qd0)) load_tile(dt0, a.down, s_ids[grp + kGroups * j], lmd, row0, a.H);
+                wait_ready(&s_ready[j], a.err, lane);
+                down_dot<DB>(a, a.down, dt0, row0, grp + kGroups * j, s_hb[j], g, lane);
+            }
+        }
+        if (wave == kShWave && has_sh_tiles) {
+            // ---- the shared expert's down tiles ---------------------------------
+            const LaneMap lm = lane_map(a.sh_down.lpr_log2, lane);
+#pragma unroll 1
+            for (int q = b; q < a.dn_tpe_sh; q += NB) {
+                load_tile(dt0, a.sh_down, 0, lm, q * DRI * lm.rpw, a.H);
+                wait_ready(&s_ready[kShBuf], a.err, lane);
+                down_dot<DB>(a, a.sh_down, dt0, q * DRI * lm.rpw, a.K, s_hb[kShBuf], g, lane);
+            }
         }
         count_done(&s_cnt[2], lane);
     } else {
-        // ---- fetch: the activations this workgroup's down tiles read ---------
-        asm volatile("" : "+v"(lane));
-        wait_count(&s_cnt[1], kWorkWaves, a.err, lane);
-        if (slot_hi >= slot_lo) {
-            // routed slots are consecutive rows of h_x; the shared slot comes last
-            const int routed_hi = min(slot_hi, a.K - 1);
-            if (routed_hi >= slot_lo)
-                poll_pairs(a.h_x + static_cast<int64_t>(slot_lo) * a.I, (routed_hi - slot_lo + 1) * a.I, a.I,
-                           a.I, g, &s_hb[0][0], lane, a.err, kMaxInterFused);
-            if (slot_hi == a.K)
-                poll_pairs(a.hsh_x, a.Is, a.Is, 0, g, s_hb[a.K - slot_lo], lane, a.err, kMaxInterFused);
+        // ---- fetch the activations this workgroup's down tiles read ------------
+        if (has_sh_tiles) {
+            poll_pairs(a.hsh_x, a.Is, a.Is, 0, g, s_hb[kShBuf], lane, a.err);
+            if constexpr (DB == 4) convert_x2_lds(s_hb[kShBuf], a.Is, lane);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            if (lane < slot_hi - slot_lo + 1)
-                __hip_atomic_store(s_ready + lane, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (lane == 0) __hip_atomic_store(&s_ready[kShBuf], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        // routed: once this workgroup's own gate/up rows are out, the group's
+        // slots (rows grp, grp + kGroups, ... of h_x), one poll for all
+        wait_count(&s_cnt[1], kGuWaves, a.err, lane);
+        if (nsg > 0) {
+            poll_pairs(a.h_x + static_cast<int64_t>(grp) * a.I, nsg * a.I, a.I, kGroups * a.I, g, &s_hb[0][0], lane,
+                       a.err, kMaxInterFused);
+            if constexpr (DB == 4) {
+                for (int j = 0; j < nsg; ++j) convert_x2_lds(s_hb[j], a.I, lane);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane < nsg) __hip_atomic_store(&s_ready[lane], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         // ---- combine ------------------------------------------------------------
         const int r0 = b * a.rows_cmb;
         const int nr = min(a.rows_cmb, a.H - r0);
         if (nr > 0) {
             const int slots = a.K + (a.has_shared ? 1 : 0);
-            wait_count(&s_cnt[2], kWorkWaves, a.err, lane);
+            wait_count(&s_cnt[2], kAuxWave, a.err, lane);
             poll_pairs(a.part_x + r0, slots * nr, nr, a.H, g, s_cmb, lane, a.err);
             const float gate = a.has_shared ? sigmoidf_ref(sg) : 0.f;
             for (int rr = lane; rr < nr; rr += kWave) {
@@ -623,9 +720,25 @@ static FusedKernel fused_kernel_for(const QMat &gate, const QMat &down, int x_dt
     return nullptr;
 }
 
-// Workgroups of the fused launch on the current device: one per CU, provided
-// a workgroup fits a CU (so the grid is resident at once on an idle device);
-// 0 if not.  Cached per device and kernel.
+// Per device: whether the workgroups of each group (b % kGroups) of a grid
+// of one workgroup per CU run on one XCD (1), do not (0), or unknown (-1,
+// before the first swq_moe_workspace_init on the device).
+static int g_groups_local[64] = {-1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1,
+                                 -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1,
+                                 -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1,
+                                 -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1};
+
+__global__ __launch_bounds__(kFusedThreads) void xcd_probe_kernel(int32_t *out) {
+    if (threadIdx.x == 0) {
+        uint32_t v;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+        out[blockIdx.x] = static_cast<int32_t>(v & 0xFu);
+    }
+}
+
+// Workgroups of the fused launch on the current device: one per CU (rounded
+// down to whole groups), provided a workgroup fits a CU, so the grid is
+// resident at once on an idle device; 0 if not.  Cached per device and kernel.
 static int fused_blocks(FusedKernel k) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
@@ -637,7 +750,7 @@ static int fused_blocks(FusedKernel k) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(k), kFusedThreads, 0) !=
         hipSuccess)
         return 0;
-    const int n = per_cu >= 1 ? min(cus, kFusedMaxBlocks) : 0;
+    const int n = per_cu >= 1 ? min(cus, kFusedMaxBlocks) / kGroups * kGroups : 0;
     cached_n[dev] = n;
     cached_k[dev] = k;
     return n;
@@ -696,14 +809,8 @@ static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch
     a.gu_tiles = a.K * a.gu_tpe;
     a.dn_tpe = (H + tile_rows(a.down) - 1) / tile_rows(a.down);
     a.dn_tpe_sh = a.has_shared ? (H + tile_rows(a.sh_down) - 1) / tile_rows(a.sh_down) : 0;
-    a.dn_tiles = a.K * a.dn_tpe + a.dn_tpe_sh;
-    a.dn_per_blk = (a.dn_tiles + blocks - 1) / blocks;
-    // every workgroup's down tiles must span at most kMaxBlkSlots slots
-    auto slot_of = [&](int u) { return u < a.K * a.dn_tpe ? u / a.dn_tpe : a.K; };
-    for (int blk = 0; blk < blocks; ++blk) {
-        const int u0 = blk * a.dn_per_blk, u1 = min(u0 + a.dn_per_blk, a.dn_tiles);
-        if (u0 < u1 && slot_of(u1 - 1) - slot_of(u0) + 1 > kMaxBlkSlots) return nullptr;
-    }
+    int dev = 0;
+    a.local = (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && g_groups_local[dev] == 1) ? 1 : 0;
     *fa = a;
     *nb = blocks;
     return kern;
@@ -743,5 +850,34 @@ int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int bat
 }
 
 size_t fused_err_offset(const swq_moe_layer *l, size_t base) { return fused_layout(l, base).err; }
+
+// Records, once per device, whether a grid of one workgroup per CU places
+// every group's workgroups on one XCD: a launch of that grid reports each
+// workgroup's XCC_ID.  Blocking; runs on `stream`.
+int fused_probe_device(hipStream_t stream) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return SWQ_ERR_HIP;
+    if (g_groups_local[dev] >= 0) return SWQ_OK;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return SWQ_ERR_HIP;
+    const int n = min(cus, kFusedMaxBlocks) / kGroups * kGroups;
+    if (n < kGroups) {
+        g_groups_local[dev] = 0;
+        return SWQ_OK;
+    }
+    int32_t *d = nullptr;
+    if (hipMalloc(&d, n * sizeof(int32_t)) != hipSuccess) return SWQ_ERR_HIP;
+    hipLaunchKernelGGL(xcd_probe_kernel, dim3(n), dim3(kFusedThreads), 0, stream, d);
+    int32_t h[kFusedMaxBlocks];
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipMemcpyAsync(h, d, n * sizeof(int32_t), hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    hipFree(d);
+    if (e != hipSuccess) return SWQ_ERR_HIP;
+    int ok = 1;
+    for (int i = kGroups; i < n; ++i) ok &= h[i] == h[i % kGroups];
+    g_groups_local[dev] = ok;
+    return SWQ_OK;
+}
 
 }  // namespace swq

@@ -88,6 +88,7 @@ inline int check_layer(const swq_moe_layer *l, int B, int x_dtype) {
 // batch and the device allow (*taken), else leaves the work to the caller.
 size_t fused_ws_bytes(const swq_moe_layer *l, size_t base);
 size_t fused_err_offset(const swq_moe_layer *l, size_t base);
+int fused_probe_device(hipStream_t stream);
 int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int batch, void *out, int out_dtype,
                  int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes, size_t staged_bytes,
                  bool accumulate, hipStream_t stream, bool *taken);

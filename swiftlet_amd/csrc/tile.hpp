@@ -8,12 +8,17 @@
 // reads LPR consecutive chunks per row.  RI = 4/CPL passes, so every lane
 // holds four 16-byte code chunks per tile.
 //
-// Two activation formats:
-//   kXF32   fp32 registers; codes go through v_cvt_f32_ubyteN and an fma.
-//   kXBF16  (4-bit codes, bf16 activations) packed bf16 pairs; each nibble
-//           becomes the bf16 value 128+q with one and-or, and v_dot2c_f32_bf16
-//           accumulates two exact products into fp32.  The 128 offset is
-//           removed through the bias: s*q + b = s*(128+q) + (b - 128*s).
+// Three activation formats:
+//   kXF32    fp32 registers; codes go through v_cvt_f32_ubyteN and an fma.
+//   kXBF16   (4-bit codes, bf16 activations) packed bf16 pairs; each nibble
+//            becomes the bf16 value 128+q with one and-or, and
+//            v_dot2c_f32_bf16 accumulates two exact products into fp32.  The
+//            128 offset is removed through the bias:
+//            s*q + b = s*(128+q) + (b - 128*s).
+//   kXBF16X2 (4-bit codes, fp32 activations) each activation split into
+//            hi = bf16(x) and lo = bf16(x - hi), both round-to-nearest-even,
+//            so hi + lo carries 16 significant bits (relative error at most
+//            2^-18); two dot2 per code pair, products still exact.
 //
 // Loads are branch-free: row and chunk indices are clamped to valid ones (the
 // caller drops results of rows past the end; chunks past a row's end get zero
@@ -28,6 +33,7 @@ namespace swq {
 
 constexpr int kXF32 = 0;
 constexpr int kXBF16 = 1;
+constexpr int kXBF16X2 = 2;
 
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 
@@ -90,9 +96,62 @@ struct XSlice<4, CPL, kXBF16> {
     float sum[CPL];
 };
 
+template <int CPL>
+struct XSlice<4, CPL, kXBF16X2> {
+    uint32_t hi[CPL][16];  // pairs {hi[8k+m], hi[8k+m+4]} for word k, m = 0..3
+    uint32_t lo[CPL][16];  // the same pairs of lo
+    float sum[CPL];
+};
+
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
                                            false);
+}
+
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+
+// hi = bf16(x0) | bf16(x1) << 16 and lo the same of the remainders
+// x - float(hi), all round-to-nearest-even (v_cvt_pk_bf16_f32); the
+// remainders are exact in fp32.
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t &hi, uint32_t &lo) {
+    const f32x2_t v = {x0, x1};
+    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+    const f32x2_t r = {x0 - __uint_as_float(hi << 16), x1 - __uint_as_float(hi & 0xFFFF0000u)};
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2_t));
+}
+
+// Sum of a 4-bit chunk's activations from its pair words, in a fixed order
+// (every path that holds the same pairs gets the same sum).
+__device__ __forceinline__ float pair_sum(const uint32_t *hi, const uint32_t *lo) {
+    float s[4] = {0.f, 0.f, 0.f, 0.f}, t[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            s[m] = dot2_bf16(hi[4 * k + m], 0x3F803F80u, s[m]);
+            t[m] = dot2_bf16(lo[4 * k + m], 0x3F803F80u, t[m]);
+        }
+    }
+    return ((s[0] + s[1]) + (s[2] + s[3])) + ((t[0] + t[1]) + (t[2] + t[3]));
+}
+
+// 32 fp32 activations of a 4-bit chunk -> pair words {x[8k+m], x[8k+m+4]}
+// (word 4k+m) of hi and lo, and the chunk's sum.
+__device__ __forceinline__ void pack_chunk_x2(const float *v, uint32_t *hi, uint32_t *lo, float &sum) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) split_pair(v[8 * k + m], v[8 * k + m + 4], hi[4 * k + m], lo[4 * k + m]);
+    }
+    sum = pair_sum(hi, lo);
+}
+
+// (v & mask) | magic in one VOP3 (the compiler otherwise emits two VOP2s
+// with literal operands).
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t magic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "v"(mask), "v"(magic));
+    return r;
 }
 
 template <int XDT, int BITS, int CPL, int XF>
@@ -112,6 +171,16 @@ __device__ __forceinline__ void load_xslice(XSlice<BITS, CPL, XF> &xs, const QMa
             for (int i = 0; i < kCPC; ++i) s += xs.v[t][i];
             xs.sum[t] = s;
         }
+    } else if constexpr (XF == kXBF16X2) {
+        static_assert(XDT == 0 && BITS == 4, "split bf16 activations need fp32 x and 4-bit codes");
+        float v[CPL][32];
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) {
+            const int c = min(lm.j + t * lm.lpr, m.chunks - 1);
+            load_x<XDT>(v[t], x, x_base + static_cast<int64_t>(c) * kCPC);
+        }
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) pack_chunk_x2(v[t], xs.hi[t], xs.lo[t], xs.sum[t]);
     } else {
         static_assert(XDT == 2 && BITS == 4, "packed bf16 activations need bf16 x and 4-bit codes");
         const uint16_t *xp = static_cast<const uint16_t *>(x) + x_base;
@@ -148,12 +217,35 @@ __device__ __forceinline__ float dot_chunk_q4_bf16(const uint4 w, const uint32_t
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const uint32_t v = ws[k];
-        a0 = dot2_bf16((v & 0x000F000Fu) | 0x43004300u, xp[4 * k + 0], a0);          // {q0, q4}
-        a1 = dot2_bf16(((v >> 4) & 0x000F000Fu) | 0x43004300u, xp[4 * k + 1], a1);   // {q1, q5}
-        a0 = dot2_bf16(((v >> 8) & 0x000F000Fu) | 0x43004300u, xp[4 * k + 2], a0);   // {q2, q6}
-        a1 = dot2_bf16(((v >> 12) & 0x000F000Fu) | 0x43004300u, xp[4 * k + 3], a1);  // {q3, q7}
+        a0 = dot2_bf16(and_or(v, 0x000F000Fu, 0x43004300u), xp[4 * k + 0], a0);          // {q0, q4}
+        a1 = dot2_bf16(and_or(v >> 4, 0x000F000Fu, 0x43004300u), xp[4 * k + 1], a1);   // {q1, q5}
+        a0 = dot2_bf16(and_or(v >> 8, 0x000F000Fu, 0x43004300u), xp[4 * k + 2], a0);   // {q2, q6}
+        a1 = dot2_bf16(and_or(v >> 12, 0x000F000Fu, 0x43004300u), xp[4 * k + 3], a1);  // {q3, q7}
     }
     return a0 + a1;
+}
+
+// sum_i (128 + q_i) * (hi_i + lo_i) over a chunk of 4-bit codes.
+__device__ __forceinline__ float dot_chunk_q4_bf16x2(const uint4 w, const uint32_t *hi, const uint32_t *lo) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;  // four independent chains
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t v = ws[k];
+        const uint32_t c0 = and_or(v, 0x000F000Fu, 0x43004300u);        // {q0, q4}
+        const uint32_t c1 = and_or(v >> 4, 0x000F000Fu, 0x43004300u);   // {q1, q5}
+        const uint32_t c2 = and_or(v >> 8, 0x000F000Fu, 0x43004300u);   // {q2, q6}
+        const uint32_t c3 = and_or(v >> 12, 0x000F000Fu, 0x43004300u);  // {q3, q7}
+        a0 = dot2_bf16(c0, hi[4 * k + 0], a0);
+        a1 = dot2_bf16(c1, hi[4 * k + 1], a1);
+        b0 = dot2_bf16(c0, lo[4 * k + 0], b0);
+        b1 = dot2_bf16(c1, lo[4 * k + 1], b1);
+        a0 = dot2_bf16(c2, hi[4 * k + 2], a0);
+        a1 = dot2_bf16(c3, hi[4 * k + 3], a1);
+        b0 = dot2_bf16(c2, lo[4 * k + 2], b0);
+        b1 = dot2_bf16(c3, lo[4 * k + 3], b1);
+    }
+    return (a0 + a1) + (b0 + b1);
 }
 
 // ---------------------------------------------------------------------------
@@ -216,20 +308,29 @@ __device__ __forceinline__ void load_tile(RowTile<BITS, CPL, ES> &rt, const QMat
 // res[i] = full dot product of row (row0 + i*rpw + q) with the activations,
 // valid in the row segment's last lane (j == LPR-1).
 //
-// The empty asm keeps the code unpacking inside the caller's token loop:
-// hoisted out of it, the unpacked codes of a tile would stay live across the
-// loop and spill.
+// The empty asm statements keep the code unpacking inside the caller's token
+// loop: hoisted out of it, the unpacked codes of a tile would stay live
+// across the loop and spill.  They all come first, so the passes' arithmetic
+// that follows can interleave.
 template <int BITS, int CPL, int ES, int XF>
 __device__ __forceinline__ void dot_tile(float (&res)[4 / CPL], const RowTile<BITS, CPL, ES> &rt,
                                          const XSlice<BITS, CPL, XF> &xs, const QMat &m, const LaneMap &lm) {
     constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
+    uint4 wt[RI][CPL];
+#pragma unroll
+    for (int i = 0; i < RI; ++i) {
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) {
+            wt[i][t] = rt.w[i][t];
+            asm volatile("" : "+v"(wt[i][t].x), "+v"(wt[i][t].y), "+v"(wt[i][t].z), "+v"(wt[i][t].w));
+        }
+    }
 #pragma unroll
     for (int i = 0; i < RI; ++i) {
         float acc = 0.f;
 #pragma unroll
         for (int t = 0; t < CPL; ++t) {
-            uint4 w = rt.w[i][t];
-            asm volatile("" : "+v"(w.x), "+v"(w.y), "+v"(w.z), "+v"(w.w));
+            const uint4 w = wt[i][t];
             const bool live = lm.j + t * lm.lpr < m.chunks;
             const float sc = live ? scale_value<ES>(rt.s[i][t], m.stype) : 0.f;
             const float bi = live ? scale_value<ES>(rt.b[i][t], m.stype) : 0.f;
@@ -237,8 +338,12 @@ __device__ __forceinline__ void dot_tile(float (&res)[4 / CPL], const RowTile<BI
                 const float qd = dot_chunk<BITS>(w, xs.v[t]);
                 acc = fmaf(sc, qd, acc);
                 acc = fmaf(bi, xs.sum[t], acc);
-            } else {
+            } else if constexpr (XF == kXBF16) {
                 const float d = dot_chunk_q4_bf16(w, xs.p[t]);
+                acc = fmaf(sc, d, acc);
+                acc = fmaf(fmaf(-128.f, sc, bi), xs.sum[t], acc);
+            } else {
+                const float d = dot_chunk_q4_bf16x2(w, xs.hi[t], xs.lo[t]);
                 acc = fmaf(sc, d, acc);
                 acc = fmaf(fmaf(-128.f, sc, bi), xs.sum[t], acc);
             }
