@@ -36,6 +36,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 # each scaled by what the counter reads for a 256 MiB device copy (FETCH x 2.0, WRITE x 1.0);
 # the runs' commands and raw counts are kept with the kernel-trace summaries.  Keyed (workload, kernel).
 MEASURED_TRAFFIC = {
+    ("qwen3.6-35b-a3b-q4-b1", "moe_fused"): 18_163_424,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_692_148,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 14_590_849,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 5_743_112,

@@ -156,20 +156,27 @@ int swq_dequantize(const swq_qlinear *lin, int64_t row0, int64_t rows,
 /* Workspace bytes swq_moe_decode needs for `batch` tokens (0 on bad input). */
 size_t swq_moe_decode_workspace_bytes(const swq_moe_layer *layer, int batch);
 
-/* Prepare a fresh workspace (zeroes its completion counters).  Call once
- * after allocating it; swq_moe_decode leaves it ready for the next call. */
+/* Prepare a fresh workspace: zeroes it, and on the first call for the
+ * current device checks (one small blocking launch) whether the batch-1
+ * kernel's workgroup groups share an XCD.  Call once after allocating the
+ * workspace, outside stream capture; swq_moe_decode leaves it ready for the
+ * next call. */
 int swq_moe_workspace_init(void *ws, size_t ws_bytes, void *stream);
 
 /* One MoE-layer decode step for `batch` independent tokens, entirely on the
- * device, three kernel launches:
- *   1. router GEMV + shared-gate GEMV + shared gate/up SwiGLU, then (last
- *      workgroup) softmax, top-k (ties -> lower expert id), renormalisation;
- *   2. gate/up SwiGLU of every distinct selected expert, indexed by the
- *      device-resident top-k ids;
+ * device.  Batch 1 runs as one launch (router, softmax, top-k with ties to the
+ * lower expert id, renormalisation, routed SwiGLU experts, down projections,
+ * sigmoid-gated shared expert and the weighted combine; its stages hand data
+ * to each other through the workspace).  Batches run as three launches:
+ *   1. router GEMV + shared-gate GEMV + shared gate/up SwiGLU;
+ *   2. top-k per token, the distinct experts, their gate/up SwiGLU rows for
+ *      all their tokens, indexed by the device-resident ids;
  *   3. down projections + weighted combine + sigmoid-gated shared expert.
  * x: [batch, hidden] of x_dtype (SWQ_F32 / SWQ_BF16).  out: [batch, hidden]
  * of out_dtype (SWQ_F32 / SWQ_BF16).  topk_ids [batch, top_k] int32 and
  * topk_weights [batch, top_k] f32 receive the routing (either may be NULL).
+ * The workspace must come from swq_moe_workspace_init and serve one stream
+ * at a time.
  * Replaces QwenMetalModel.moeForward / routerPicks / encodePendingMoE
  * (QwenMetalModel.swift:609-716, 798-892) with the numerics of
  * QwenCPUModel.moeForward (QwenCPUModel.swift:500-569). */

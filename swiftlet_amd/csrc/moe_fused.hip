@@ -560,7 +560,11 @@ __global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
         const int qd0 = rank + NPG * dshare;
         const bool early = wave >= kGuWaves && dshare >= 0 && qd0 < nqd;
         if (early) {
-            // ---- the first routed down tile, loaded now and held ------------
+            // ---- the first routed down tile, held until the activations
+            // arrive.  Loaded once this workgroup's gate/up rows are in: the
+            // gate/up loads are on the critical path, the down tiles are
+            // needed only after the activations' round trip.
+            wait_count(&s_cnt[1], kGuWaves, a.err, lane);
             const int j = qd0 / a.dn_tpe;
             load_tile(dt0, a.down, s_ids[grp + kGroups * j], lmd, (qd0 - j * a.dn_tpe) * DRI * lmd.rpw, a.H);
             // Without this the compiler may sink the loads below the waits
