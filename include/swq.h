@@ -186,6 +186,37 @@ int swq_moe_decode(const swq_moe_layer *layer,
                    int32_t *topk_ids, float *topk_weights,
                    void *ws, size_t ws_bytes, int flags, void *stream);
 
+/* ---- MoE layer prefill ------------------------------------------------ */
+
+/* Workspace bytes swq_moe_prefill needs for `tokens` tokens; 0 on bad input
+ * or a layer outside the prefill formats (below). */
+size_t swq_moe_prefill_workspace_bytes(const swq_moe_layer *layer, int tokens);
+
+/* The MoE layer over a chunk of `tokens` tokens (a prompt), each token routed
+ * on its own exactly as in swq_moe_decode, with the (token, expert) pairs
+ * grouped by expert so each expert's weights are contracted against all of
+ * its tokens at once on the bf16 matrix cores (codes exact in bf16, fp32
+ * accumulation, per-group scales applied in fp32).  Five launches: router
+ * GEMM; top-k + grouping; gate/up + SwiGLU; down; weighted combine in pick
+ * order, then the sigmoid-gated shared expert.
+ * Formats: 4/8-bit codes with group 64 for the router, routed and shared
+ * matrices; in_dim a multiple of 128 and at most 4096; the shared gate/up and
+ * down matrices with the routed ones' bit widths.  Others: SWQ_ERR_LIMIT.
+ * x: [tokens, hidden] of x_dtype (SWQ_F32 / SWQ_BF16); out: [tokens, hidden]
+ * of out_dtype; topk_ids / topk_weights: [tokens, top_k] (either may be NULL).
+ * The workspace comes from swq_moe_workspace_init, sized by
+ * swq_moe_prefill_workspace_bytes, and is left ready for the next call; it is
+ * not shared with swq_moe_decode.
+ * Replaces the per-token loop of QwenMetalModel.step (QwenMetalModel.swift:359-366)
+ * with the grouped form of mlx's SwitchGLU (switch_layers.py:12-24, 75-90,
+ * 176-199) and the numerics of QwenCPUModel.moeForward for S tokens
+ * (QwenCPUModel.swift:500-569). */
+int swq_moe_prefill(const swq_moe_layer *layer,
+                    const void *x, int x_dtype, int tokens,
+                    void *out, int out_dtype,
+                    int32_t *topk_ids, float *topk_weights,
+                    void *ws, size_t ws_bytes, int flags, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,6 +52,15 @@ int swq_moe_decode_stages(const swq_moe_layer *layer, const void *x, int x_dtype
  * sets nonzero if one of its bounded waits ran out (0 on bad input). */
 size_t swq_moe_workspace_error_offset(const swq_moe_layer *layer, int batch);
 
+/* swq_moe_prefill with logit_bias[e] (device, [num_experts] f32) added to
+ * every token's router logit of expert e before the softmax: the synthetic
+ * skewed-load workload, whose per-expert token counts follow a chosen
+ * distribution.  The reference has no such bias; with all entries 0 the
+ * result equals swq_moe_prefill's. */
+int swq_moe_prefill_biased(const swq_moe_layer *layer, const void *x, int x_dtype, int tokens, void *out,
+                           int out_dtype, int32_t *topk_ids, float *topk_weights, const float *logit_bias,
+                           void *ws, size_t ws_bytes, int flags, void *stream);
+
 /* One single-wave kernel that sleeps `iterations` times (s_sleep 127, about
  * 8k cycles each) and exits; iterations <= 1000000. */
 int swq_bench_stall(int iterations, void *stream);

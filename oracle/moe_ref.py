@@ -268,8 +268,13 @@ class MoELayerRef:
         return self.router.out_dim
 
 
-def moe_forward(x: np.ndarray, layer: MoELayerRef, dtype=np.float32):
+def moe_forward(x: np.ndarray, layer: MoELayerRef, dtype=np.float32, logit_bias=None):
     """QwenCPUModel.moeForward (QwenCPUModel.swift:500-569) for S tokens.
+
+    ``logit_bias`` ([E] f32, optional) is added to every token's router
+    logits before the softmax: the synthetic skewed-load workload of the
+    prefill benchmark, with no counterpart in the reference (None = the
+    reference's computation).
 
     Returns (out [S, H], picks per token, combine weights [S, K]).
     With dtype=np.float32 this follows the reference's f32 arithmetic; with
@@ -280,8 +285,9 @@ def moe_forward(x: np.ndarray, layer: MoELayerRef, dtype=np.float32):
     x = np.atleast_2d(np.asarray(x, dtype=np.float32))
     S, H = x.shape
     K = layer.top_k
-    router = (x.astype(dtype) @ layer.router_dense.T.astype(dtype))      # :506
-    router32 = (x @ layer.router_dense.T).astype(np.float32)
+    router32 = (x @ layer.router_dense.T).astype(np.float32)            # :506
+    if logit_bias is not None:
+        router32 = router32 + np.asarray(logit_bias, dtype=np.float32)
     picks_per_row = []
     for s in range(S):                                                   # :508-522
         p = softmax_row(router32[s])
@@ -334,13 +340,16 @@ def _silu(v, dtype):
     return v / (1.0 + np.exp(-v))
 
 
-def router_margin(x: np.ndarray, layer: MoELayerRef) -> np.ndarray:
-    """Per token: float64 gap between the k-th and (k+1)-th router logits.
+def router_margin(x: np.ndarray, layer: MoELayerRef, logit_bias=None) -> np.ndarray:
+    """Per token: float64 gap between the k-th and (k+1)-th router logits
+    (plus ``logit_bias`` as in moe_forward).
 
     Expert selection is compared bit for bit only where this margin exceeds
     the f32 summation-order noise of the router GEMV."""
     x = np.atleast_2d(np.asarray(x, dtype=np.float64))
     l = x @ layer.router_dense.T.astype(np.float64)
+    if logit_bias is not None:
+        l = l + np.asarray(logit_bias, dtype=np.float32).astype(np.float64)
     srt = -np.sort(-l, axis=1)
     K = layer.top_k
     if K >= l.shape[1]:

@@ -84,6 +84,9 @@ SIGNATURES = {
     "swq_moe_decode_stages": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _I, _I, _P]),
     "swq_bench_stall": (_I, [_I, _P]),
     "swq_moe_workspace_error_offset": (_SZ, [_c.POINTER(MoELayer), _I]),
+    "swq_moe_prefill_workspace_bytes": (_SZ, [_c.POINTER(MoELayer), _I]),
+    "swq_moe_prefill": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _I, _P]),
+    "swq_moe_prefill_biased": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _P, _SZ, _I, _P]),
 }
 
 _lib = None

@@ -1,0 +1,993 @@
+// Ragged MoE prefill on gfx950: the layer of QwenCPUModel.moeForward
+// (QwenCPUModel.swift:500-569) applied to S tokens at once.  The (token,
+// expert) pairs are grouped by expert, so each expert's weights are read once
+// per tile of up to 64 of its tokens and contracted on the bf16 matrix cores.
+// The grouping follows mlx's _gather_sort / gather_qmm / _scatter_unsort
+// (switch_layers.py:12-24, 75-90, 176-199); the arithmetic follows the CPU
+// path, which loops the same per-token computation (QwenCPUModel.swift:544-567).
+//
+// Launches, all on the caller's stream:
+//   1. router GEMM: logits[T, E], 16-token tiles;
+//   2. route: softmax, top-k (ties to the lower id), renormalisation, the
+//      shared-expert gate logit, per-expert pair counts; the last workgroup
+//      to finish turns the counts into the sorted pair order and the table
+//      of 64-row tiles (routed experts, then the shared expert over all
+//      tokens), and leaves the counters at zero for the next call;
+//   3. gate/up GEMM over the tile table with the SwiGLU epilogue: h in
+//      sorted pair order, as bf16 hi + lo planes;
+//   4. down GEMM over the same tiles: y rows (f32) in sorted pair order;
+//   5. combine: out[t] = sum_k w_tk y[pos(t,k)] in pick order, then
+//      + sigmoid(sg_t) y_shared[t] (QwenCPUModel.swift:556, :566).
+//
+// Quantised contraction on the matrix cores.  For output n, input group g
+// (64 inputs) and activation row m, with w = s*q + b:
+//   y[m,n] = sum_g s[n,g] * C_g[m,n] + sum_g b'[n,g] * X_g[m]
+//   C_g[m,n] = sum_{i in g} c_i * a[m,i],   X_g[m] = sum_{i in g} a[m,i]
+// where c = 16 + q, b' = b - 16 s for 4-bit codes (the bf16 bit pattern
+// 0x4180 | q << 3 is 16 + q, built two codes per shift and and-or; the small
+// offset keeps the cancellation between the two terms to a few bits), and
+// c = q, b' = b for 8-bit codes.  The codes are exact in bf16; activations are bf16 (exact)
+// or split into bf16 hi + lo (fp32 inputs, the SwiGLU output), one MFMA per
+// part.  Every product is exact and accumulates in fp32, the scale applies
+// per group in fp32, and the bias term is one more MFMA chain over the group
+// axis with both factors split hi + lo.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "moe_host.hpp"
+#include "route.hpp"
+
+namespace swq {
+namespace {
+
+constexpr int kPfThreads = 256;  // 4 waves
+constexpr int kGroupK = 64;      // the quantisation group: one MFMA pair of k = 32
+constexpr int kLdsPitch = 72;    // bf16 per staged row: 64 + 8 (144 B rows, conflict-free b128 reads)
+constexpr int kMaxGroups = 64;   // inputs per row <= 4096
+constexpr int kXsPitch = kMaxGroups + 4;
+constexpr int kTileRows = 64;    // rows of a routed / shared tile
+constexpr int kRouterRows = 16;  // rows of a router tile
+constexpr int kRouteWaves = 4;   // tokens per route workgroup
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
+
+enum { kSrcBF16 = 0, kSrcF32 = 1, kSrcSplit = 2 };
+enum { kEpiRows = 0, kEpiSwiGLU = 1 };
+
+struct Tile {
+    int32_t expert;  // 0..E-1, or E for the shared expert
+    int32_t row0;    // first row in sorted pair order
+    int32_t rows;    // 1..64
+    int32_t pad;
+};
+
+struct GemmArgs {
+    QMat m[2];                // routed matrices of B operands 0 and 1 (stacked over experts)
+    QMat sh[2];               // shared-expert matrices (tiles with expert == E)
+    const void *a0;           // activation rows: x, or the h hi plane
+    const void *a1;           // the h lo plane
+    const int32_t *row_src;   // tile row -> activation row; null: the tile row itself
+    const Tile *tiles;        // null: dense tiles of 16*MT rows over rows_total
+    const int32_t *n_tiles;
+    void *o0, *o1;            // outputs: rows (f32), or h hi / lo planes (bf16)
+    int64_t a_ld, o_ld;       // elements per activation / output row
+    int32_t K, Ksh;           // inputs of the routed / shared matrices
+    int32_t N, Nsh;           // outputs of the routed / shared matrices
+    int32_t E;                // tiles with this expert id use `sh` (-1: none)
+    int32_t rows_total;       // dense tiles: rows; table tiles: rows of the sorted order
+    int32_t a_rows;           // rows of the activation source
+    int32_t nblk;             // column blocks per tile
+    int32_t col_block, col_wave, col_op;  // output column of block / wave / operand steps
+};
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__device__ __forceinline__ f32x4_t mfma(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float scale_of(uint32_t raw, int stype) {
+    if (stype == 1) return f16_to_f32(static_cast<uint16_t>(raw));
+    if (stype == 2) return bf16_to_f32(static_cast<uint16_t>(raw));
+    return __uint_as_float(raw);
+}
+
+__device__ __forceinline__ uint32_t scale_raw(const uint8_t *base, int64_t idx, int stype) {
+    if (stype == 0) return *reinterpret_cast<const uint32_t *>(base + idx * 4);
+    return *reinterpret_cast<const uint16_t *>(base + idx * 2);
+}
+
+// Eight natural-order bf16 (pairs d0 = {x0,x1} .. d3 = {x6,x7}) reordered to
+// {x0,x4},{x1,x5},{x2,x6},{x3,x7}: the order in which a 4-bit code word
+// yields its codes two at a time (nibbles j and j+4 of `v >> 4j`).
+__device__ __forceinline__ u32x4_t nibble_order(u32x4_t d) {
+    u32x4_t o;
+    o[0] = (d[0] & 0xFFFFu) | (d[2] << 16);
+    o[1] = (d[0] >> 16) | (d[2] & 0xFFFF0000u);
+    o[2] = (d[1] & 0xFFFFu) | (d[3] << 16);
+    o[3] = (d[1] >> 16) | (d[3] & 0xFFFF0000u);
+    return o;
+}
+
+__device__ __forceinline__ uint32_t and_or_u32(uint32_t v, uint32_t mask, uint32_t magic) {
+    return (v & mask) | magic;
+}
+
+// 8 codes of one 4-bit word as bf16 (16 + q: the code in the top four
+// mantissa bits of 16.0), in nibble_order.
+__device__ __forceinline__ u32x4_t codes_q4(uint32_t w) {
+    u32x4_t o;
+    o[0] = and_or_u32(w << 3, 0x00780078u, 0x41804180u);
+    o[1] = and_or_u32(w >> 1, 0x00780078u, 0x41804180u);
+    o[2] = and_or_u32(w >> 5, 0x00780078u, 0x41804180u);
+    o[3] = and_or_u32(w >> 9, 0x00780078u, 0x41804180u);
+    return o;
+}
+
+// Two bytes of an 8-bit word as a bf16 pair (exact: q < 256 has 8 bits).
+__device__ __forceinline__ uint32_t byte_pair_bf16(uint32_t w, int b0) {
+    const float f0 = static_cast<float>((w >> (8 * b0)) & 0xFFu);
+    const float f1 = static_cast<float>((w >> (8 * b0 + 8)) & 0xFFu);
+    return (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+}
+
+// 8 codes of two 8-bit words as bf16, natural order.
+__device__ __forceinline__ u32x4_t codes_q8(uint32_t w0, uint32_t w1) {
+    u32x4_t o;
+    o[0] = byte_pair_bf16(w0, 0);
+    o[1] = byte_pair_bf16(w0, 2);
+    o[2] = byte_pair_bf16(w1, 0);
+    o[3] = byte_pair_bf16(w1, 2);
+    return o;
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+// Eight fp32 values as bf16 hi and lo pairs (natural order).
+__device__ __forceinline__ void split8(const float (&v)[8], u32x4_t &hi, u32x4_t &lo) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t h, l;
+        split_pair(v[2 * i], v[2 * i + 1], h, l);
+        hi[i] = h;
+        lo[i] = l;
+    }
+}
+
+// Eight fp32 values as three bf16 parts hi + mid + lo (24 significant bits):
+// the group sums of the bias term, which cancels against the scaled codes.
+__device__ __forceinline__ void split8x3(const float (&v)[8], u32x4_t &hi, u32x4_t &mid, u32x4_t &lo) {
+    float r[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t h, m;
+        split_pair(v[2 * i], v[2 * i + 1], h, m);
+        hi[i] = h;
+        r[2 * i] = v[2 * i] - bf16_lo(h);
+        r[2 * i + 1] = v[2 * i + 1] - bf16_hi(h);
+    }
+    split8(r, mid, lo);
+}
+
+// ---------------------------------------------------------------------------
+// the grouped quantised GEMM
+
+// One staged group (64 inputs) of this thread's pieces: piece p = tid + 256 i
+// is row p / 8, inputs 8 (p % 8) .. +7 of the group.
+template <int SRC, int PPT>
+struct AStage {
+    u32x4_t v[PPT][SRC == kSrcBF16 ? 1 : 2];
+};
+
+template <int BITS>
+struct BSlot {
+    uint32_t w[2][BITS == 4 ? 2 : 4];  // operand j: the lane's code words of the group
+    uint32_t s[2];                     // operand j: the raw scale of (row, group)
+};
+
+template <int BITS, int SRC, int MT, int EPI>
+__global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
+    constexpr int ROWS = 16 * MT;
+    constexpr int NPL = SRC == kSrcBF16 ? 1 : 2;
+    constexpr int PIECES = ROWS * 8;
+    constexpr int PPT = (PIECES + kPfThreads - 1) / kPfThreads;
+    __shared__ __attribute__((aligned(16))) uint16_t s_a[2][NPL][ROWS * kLdsPitch];
+    __shared__ __attribute__((aligned(16))) float s_xs[ROWS * kXsPitch];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, kg = lane >> 4;
+
+    const int wi = blockIdx.x;
+    const int ti = wi / a.nblk, nb = wi - ti * a.nblk;
+    int expert = 0, row0, rows;
+    if (a.tiles) {
+        if (ti >= *a.n_tiles) return;
+        const Tile t = a.tiles[ti];
+        expert = t.expert;
+        row0 = t.row0;
+        rows = t.rows;
+        // a table from a workspace that skipped swq_moe_workspace_init
+        if (expert < 0 || expert > a.E || rows <= 0 || rows > ROWS || row0 < 0 || row0 + rows > a.rows_total)
+            return;
+    } else {
+        row0 = ti * ROWS;
+        rows = min(ROWS, a.rows_total - row0);
+    }
+    const bool shared = expert == a.E;
+    const int K = shared ? a.Ksh : a.K;
+    const int N = shared ? a.Nsh : a.N;
+    const int NG = K / kGroupK;
+    const int NG32 = (NG + 31) & ~31;
+    const int wcol = nb * a.col_block + wave * a.col_wave;
+    const bool active = wcol < N;
+
+    // ---- B operands: matrix row R_j of this lane, clamped into the matrix
+    const uint8_t *wrow[2];
+    const uint8_t *sbase[2];
+    const uint8_t *bbase[2];
+    int64_t srow[2];
+    int col[2];
+    int stype[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const QMat &m = shared ? a.sh[j] : a.m[j];
+        stype[j] = m.stype;
+        col[j] = wcol + j * a.col_op + n;
+        const int R = min(col[j], N - 1);
+        const int64_t eoff_w = shared ? 0 : static_cast<int64_t>(expert) * m.stride_w;
+        const int64_t eoff_s = shared ? 0 : static_cast<int64_t>(expert) * m.stride_sb;
+        wrow[j] = m.w + eoff_w + static_cast<int64_t>(R) * m.row_bytes + (BITS == 4 ? 8 : 16) * kg;
+        sbase[j] = m.s + eoff_s;
+        bbase[j] = m.b + eoff_s;
+        srow[j] = static_cast<int64_t>(R) * m.gpr;
+    }
+
+    auto load_b = [&](BSlot<BITS> &sl, int g) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if constexpr (BITS == 4) {
+                const uint2 v = *reinterpret_cast<const uint2 *>(wrow[j] + 32 * g);
+                sl.w[j][0] = v.x;
+                sl.w[j][1] = v.y;
+            } else {
+                const uint4 v = *reinterpret_cast<const uint4 *>(wrow[j] + 64 * g);
+                sl.w[j][0] = v.x;
+                sl.w[j][1] = v.y;
+                sl.w[j][2] = v.z;
+                sl.w[j][3] = v.w;
+            }
+            sl.s[j] = scale_raw(sbase[j], srow[j] + g, stype[j]);
+        }
+    };
+
+    // ---- A staging
+    int64_t src[PPT];
+    bool pok[PPT];
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+        const int p = tid + kPfThreads * i;
+        const int r = p >> 3;
+        pok[i] = p < PIECES && r < rows;
+        int64_t s = 0;
+        if (pok[i]) s = min(max(a.row_src ? a.row_src[row0 + r] : row0 + r, 0), a.a_rows - 1);
+        src[i] = s * a.a_ld + 8 * (p & 7);
+    }
+
+    auto load_a = [&](AStage<SRC, PPT> &st, int g) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            if (!pok[i]) continue;
+            const int64_t e = src[i] + kGroupK * g;
+            if constexpr (SRC == kSrcBF16) {
+                st.v[i][0] = *reinterpret_cast<const u32x4_t *>(static_cast<const uint16_t *>(a.a0) + e);
+            } else if constexpr (SRC == kSrcF32) {
+                const float *p = static_cast<const float *>(a.a0) + e;
+                st.v[i][0] = *reinterpret_cast<const u32x4_t *>(p);
+                st.v[i][1] = *reinterpret_cast<const u32x4_t *>(p + 4);
+            } else {
+                st.v[i][0] = *reinterpret_cast<const u32x4_t *>(static_cast<const uint16_t *>(a.a0) + e);
+                st.v[i][1] = *reinterpret_cast<const u32x4_t *>(static_cast<const uint16_t *>(a.a1) + e);
+            }
+        }
+    };
+
+    auto store_a = [&](const AStage<SRC, PPT> &st, int buf, int g) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int p = tid + kPfThreads * i;
+            if (p >= PIECES) continue;  // whole waves
+            const int r = p >> 3, c8 = p & 7;
+            u32x4_t hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
+            float sum = 0.f;
+            if (pok[i]) {
+                if constexpr (SRC == kSrcBF16) {
+                    hi = st.v[i][0];
+                    float t[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) t[q] = bf16_lo(hi[q]) + bf16_hi(hi[q]);
+                    sum = (t[0] + t[1]) + (t[2] + t[3]);
+                } else if constexpr (SRC == kSrcF32) {
+                    float v[8];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        v[q] = __uint_as_float(st.v[i][0][q]);
+                        v[4 + q] = __uint_as_float(st.v[i][1][q]);
+                    }
+                    split8(v, hi, lo);
+                } else {
+                    hi = st.v[i][0];
+                    lo = st.v[i][1];
+                }
+                if constexpr (SRC != kSrcBF16) {
+                    float t[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        t[q] = (bf16_lo(hi[q]) + bf16_lo(lo[q])) + (bf16_hi(hi[q]) + bf16_hi(lo[q]));
+                    sum = (t[0] + t[1]) + (t[2] + t[3]);
+                }
+            }
+            if constexpr (BITS == 4) {
+                hi = nibble_order(hi);
+                lo = nibble_order(lo);
+            }
+            *reinterpret_cast<u32x4_t *>(&s_a[buf][0][r * kLdsPitch + 8 * c8]) = hi;
+            if constexpr (NPL == 2) *reinterpret_cast<u32x4_t *>(&s_a[buf][1][r * kLdsPitch + 8 * c8]) = lo;
+            sum = segment_reduce(sum, 3);  // the 8 pieces of (row, group): 8 consecutive lanes
+            if (c8 == 0) s_xs[r * kXsPitch + g] = sum;
+        }
+    };
+
+    // zero the group-sum columns past NG that the bias MFMA reads
+    for (int i = tid; i < ROWS * (NG32 - NG); i += kPfThreads) {
+        const int r = i / (NG32 - NG), c = NG + i % (NG32 - NG);
+        s_xs[r * kXsPitch + c] = 0.f;
+    }
+
+    f32x4_t acc[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](const BSlot<BITS> &sl, int buf) {
+        if (!active) return;
+        u32x4_t bq[2][2];
+        float sc[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if constexpr (BITS == 4) {
+                bq[j][0] = codes_q4(sl.w[j][0]);
+                bq[j][1] = codes_q4(sl.w[j][1]);
+            } else {
+                bq[j][0] = codes_q8(sl.w[j][0], sl.w[j][1]);
+                bq[j][1] = codes_q8(sl.w[j][2], sl.w[j][3]);
+            }
+            sc[j] = scale_of(sl.s[j], stype[j]);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            if (16 * mt >= rows) break;
+            const uint16_t *ar = &s_a[buf][0][(16 * mt + n) * kLdsPitch + 16 * kg];
+            const u32x4_t a_0 = *reinterpret_cast<const u32x4_t *>(ar);
+            const u32x4_t a_1 = *reinterpret_cast<const u32x4_t *>(ar + 8);
+            u32x4_t l_0, l_1;
+            if constexpr (NPL == 2) {
+                const uint16_t *lr = &s_a[buf][1][(16 * mt + n) * kLdsPitch + 16 * kg];
+                l_0 = *reinterpret_cast<const u32x4_t *>(lr);
+                l_1 = *reinterpret_cast<const u32x4_t *>(lr + 8);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                f32x4_t c = mfma(a_0, bq[j][0], f32x4_t{0.f, 0.f, 0.f, 0.f});
+                c = mfma(a_1, bq[j][1], c);
+                if constexpr (NPL == 2) {
+                    c = mfma(l_0, bq[j][0], c);
+                    c = mfma(l_1, bq[j][1], c);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[mt][j][r] = fmaf(sc[j], c[r], acc[mt][j][r]);
+            }
+        }
+    };
+
+    // ---- the K loop: A two groups ahead (registers, then LDS), B two groups
+    // ahead (registers); NG is even
+    AStage<SRC, PPT> sx, sy;
+    BSlot<BITS> b0, b1;
+    load_a(sx, 0);
+    if (active) load_b(b0, 0);
+    load_a(sy, 1);
+    if (active) load_b(b1, 1);
+    store_a(sx, 0, 0);
+    __syncthreads();
+#pragma unroll 1
+    for (int g = 0; g < NG; g += 2) {
+        if (g + 2 < NG) load_a(sx, g + 2);
+        compute(b0, 0);
+        if (active && g + 2 < NG) load_b(b0, g + 2);
+        store_a(sy, 1, g + 1);
+        __syncthreads();
+        if (g + 3 < NG) load_a(sy, g + 3);
+        compute(b1, 1);
+        if (active && g + 3 < NG) load_b(b1, g + 3);
+        if (g + 2 < NG) store_a(sx, 0, g + 2);
+        __syncthreads();
+    }
+
+    if (!active) return;
+
+    // ---- bias term: sum_g b'[n,g] X_g[m] on the group axis.  b' is exact as
+    // bf16 hi + lo (an fp16 bias less 16 fp16 scales); X_g as hi + mid + lo.
+    // The five products above 2^-24 relative are accumulated.
+#pragma unroll 1
+    for (int g0 = 0; g0 < NG32; g0 += 32) {
+        u32x4_t bh[2], bl[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int gg = g0 + 8 * kg + i;
+                float bp = 0.f;
+                if (gg < NG) {
+                    const float bb = load_scale(bbase[j], srow[j] + gg, stype[j]);
+                    if constexpr (BITS == 4) {
+                        const float ss = load_scale(sbase[j], srow[j] + gg, stype[j]);
+                        bp = fmaf(-16.f, ss, bb);
+                    } else {
+                        bp = bb;
+                    }
+                }
+                v[i] = bp;
+            }
+            split8(v, bh[j], bl[j]);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            if (16 * mt >= rows) break;
+            const float *xr = &s_xs[(16 * mt + n) * kXsPitch + g0 + 8 * kg];
+            float v[8];
+            const float4 x0 = *reinterpret_cast<const float4 *>(xr);
+            const float4 x1 = *reinterpret_cast<const float4 *>(xr + 4);
+            v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+            v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+            u32x4_t xh, xm, xl;
+            split8x3(v, xh, xm, xl);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                acc[mt][j] = mfma(xl, bh[j], acc[mt][j]);
+                acc[mt][j] = mfma(xm, bl[j], acc[mt][j]);
+                acc[mt][j] = mfma(xm, bh[j], acc[mt][j]);
+                acc[mt][j] = mfma(xh, bl[j], acc[mt][j]);
+                acc[mt][j] = mfma(xh, bh[j], acc[mt][j]);
+            }
+        }
+    }
+
+    // ---- epilogue: lane holds column n of rows 16 mt + 4 kg + r
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        if (16 * mt >= rows) break;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 16 * mt + 4 * kg + r;
+            if (row >= rows) continue;
+            const int64_t o = static_cast<int64_t>(row0 + row) * a.o_ld;
+            if constexpr (EPI == kEpiSwiGLU) {
+                if (col[0] < N) {
+                    const float h = swiglu(acc[mt][0][r], acc[mt][1][r]);
+                    uint32_t hi, lo;
+                    split_pair(h, 0.f, hi, lo);
+                    static_cast<uint16_t *>(a.o0)[o + col[0]] = static_cast<uint16_t>(hi);
+                    static_cast<uint16_t *>(a.o1)[o + col[0]] = static_cast<uint16_t>(lo);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    if (col[j] < N) static_cast<float *>(a.o0)[o + col[j]] = acc[mt][j][r];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// routing and grouping
+
+struct RouteArgs {
+    QMat seg;                 // shared_expert_gate [1, H]
+    const void *x;
+    const float *logits;      // [T, E]
+    const float *bias;        // [E] added to the logits, or null
+    int32_t *ids;             // [T, K]
+    float *wts;               // [T, K]
+    int32_t *user_ids;
+    float *user_w;
+    float *sg;                // [T]
+    int32_t *slot;            // [T, K]: rank of the pair within its expert
+    int32_t *counts;          // [E]: zero on entry; left zero
+    uint32_t *done;           // finished workgroups: zero on entry; left zero
+    int32_t *pos;             // [T, K]: sorted index of pair (t, k)
+    int32_t *tok;             // [P + T]: token of each sorted row
+    Tile *tiles;
+    int32_t *n_tiles;
+    int32_t T, E, K, H, norm, has_shared;
+};
+
+// <w_sg, x_t> over one row of any vector-path format (QwenCPUModel.swift:559).
+template <int XDT>
+__device__ float row_dot(const QMat &m, const void *x, int64_t x0, int lane) {
+    float acc = 0.f;
+    const int cpc = 128 / m.bits;
+    for (int c = lane; c < m.chunks; c += kWave) {
+        const uint4 w = *reinterpret_cast<const uint4 *>(m.w + 16 * static_cast<int64_t>(c));
+        const int g = (c * cpc) / m.group;
+        const float s = load_scale(m.s, g, m.stype), b = load_scale(m.b, g, m.stype);
+        float d, xs = 0.f;
+        if (m.bits == 4) {
+            float xv[32];
+            load_x<XDT, 32>(xv, x, x0 + static_cast<int64_t>(c) * 32);
+#pragma unroll
+            for (int i = 0; i < 32; ++i) xs += xv[i];
+            d = dot_chunk_q4(w, xv);
+        } else {
+            float xv[16];
+            load_x<XDT, 16>(xv, x, x0 + static_cast<int64_t>(c) * 16);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xs += xv[i];
+            d = dot_chunk_q8(w, xv);
+        }
+        acc += s * d + b * xs;
+    }
+    return wave_sum(acc);
+}
+
+// The last workgroup: exclusive scans of the pair counts and of the tile
+// counts, the tile table, the sorted pair order; then counters back to zero.
+__device__ void group_pairs(const RouteArgs &a) {
+    __shared__ int32_t s_off[kMaxExperts];
+    __shared__ int32_t s_cnt[kMaxExperts];
+    __shared__ int32_t s_part[2][kPfThreads];
+    const int tid = threadIdx.x;
+    constexpr int EPT = kMaxExperts / kPfThreads;  // experts per thread
+    int cnt[EPT], tl[EPT];
+    int csum = 0, tsum = 0;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int e = tid * EPT + i;
+        cnt[i] = e < a.E ? __hip_atomic_load(&a.counts[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+        tl[i] = (cnt[i] + kTileRows - 1) / kTileRows;
+        csum += cnt[i];
+        tsum += tl[i];
+    }
+    s_part[0][tid] = csum;
+    s_part[1][tid] = tsum;
+    __syncthreads();
+    // inclusive scan over the 256 partials (Hillis-Steele in LDS)
+    for (int d = 1; d < kPfThreads; d <<= 1) {
+        const int c = tid >= d ? s_part[0][tid - d] : 0;
+        const int t = tid >= d ? s_part[1][tid - d] : 0;
+        __syncthreads();
+        s_part[0][tid] += c;
+        s_part[1][tid] += t;
+        __syncthreads();
+    }
+    int c0 = s_part[0][tid] - csum, t0 = s_part[1][tid] - tsum;
+    const int routed_tiles = s_part[1][kPfThreads - 1];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int e = tid * EPT + i;
+        if (e < a.E) {
+            s_off[e] = c0;
+            s_cnt[e] = cnt[i];
+            for (int q = 0; q < tl[i]; ++q)
+                a.tiles[t0 + q] = Tile{e, c0 + q * kTileRows, min(kTileRows, cnt[i] - q * kTileRows), 0};
+            a.counts[e] = 0;
+        }
+        c0 += cnt[i];
+        t0 += tl[i];
+    }
+    const int P = a.T * a.K;
+    const int sh_tiles = a.has_shared ? (a.T + kTileRows - 1) / kTileRows : 0;
+    for (int q = tid; q < sh_tiles; q += kPfThreads)
+        a.tiles[routed_tiles + q] = Tile{a.E, P + q * kTileRows, min(kTileRows, a.T - q * kTileRows), 0};
+    if (tid == 0) {
+        *a.n_tiles = routed_tiles + sh_tiles;
+        *a.done = 0u;
+    }
+    __syncthreads();
+    for (int p = tid; p < P; p += kPfThreads) {
+        const int e = __hip_atomic_load(&a.ids[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int s = __hip_atomic_load(&a.slot[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (e < 0 || e >= a.E || s < 0 || s >= s_cnt[e]) continue;  // counters not zeroed on entry
+        const int q = s_off[e] + s;
+        if (q >= P) continue;
+        a.pos[p] = q;
+        a.tok[q] = p / a.K;
+    }
+    if (a.has_shared)
+        for (int t = tid; t < a.T; t += kPfThreads) a.tok[P + t] = t;
+}
+
+template <int XDT>
+__global__ __launch_bounds__(kPfThreads) void pf_route(const RouteArgs a) {
+    __shared__ float s_lg[kRouteWaves][kMaxExperts];
+    __shared__ int s_last;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.x * kRouteWaves + wave;
+    if (t < a.T) {
+        const float *lg = a.logits + static_cast<int64_t>(t) * a.E;
+        for (int e = lane; e < a.E; e += kWave) s_lg[wave][e] = a.bias ? lg[e] + a.bias[e] : lg[e];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        int32_t my_id;
+        float my_w;
+        topk_wave(s_lg[wave], a.E, a.K, a.norm, lane, my_id, my_w);
+        if (lane < a.K) {
+            const int64_t p = static_cast<int64_t>(t) * a.K + lane;
+            a.ids[p] = my_id;
+            a.wts[p] = my_w;
+            if (a.user_ids) a.user_ids[p] = my_id;
+            if (a.user_w) a.user_w[p] = my_w;
+            a.slot[p] = atomicAdd(&a.counts[my_id], 1);
+        }
+        if (a.has_shared) {
+            const float v = row_dot<XDT>(a.seg, a.x, static_cast<int64_t>(t) * a.H, lane);
+            if (lane == 0) a.sg[t] = v;
+        }
+    }
+    // the last workgroup to arrive groups the pairs
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    group_pairs(a);
+}
+
+// ---------------------------------------------------------------------------
+// combine
+
+struct CombineArgs {
+    const float *y;        // [P + T, H] in sorted pair order
+    const int32_t *pos;    // [T, K]
+    const float *wts;      // [T, K]
+    const float *sg;       // [T]
+    void *out;
+    int32_t T, K, H, odt, accumulate, has_shared;
+};
+
+__global__ __launch_bounds__(kPfThreads) void pf_combine(const CombineArgs a) {
+    __shared__ int32_t s_pos[SWQ_MAX_TOPK];
+    __shared__ float s_w[SWQ_MAX_TOPK];
+    const int t = blockIdx.x;
+    const int64_t P = static_cast<int64_t>(a.T) * a.K;
+    if (threadIdx.x < static_cast<unsigned>(a.K)) {
+        s_pos[threadIdx.x] = min(max(a.pos[t * a.K + threadIdx.x], 0), static_cast<int32_t>(P) - 1);
+        s_w[threadIdx.x] = a.wts[t * a.K + threadIdx.x];
+    }
+    __syncthreads();
+    const float gate = a.has_shared ? sigmoidf_ref(a.sg[t]) : 0.f;
+    for (int c = 4 * threadIdx.x; c < a.H; c += 4 * kPfThreads) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < a.K; ++k) {
+            const float4 v = *reinterpret_cast<const float4 *>(a.y + static_cast<int64_t>(s_pos[k]) * a.H + c);
+            acc[0] += s_w[k] * v.x;
+            acc[1] += s_w[k] * v.y;
+            acc[2] += s_w[k] * v.z;
+            acc[3] += s_w[k] * v.w;
+        }
+        if (a.has_shared) {
+            const float4 v = *reinterpret_cast<const float4 *>(a.y + (P + t) * a.H + c);
+            acc[0] += gate * v.x;
+            acc[1] += gate * v.y;
+            acc[2] += gate * v.z;
+            acc[3] += gate * v.w;
+        }
+        const int64_t o = static_cast<int64_t>(t) * a.H + c;
+        if (a.odt == SWQ_BF16) {
+            uint16_t *out = static_cast<uint16_t *>(a.out) + o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) out[i] = f32_to_bf16_rne(acc[i]);
+        } else {
+            float *out = static_cast<float *>(a.out) + o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) out[i] = a.accumulate ? out[i] + acc[i] : acc[i];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+
+struct PfLayout {
+    size_t header, counts, logits, sg, ids, wts, slot, pos, tok, tiles, h_hi, h_lo, y, total;
+    int max_tiles, Ih;
+};
+
+PfLayout pf_layout(const swq_moe_layer *l, int T) {
+    PfLayout w{};
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        const size_t o = off;
+        off = align256(off + n);
+        return o;
+    };
+    const size_t P = static_cast<size_t>(T) * l->top_k;
+    const size_t rows = P + (l->has_shared ? T : 0);
+    const int U = static_cast<int>(std::min<size_t>(P, static_cast<size_t>(l->num_experts)));
+    w.max_tiles = static_cast<int>((P + static_cast<size_t>(kTileRows - 1) * U) / kTileRows) +
+                  (l->has_shared ? (T + kTileRows - 1) / kTileRows : 0);
+    w.Ih = std::max(l->moe_intermediate, l->has_shared ? l->shared_intermediate : 0);
+    w.header = take(256);  // [0] finished route workgroups, [1] tile count
+    w.counts = take(static_cast<size_t>(l->num_experts) * 4);
+    w.logits = take(static_cast<size_t>(T) * l->num_experts * 4);
+    w.sg = take(static_cast<size_t>(T) * 4);
+    w.ids = take(P * 4);
+    w.wts = take(P * 4);
+    w.slot = take(P * 4);
+    w.pos = take(P * 4);
+    w.tok = take(rows * 4);
+    w.tiles = take(static_cast<size_t>(w.max_tiles) * sizeof(Tile));
+    w.h_hi = take(rows * w.Ih * 2);
+    w.h_lo = take(rows * w.Ih * 2);
+    w.y = take(rows * l->hidden * 4);
+    w.total = off;
+    return w;
+}
+
+// A matrix on the MFMA path: 4/8-bit codes, group 64, rows of whole 128-input
+// blocks (an even number of groups), at most 4096 inputs, 16 B aligned rows.
+int check_mfma(const swq_qlinear *l, int out_dim, int in_dim, bool stacked, int E) {
+    int st = check_linear_shape(l);
+    if (st != SWQ_OK) return st;
+    if (l->out_dim != out_dim || l->in_dim != in_dim) return SWQ_ERR_BAD_SHAPE;
+    if (l->bits != 4 && l->bits != 8) return SWQ_ERR_UNSUPPORTED_BITS;
+    if (l->group_size != kGroupK) return SWQ_ERR_LIMIT;
+    if (in_dim % (2 * kGroupK) != 0 || in_dim > kGroupK * kMaxGroups) return SWQ_ERR_LIMIT;
+    if (!vector_path_ok(l, 0, 0, 0)) return SWQ_ERR_MISALIGNED;
+    if (stacked && E > 1 && (l->expert_stride_w == 0 || l->expert_stride_sb == 0)) return SWQ_ERR_INVALID_ARGUMENT;
+    return SWQ_OK;
+}
+
+int check_prefill_layer(const swq_moe_layer *l, int T) {
+    if (!l) return SWQ_ERR_INVALID_ARGUMENT;
+    if (l->reserved != 0) return SWQ_ERR_INVALID_ARGUMENT;
+    if (T <= 0 || l->hidden <= 0 || l->num_experts <= 0 || l->moe_intermediate <= 0) return SWQ_ERR_INVALID_ARGUMENT;
+    if (l->top_k <= 0 || l->top_k > l->num_experts) return SWQ_ERR_EXPERT_RANGE;
+    if (l->top_k > SWQ_MAX_TOPK || l->num_experts > kMaxExperts) return SWQ_ERR_LIMIT;
+    if (static_cast<int64_t>(T) * l->top_k > (1 << 24)) return SWQ_ERR_LIMIT;
+    const int H = l->hidden, E = l->num_experts, I = l->moe_intermediate;
+    int st;
+    if ((st = check_mfma(&l->router, E, H, false, E)) != SWQ_OK) return st;
+    if ((st = check_mfma(&l->gate, I, H, true, E)) != SWQ_OK) return st;
+    if ((st = check_mfma(&l->up, I, H, true, E)) != SWQ_OK) return st;
+    if ((st = check_mfma(&l->down, H, I, true, E)) != SWQ_OK) return st;
+    if (l->gate.bits != l->up.bits) return SWQ_ERR_LIMIT;
+    if (l->has_shared) {
+        const int Is = l->shared_intermediate;
+        if (Is <= 0) return SWQ_ERR_INVALID_ARGUMENT;
+        if ((st = check_mfma(&l->shared_gate, Is, H, false, 1)) != SWQ_OK) return st;
+        if ((st = check_mfma(&l->shared_up, Is, H, false, 1)) != SWQ_OK) return st;
+        if ((st = check_mfma(&l->shared_down, H, Is, false, 1)) != SWQ_OK) return st;
+        if ((st = check_linear_shape(&l->shared_expert_gate)) != SWQ_OK) return st;
+        const swq_qlinear &sg = l->shared_expert_gate;
+        if (sg.out_dim != 1 || sg.in_dim != H) return SWQ_ERR_BAD_SHAPE;
+        if (sg.bits != 4 && sg.bits != 8) return SWQ_ERR_UNSUPPORTED_BITS;
+        if ((static_cast<int64_t>(H) * sg.bits) % 128 != 0 || (static_cast<int64_t>(sg.group_size) * sg.bits) % 128 != 0)
+            return SWQ_ERR_BAD_SHAPE;
+        if (!vector_path_ok(&sg, 0, 0, 0)) return SWQ_ERR_MISALIGNED;
+        // one kernel instantiation serves the routed and the shared tiles
+        if (l->shared_gate.bits != l->gate.bits || l->shared_up.bits != l->gate.bits ||
+            l->shared_down.bits != l->down.bits)
+            return SWQ_ERR_LIMIT;
+    }
+    return SWQ_OK;
+}
+
+template <int SRC, int MT, int EPI>
+int launch_gemm(int bits, const GemmArgs &a, int blocks, hipStream_t s) {
+    if (blocks <= 0) return SWQ_OK;
+    if (bits == 4) hipLaunchKernelGGL((pf_gemm<4, SRC, MT, EPI>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+    else hipLaunchKernelGGL((pf_gemm<8, SRC, MT, EPI>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+    return launch_status();
+}
+
+int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, void *out, int out_dtype,
+                 int32_t *topk_ids, float *topk_weights, const float *logit_bias, void *ws, size_t ws_bytes,
+                 int flags, void *stream) {
+    if (x_dtype != SWQ_F32 && x_dtype != SWQ_BF16) return SWQ_ERR_UNSUPPORTED_DTYPE;
+    int st = check_prefill_layer(layer, T);
+    if (st != SWQ_OK) return st;
+    if (!x || !out) return SWQ_ERR_INVALID_ARGUMENT;
+    if (out_dtype != SWQ_F32 && out_dtype != SWQ_BF16) return SWQ_ERR_UNSUPPORTED_DTYPE;
+    if ((flags & ~SWQ_MOE_ACCUMULATE) != 0) return SWQ_ERR_INVALID_ARGUMENT;
+    const bool accumulate = (flags & SWQ_MOE_ACCUMULATE) != 0;
+    if (accumulate && out_dtype != SWQ_F32) return SWQ_ERR_UNSUPPORTED_DTYPE;
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(out) % 16 != 0)
+        return SWQ_ERR_MISALIGNED;
+    const PfLayout wl = pf_layout(layer, T);
+    if (!ws || ws_bytes < wl.total) return SWQ_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(ws) % 256 != 0) return SWQ_ERR_MISALIGNED;
+
+    uint8_t *wsb = static_cast<uint8_t *>(ws);
+    uint32_t *header = reinterpret_cast<uint32_t *>(wsb + wl.header);
+    const int H = layer->hidden, E = layer->num_experts, K = layer->top_k, I = layer->moe_intermediate;
+    const int Is = layer->has_shared ? layer->shared_intermediate : 0;
+    const int P = T * K;
+    const int rows_sorted = P + (layer->has_shared ? T : 0);
+    float *logits = reinterpret_cast<float *>(wsb + wl.logits);
+    int32_t *tok = reinterpret_cast<int32_t *>(wsb + wl.tok);
+    int32_t *pos = reinterpret_cast<int32_t *>(wsb + wl.pos);
+    float *wts = reinterpret_cast<float *>(wsb + wl.wts);
+    float *sg = reinterpret_cast<float *>(wsb + wl.sg);
+    Tile *tiles = reinterpret_cast<Tile *>(wsb + wl.tiles);
+    int32_t *n_tiles = reinterpret_cast<int32_t *>(header + 1);
+    uint16_t *h_hi = reinterpret_cast<uint16_t *>(wsb + wl.h_hi);
+    uint16_t *h_lo = reinterpret_cast<uint16_t *>(wsb + wl.h_lo);
+    float *y = reinterpret_cast<float *>(wsb + wl.y);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool bf16x = x_dtype == SWQ_BF16;
+
+    // 1. router logits
+    {
+        GemmArgs g{};
+        g.m[0] = g.m[1] = make_qmat(&layer->router);
+        g.a0 = x;
+        g.a_ld = H;
+        g.o0 = logits;
+        g.o_ld = E;
+        g.K = g.Ksh = H;
+        g.N = g.Nsh = E;
+        g.E = -1;
+        g.rows_total = T;
+        g.a_rows = T;
+        g.col_block = 128;
+        g.col_wave = 32;
+        g.col_op = 16;
+        g.nblk = (E + 127) / 128;
+        const int blocks = ((T + kRouterRows - 1) / kRouterRows) * g.nblk;
+        st = bf16x ? launch_gemm<kSrcBF16, 1, kEpiRows>(layer->router.bits, g, blocks, s)
+                   : launch_gemm<kSrcF32, 1, kEpiRows>(layer->router.bits, g, blocks, s);
+        if (st != SWQ_OK) return st;
+    }
+    // 2. routing and grouping
+    {
+        RouteArgs r{};
+        if (layer->has_shared) r.seg = make_qmat(&layer->shared_expert_gate);
+        r.x = x;
+        r.logits = logits;
+        r.bias = logit_bias;
+        r.ids = reinterpret_cast<int32_t *>(wsb + wl.ids);
+        r.wts = wts;
+        r.user_ids = topk_ids;
+        r.user_w = topk_weights;
+        r.sg = sg;
+        r.slot = reinterpret_cast<int32_t *>(wsb + wl.slot);
+        r.counts = reinterpret_cast<int32_t *>(wsb + wl.counts);
+        r.done = header;
+        r.pos = pos;
+        r.tok = tok;
+        r.tiles = tiles;
+        r.n_tiles = n_tiles;
+        r.T = T;
+        r.E = E;
+        r.K = K;
+        r.H = H;
+        r.norm = layer->norm_topk_prob ? 1 : 0;
+        r.has_shared = layer->has_shared ? 1 : 0;
+        const int blocks = (T + kRouteWaves - 1) / kRouteWaves;
+        if (bf16x) hipLaunchKernelGGL(pf_route<SWQ_BF16>, dim3(blocks), dim3(kPfThreads), 0, s, r);
+        else hipLaunchKernelGGL(pf_route<SWQ_F32>, dim3(blocks), dim3(kPfThreads), 0, s, r);
+        if ((st = launch_status()) != SWQ_OK) return st;
+    }
+    // 3. gate/up + SwiGLU over the tiles
+    {
+        GemmArgs g{};
+        g.m[0] = make_qmat(&layer->gate);
+        g.m[1] = make_qmat(&layer->up);
+        if (layer->has_shared) {
+            g.sh[0] = make_qmat(&layer->shared_gate);
+            g.sh[1] = make_qmat(&layer->shared_up);
+        }
+        g.a0 = x;
+        g.a_ld = H;
+        g.row_src = tok;
+        g.tiles = tiles;
+        g.n_tiles = n_tiles;
+        g.o0 = h_hi;
+        g.o1 = h_lo;
+        g.o_ld = wl.Ih;
+        g.rows_total = rows_sorted;
+        g.a_rows = T;
+        g.K = g.Ksh = H;
+        g.N = I;
+        g.Nsh = Is;
+        g.E = E;
+        g.col_block = 64;
+        g.col_wave = 16;
+        g.col_op = 0;
+        g.nblk = (wl.Ih + 63) / 64;
+        const int blocks = wl.max_tiles * g.nblk;
+        st = bf16x ? launch_gemm<kSrcBF16, 4, kEpiSwiGLU>(layer->gate.bits, g, blocks, s)
+                   : launch_gemm<kSrcF32, 4, kEpiSwiGLU>(layer->gate.bits, g, blocks, s);
+        if (st != SWQ_OK) return st;
+    }
+    // 4. down over the tiles
+    {
+        GemmArgs g{};
+        g.m[0] = g.m[1] = make_qmat(&layer->down);
+        if (layer->has_shared) g.sh[0] = g.sh[1] = make_qmat(&layer->shared_down);
+        g.a0 = h_hi;
+        g.a1 = h_lo;
+        g.a_ld = wl.Ih;
+        g.tiles = tiles;
+        g.n_tiles = n_tiles;
+        g.o0 = y;
+        g.o_ld = H;
+        g.rows_total = rows_sorted;
+        g.a_rows = rows_sorted;
+        g.K = I;
+        g.Ksh = Is;
+        g.N = g.Nsh = H;
+        g.E = E;
+        g.col_block = 128;
+        g.col_wave = 32;
+        g.col_op = 16;
+        g.nblk = (H + 127) / 128;
+        const int blocks = wl.max_tiles * g.nblk;
+        if ((st = launch_gemm<kSrcSplit, 4, kEpiRows>(layer->down.bits, g, blocks, s)) != SWQ_OK) return st;
+    }
+    // 5. weighted combine in pick order, then the gated shared expert
+    {
+        CombineArgs c{};
+        c.y = y;
+        c.pos = pos;
+        c.wts = wts;
+        c.sg = sg;
+        c.out = out;
+        c.T = T;
+        c.K = K;
+        c.H = H;
+        c.odt = out_dtype;
+        c.accumulate = accumulate ? 1 : 0;
+        c.has_shared = layer->has_shared ? 1 : 0;
+        hipLaunchKernelGGL(pf_combine, dim3(T), dim3(kPfThreads), 0, s, c);
+        if ((st = launch_status()) != SWQ_OK) return st;
+    }
+    (void)P;
+    return SWQ_OK;
+}
+
+}  // namespace
+}  // namespace swq
+
+using namespace swq;
+
+extern "C" size_t swq_moe_prefill_workspace_bytes(const swq_moe_layer *layer, int tokens) {
+    if (check_prefill_layer(layer, tokens) != SWQ_OK) return 0;
+    return pf_layout(layer, tokens).total;
+}
+
+extern "C" int swq_moe_prefill(const swq_moe_layer *layer, const void *x, int x_dtype, int tokens, void *out,
+                               int out_dtype, int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes,
+                               int flags, void *stream) {
+    return prefill_impl(layer, x, x_dtype, tokens, out, out_dtype, topk_ids, topk_weights, nullptr, ws, ws_bytes,
+                        flags, stream);
+}
+
+extern "C" int swq_moe_prefill_biased(const swq_moe_layer *layer, const void *x, int x_dtype, int tokens,
+                                      void *out, int out_dtype, int32_t *topk_ids, float *topk_weights,
+                                      const float *logit_bias, void *ws, size_t ws_bytes, int flags, void *stream) {
+    if (!logit_bias) return SWQ_ERR_INVALID_ARGUMENT;
+    return prefill_impl(layer, x, x_dtype, tokens, out, out_dtype, topk_ids, topk_weights, logit_bias, ws, ws_bytes,
+                        flags, stream);
+}

@@ -107,6 +107,52 @@ class MoELayerGPU:
             check(self.lib.swq_moe_decode_stages(*args, mask, _stream_handle(stream)), f"moe_decode ({path})")
         return out, topk_ids, topk_weights
 
+    # -- prefill -------------------------------------------------------
+    def prefill_workspace_bytes(self, tokens: int) -> int:
+        n = self.lib.swq_moe_prefill_workspace_bytes(ctypes.byref(self._c), tokens)
+        if n == 0:
+            raise _lib.SwqError(_lib.SWQ_ERR_LIMIT, "moe_prefill_workspace_bytes")
+        return n
+
+    def new_prefill_workspace(self, tokens: int, stream=None):
+        torch = _torch()
+        n = self.prefill_workspace_bytes(tokens)
+        ws = torch.empty(n, dtype=torch.uint8, device=self.router.w.device)
+        check(self.lib.swq_moe_workspace_init(ws.data_ptr(), n, _stream_handle(stream)), "workspace_init")
+        return ws
+
+    def prefill(self, x, out=None, out_dtype=None, ws=None, accumulate: bool = False,
+                topk_ids=None, topk_weights=None, logit_bias=None, stream=None):
+        """The layer over x [T, H] (bf16 or f32 device tensor) with the pairs
+        grouped by expert (swq_moe_prefill).  ``logit_bias`` (f32 [E] device
+        tensor) adds a per-expert bias to the router logits before the
+        softmax (swq_moe_prefill_biased, the skewed-load workload).
+        Returns (out [T, H], topk_ids [T, K] int32, topk_weights [T, K] f32)."""
+        torch = _torch()
+        if x.dim() == 1:
+            x = x.unsqueeze(0)
+        T = x.shape[0]
+        x_dtype = {torch.bfloat16: SWQ_BF16, torch.float32: SWQ_F32}[x.dtype]
+        if out is None:
+            out = torch.empty((T, self.hidden), dtype=out_dtype or torch.float32, device=x.device)
+        o_dtype = {torch.bfloat16: SWQ_BF16, torch.float32: SWQ_F32}[out.dtype]
+        if ws is None:
+            ws = self.new_prefill_workspace(T, stream)
+        if topk_ids is None:
+            topk_ids = torch.empty((T, self.top_k), dtype=torch.int32, device=x.device)
+        if topk_weights is None:
+            topk_weights = torch.empty((T, self.top_k), dtype=torch.float32, device=x.device)
+        head = (ctypes.byref(self._c), x.data_ptr(), x_dtype, T, out.data_ptr(), o_dtype,
+                topk_ids.data_ptr(), topk_weights.data_ptr())
+        tail = (ws.data_ptr(), ws.numel(), _lib.SWQ_MOE_ACCUMULATE if accumulate else 0,
+                _stream_handle(stream))
+        if logit_bias is None:
+            check(self.lib.swq_moe_prefill(*head, *tail), "moe_prefill")
+        else:
+            assert logit_bias.dtype == torch.float32 and logit_bias.numel() == self.num_experts
+            check(self.lib.swq_moe_prefill_biased(*head, logit_bias.data_ptr(), *tail), "moe_prefill_biased")
+        return out, topk_ids, topk_weights
+
     def touched_bytes(self, unique_experts: int, batch: int = 1, x_bytes: int = 2,
                       out_bytes: int = 2) -> int:
         """Algorithmic HBM bytes of one decode step: every matrix read once,

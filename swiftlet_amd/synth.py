@@ -154,3 +154,21 @@ SHAPES = {
     "qwen3-next-80b-a3b-q4": MoEShape("qwen3-next-80b-a3b-q4", 2048, 512, 10, 512, 512, 4),
     "qwen3.6-35b-a3b-q8": MoEShape("qwen3.6-35b-a3b-q8", 2048, 256, 8, 512, 512, 8),
 }
+
+
+# --------------------------------------------------------------------------
+# skewed expert load for the prefill workload
+
+ZIPF_S = 1.1
+# Calibrated at the 35B shape with 512 tokens of N(0, 1) x: the realised
+# per-expert pair counts, ordered by rank, fall off as rank^-1.09 over ranks
+# 4..64 (239 of 256 experts touched, 266 tiles of 64 rows).
+ZIPF_TAU = 1.4
+
+
+def zipf_logit_bias(seed: int, experts: int, s: float = ZIPF_S, tau: float = ZIPF_TAU) -> np.ndarray:
+    """Per-expert router-logit bias b_e = -tau * s * ln(rank_e), with rank a
+    seeded permutation of 1..E: added to the logits before the softmax, it
+    skews the per-expert token counts towards Zipf(s)."""
+    rank = np.random.default_rng(seed).permutation(experts) + 1
+    return (-tau * s * np.log(rank)).astype(np.float32)

@@ -130,3 +130,49 @@ def test_no_device_reported(lib):
     from swiftlet_amd.engine import HipEngine, NoDevice
     with pytest.raises(NoDevice):
         HipEngine()
+
+
+def prefill(lib, L, T=64, ws_bytes=None, x=FAKE, x_dtype=_lib.SWQ_BF16, out_dtype=_lib.SWQ_F32, flags=0):
+    if ws_bytes is None:
+        ws_bytes = max(lib.swq_moe_prefill_workspace_bytes(ctypes.byref(L), T), 1 << 20)
+    return lib.swq_moe_prefill(ctypes.byref(L), x, x_dtype, T, FAKE, out_dtype, None, None, FAKE, ws_bytes,
+                               flags, None)
+
+
+def test_prefill_workspace_query(lib):
+    L = layer()
+    n = lib.swq_moe_prefill_workspace_bytes(ctypes.byref(L), 512)
+    rows = 512 * 8 + 512
+    assert n > rows * 2048 * 4 + rows * 512 * 4 and n % 256 == 0  # y rows, h hi/lo planes
+    assert lib.swq_moe_prefill_workspace_bytes(ctypes.byref(L), 1024) > n
+    assert lib.swq_moe_prefill_workspace_bytes(ctypes.byref(L), 0) == 0
+    assert lib.swq_moe_prefill_workspace_bytes(ctypes.byref(layer(router=lin(256, 2048, 8, group=32))), 8) == 0
+
+
+@pytest.mark.parametrize("mutate,code", [
+    (dict(router=lin(256, 2048, 8, group=32)), _lib.SWQ_ERR_LIMIT),        # group 64 only
+    (dict(I=64, Is=64), _lib.SWQ_ERR_LIMIT),                                # down rows of 64 inputs
+    (dict(router=lin(256, 2048, 2)), _lib.SWQ_ERR_UNSUPPORTED_BITS),
+    (dict(shared_down=lin(2048, 512, 8)), _lib.SWQ_ERR_LIMIT),              # shared bits != routed
+    (dict(hidden=4096, router=lin(256, 4096, 8)), _lib.SWQ_ERR_BAD_SHAPE),  # gate in_dim != hidden
+    (dict(hidden=8192, router=lin(256, 8192, 8)), _lib.SWQ_ERR_LIMIT),      # rows above 4096 inputs
+    (dict(top_k=0), _lib.SWQ_ERR_EXPERT_RANGE),
+    (dict(reserved=2), _lib.SWQ_ERR_INVALID_ARGUMENT),
+    (dict(router=lin(256, 2048, 8, base=FAKE + 4)), _lib.SWQ_ERR_MISALIGNED),
+])
+def test_prefill_layer_validation(lib, mutate, code):
+    assert prefill(lib, layer(**mutate)) == code
+
+
+def test_prefill_call_validation(lib):
+    L = layer()
+    assert prefill(lib, L, T=0) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert prefill(lib, L, ws_bytes=64) == _lib.SWQ_ERR_WORKSPACE
+    assert prefill(lib, L, x=0) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert prefill(lib, L, x=FAKE + 2) == _lib.SWQ_ERR_MISALIGNED
+    assert prefill(lib, L, x_dtype=_lib.SWQ_F16) == _lib.SWQ_ERR_UNSUPPORTED_DTYPE
+    assert prefill(lib, L, flags=2) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert prefill(lib, L, flags=_lib.SWQ_MOE_ACCUMULATE, out_dtype=_lib.SWQ_BF16) == _lib.SWQ_ERR_UNSUPPORTED_DTYPE
+    n = lib.swq_moe_prefill_workspace_bytes(ctypes.byref(L), 64)
+    assert lib.swq_moe_prefill_biased(ctypes.byref(L), FAKE, _lib.SWQ_BF16, 64, FAKE, _lib.SWQ_F32, None, None,
+                                      None, FAKE, n, 0, None) == _lib.SWQ_ERR_INVALID_ARGUMENT

@@ -1,0 +1,196 @@
+"""Ragged MoE prefill on the device (swq_moe_prefill) against the oracle
+(QwenCPUModel.moeForward for S tokens, QwenCPUModel.swift:500-569), at the
+benchmark shapes, at odd shapes, and at the 512-token skewed-load workload.
+
+Bar: expert ids equal the oracle's wherever the router's k-th/(k+1)-th
+logit gap exceeds 1e-3; combine weights within 1e-5; layer output within
+1e-3 relative L2 of the f32 oracle, and within 1e-5 (fp32 accumulation on
+exact bf16 operands: the observed error is ~1e-6).  At 512 tokens the oracle
+runs on a sample of tokens, and size-independent properties cover the rest:
+each token's row is the same bit for bit whatever other tokens share the
+call (rows never mix in the matrix cores), and repeated calls agree."""
+
+import numpy as np
+import pytest
+
+from oracle import moe_ref as R
+from swiftlet_amd import moe, synth
+from tests import helpers
+
+pytestmark = pytest.mark.gpu
+
+REL_L2_BAR = 1e-3
+TIGHT = 1e-5
+MARGIN = 1e-3
+ZIPF_SEED = 2024
+
+
+def _x(seed, T, H, dtype="bf16"):
+    import torch
+    xb = synth.activations_bf16(seed, T, H)
+    xf = synth.bf16_to_f32(xb)
+    x = helpers.bf16_bits_to_torch(xb) if dtype == "bf16" else torch.from_numpy(xf).cuda()
+    return x, xf
+
+
+def _check(shape, xf, out, ids, w, rows=None, seed=helpers.SEED, layer=0, bias=None, ref_layer=None):
+    """Compare rows `rows` (default all) of a prefill result with the oracle."""
+    import torch
+    rows = np.arange(xf.shape[0]) if rows is None else np.asarray(rows)
+    ref_layer = ref_layer or helpers.ref_layer(shape, seed, layer)
+    ref_out, picks, ref_w = R.moe_forward(xf[rows], ref_layer, logit_bias=bias)
+    margin = R.router_margin(xf[rows], ref_layer, logit_bias=bias)
+    checked = 0
+    for i, t in enumerate(rows):
+        if margin[i] > MARGIN:
+            assert list(ids[t]) == [e for e, _ in picks[i]], (t, ids[t], picks[i])
+            assert np.allclose(w[t], ref_w[i], rtol=1e-5, atol=1e-7), t
+            checked += 1
+    assert checked >= len(rows) - 1  # margins below 1e-3 are rare at these shapes
+    if out.dtype == torch.bfloat16:
+        got = R.bf16_bits_to_f32(helpers.torch_bf16_to_bits(out))[rows]
+        # each element is the bf16 rounding of an f32 value within 1e-5 rms of the oracle's
+        ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref_out), 1e-30))) - 7)
+        rms = np.sqrt(np.mean(ref_out.astype(np.float64) ** 2))
+        assert np.all(np.abs(got - ref_out) <= ulp + TIGHT * rms)
+        assert R.rel_l2(got, R.bf16_bits_to_f32(R.f32_to_bf16_bits_rne(ref_out))) < REL_L2_BAR
+    else:
+        err = R.rel_l2(out.cpu().numpy()[rows], ref_out)
+        print(f"rel_l2 vs oracle: {err:.3g}", flush=True)
+        assert err < REL_L2_BAR, err
+        assert err < TIGHT, err
+
+
+@pytest.mark.parametrize("name,T,rows", [
+    ("qwen3.6-35b-a3b-q4", 64, [0, 17, 40, 63]),
+    ("qwen3-next-80b-a3b-q4", 40, [1, 22, 39]),
+    ("qwen3.6-35b-a3b-q8", 33, [0, 16, 32]),
+])
+def test_prefill_matches_oracle(name, T, rows):
+    import torch
+    shape = synth.SHAPES[name]
+    print(f"prefill vs oracle: {name} T={T}", flush=True)
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    x, xf = _x(helpers.SEED + 500 + T, T, shape.hidden)
+    out, ids, w = gpu.prefill(x)
+    torch.cuda.synchronize()
+    _check(shape, xf, out, ids.cpu().numpy(), w.cpu().numpy(), rows=rows)
+
+
+@pytest.mark.parametrize("E,K,I,Is,H,bits,norm,T", [
+    (8, 2, 128, 128, 128, 4, True, 50),       # few experts: long tiles
+    (60, 4, 128, 256, 256, 8, False, 70),     # E not a multiple of 16; Is != I; no renorm
+    (1024, 16, 128, 128, 128, 4, True, 20),   # widest top-k table: mostly 1-row tiles
+    (128, 1, 256, 128, 384, 4, True, 130),    # top-1; 6 groups per row
+])
+def test_prefill_odd_shapes(E, K, I, Is, H, bits, norm, T):
+    import torch
+    shape = synth.MoEShape("odd", H, E, K, I, Is, expert_bits=bits, router_bits=8, group=64,
+                           norm_topk_prob=norm)
+    print(f"prefill odd: E={E} K={K} I={I} Is={Is} H={H} q{bits} T={T}", flush=True)
+    gpu = moe.synth_layer(shape, 77, 0)
+    x, xf = _x(78, T, H)
+    out, ids, w = gpu.prefill(x)
+    torch.cuda.synchronize()
+    _check(shape, xf, out, ids.cpu().numpy(), w.cpu().numpy(), seed=77)
+
+
+def test_prefill_f32_x_bf16_out():
+    import torch
+    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    x, xf = _x(helpers.SEED + 9, 24, shape.hidden, dtype="f32")
+    out, ids, w = gpu.prefill(x, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    _check(shape, xf, out, ids.cpu().numpy(), w.cpu().numpy(), rows=[0, 11, 23])
+
+
+def test_prefill_skewed_512_tokens():
+    """The benchmark workload: 512 tokens, Zipf(1.1)-skewed expert load.
+    Routing checked for every token, outputs for a sample against the oracle,
+    and every row against a smaller call holding only that row's token."""
+    import torch
+    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    bias = synth.zipf_logit_bias(ZIPF_SEED, shape.experts)
+    bias_t = torch.from_numpy(bias).cuda()
+    x, xf = _x(helpers.SEED + 4242, 512, shape.hidden)
+    ws = gpu.new_prefill_workspace(512)
+    out, ids, w = gpu.prefill(x, ws=ws, logit_bias=bias_t)
+    out, ids, w = out.clone(), ids.clone(), w.clone()
+    torch.cuda.synchronize()
+    ids_np, w_np = ids.cpu().numpy(), w.cpu().numpy()
+    counts = np.bincount(ids_np.ravel(), minlength=shape.experts)
+    assert counts.sum() == 512 * 8 and counts.max() <= 512
+    assert counts.max() > 200  # skewed: the top expert takes a large share
+    ref_layer = helpers.ref_layer(shape, helpers.SEED, 0)
+    # routing of every token
+    logits = xf @ ref_layer.router_dense.T + bias
+    margin = R.router_margin(xf, ref_layer, logit_bias=bias)
+    for t in range(512):
+        if margin[t] > MARGIN:
+            p = R.softmax_row(logits[t].astype(np.float32))
+            picks = R.topk_insertion(p, 8)
+            assert list(ids_np[t]) == [e for e, _ in picks], t
+    # outputs of a sample
+    _check(shape, xf, out, ids_np, w_np, rows=[0, 255, 511], bias=bias, ref_layer=ref_layer)
+    # repeat: identical
+    out2, ids2, w2 = gpu.prefill(x, ws=ws, logit_bias=bias_t)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2) and torch.equal(ids, ids2) and torch.equal(w, w2)
+    # each row equals the row of a call that holds only some of the tokens
+    sub = [3, 100, 511, 7]
+    o_sub, i_sub, w_sub = gpu.prefill(x[sub].contiguous(), logit_bias=bias_t)
+    torch.cuda.synchronize()
+    assert torch.equal(o_sub, out[sub]) and torch.equal(i_sub, ids[sub]) and torch.equal(w_sub, w[sub])
+
+
+def test_prefill_matches_decode():
+    """A token's prefill row against the decode step on that token alone:
+    the same routing and, both within 1e-5 of the oracle, outputs within 2e-5."""
+    import torch
+    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    x, xf = _x(helpers.SEED + 31, 12, shape.hidden)
+    out, ids, w = gpu.prefill(x)
+    ws = gpu.new_workspace(1)
+    margin = R.router_margin(xf, helpers.ref_layer(shape, helpers.SEED, 0))
+    for t in range(12):
+        od, idd, wd = gpu.decode(x[t:t + 1], ws=ws)
+        torch.cuda.synchronize()
+        if margin[t] > MARGIN:
+            assert torch.equal(idd[0], ids[t]), t
+            assert torch.allclose(wd[0], w[t], rtol=1e-5, atol=1e-7), t
+            # each path is within TIGHT of the oracle
+            assert R.rel_l2(out[t].cpu().numpy(), od[0].cpu().numpy()) < 2 * TIGHT, t
+
+
+def test_prefill_accumulate():
+    import torch
+    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    x, _ = _x(5, 40, shape.hidden)
+    ws = gpu.new_prefill_workspace(40)
+    o1, _, _ = gpu.prefill(x, ws=ws)
+    o1 = o1.clone()
+    resid = torch.randn_like(o1)
+    acc = resid.clone()
+    gpu.prefill(x, out=acc, ws=ws, accumulate=True)
+    torch.cuda.synchronize()
+    assert torch.allclose(acc, resid + o1, rtol=0, atol=1e-5)
+
+
+def test_prefill_single_token_and_workspace_reuse():
+    """T = 1, then larger calls on a workspace sized for the largest: the
+    counters the grouping leaves at zero serve every later call."""
+    import torch
+    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    ws = gpu.new_prefill_workspace(96)
+    for T in (1, 96, 17, 1):
+        x, xf = _x(900 + T, T, shape.hidden)
+        out, ids, w = gpu.prefill(x, ws=ws)
+        fresh, ids_f, w_f = gpu.prefill(x)
+        torch.cuda.synchronize()
+        assert torch.equal(out, fresh) and torch.equal(ids, ids_f) and torch.equal(w, w_f), T
+    _check(shape, xf, out, ids.cpu().numpy(), w.cpu().numpy())
