@@ -39,9 +39,15 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+# Per-file code generation options.  The MFMA kernels keep their results in
+# VGPRs: the per-group scale is applied by VALU right after each product, and
+# results in AGPRs would each cost a copy back.
+FILE_FLAGS = {"moe_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stdout}\n{r.stderr}")

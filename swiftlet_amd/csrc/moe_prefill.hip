@@ -8,11 +8,11 @@
 //
 // Launches, all on the caller's stream:
 //   1. router GEMM: logits[T, E], 16-token tiles;
-//   2. route: softmax, top-k (ties to the lower id), renormalisation, the
-//      shared-expert gate logit, per-expert pair counts; the last workgroup
-//      to finish turns the counts into the sorted pair order and the table
-//      of 64-row tiles (routed experts, then the shared expert over all
-//      tokens), and leaves the counters at zero for the next call;
+//   2. route: softmax, top-k (ties to the lower id), renormalisation and
+//      the shared-expert gate logit per token; the last workgroup to finish
+//      counts the pairs per expert and builds the sorted pair order and the
+//      table of 64-row tiles (routed experts, then the shared expert over
+//      all tokens), and leaves its arrival counter at zero for the next call;
 //   3. gate/up GEMM over the tile table with the SwiGLU epilogue: h in
 //      sorted pair order, as bf16 hi + lo planes;
 //   4. down GEMM over the same tiles: y rows (f32) in sorted pair order;
@@ -49,6 +49,11 @@ constexpr int kXsPitch = kMaxGroups + 4;
 constexpr int kTileRows = 64;    // rows of a routed / shared tile
 constexpr int kRouterRows = 16;  // rows of a router tile
 constexpr int kRouteWaves = 4;   // tokens per route workgroup
+constexpr int kXcds = 8;         // XCDs of the device: workgroup b runs on XCD b % 8
+
+// Workgroups covering `tiles` tiles of `nblk` column blocks under the XCD
+// mapping of pf_gemm (tiles rounded up to a multiple of 8).
+int gemm_blocks(int tiles, int nblk) { return ((tiles + kXcds - 1) / kXcds) * kXcds * nblk; }
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
@@ -56,6 +61,7 @@ typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
 
 enum { kSrcBF16 = 0, kSrcF32 = 1, kSrcSplit = 2 };
 enum { kEpiRows = 0, kEpiSwiGLU = 1 };
+enum { kSumStage = 0, kSumLoad = 1 };  // group sums: computed while staging / read from xs_in
 
 struct Tile {
     int32_t expert;  // 0..E-1, or E for the shared expert
@@ -81,6 +87,14 @@ struct GemmArgs {
     int32_t a_rows;           // rows of the activation source
     int32_t nblk;             // column blocks per tile
     int32_t col_block, col_wave, col_op;  // output column of block / wave / operand steps
+    // Group sums X_g of the activation rows, [rows][xs_ld] f32.  The router
+    // computes those of x while staging it and writes them (xs_out, by
+    // token); gate/up reads them by token and writes those of h (by sorted
+    // row, one group per 64-column block); down reads those.
+    const float *xs_in;
+    float *xs_out;
+    int32_t xs_ld, xs_ld_out;
+    int32_t o_perm;           // SwiGLU output in nibble_order within each 8 columns (4-bit down)
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -89,41 +103,44 @@ __device__ __forceinline__ f32x4_t mfma(u32x4_t a, u32x4_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float scale_of(uint32_t raw, int stype) {
-    if (stype == 1) return f16_to_f32(static_cast<uint16_t>(raw));
-    if (stype == 2) return bf16_to_f32(static_cast<uint16_t>(raw));
-    return __uint_as_float(raw);
+// Scales and biases of dtype ST (SWQ_F32 / SWQ_F16 / SWQ_BF16), fixed per
+// kernel instance so that the K loop has no branches: a branch around a
+// load or its use makes the compiler wait for every load in flight.
+template <int ST>
+__device__ __forceinline__ float scale_of(uint32_t raw) {
+    if constexpr (ST == SWQ_F16) return f16_to_f32(static_cast<uint16_t>(raw));
+    else if constexpr (ST == SWQ_BF16) return bf16_to_f32(static_cast<uint16_t>(raw));
+    else return __uint_as_float(raw);
 }
 
-__device__ __forceinline__ uint32_t scale_raw(const uint8_t *base, int64_t idx, int stype) {
-    if (stype == 0) return *reinterpret_cast<const uint32_t *>(base + idx * 4);
-    return *reinterpret_cast<const uint16_t *>(base + idx * 2);
+template <int ST>
+__device__ __forceinline__ uint32_t scale_raw(const uint8_t *base, int64_t idx) {
+    if constexpr (ST == SWQ_F32) return *reinterpret_cast<const uint32_t *>(base + idx * 4);
+    else return *reinterpret_cast<const uint16_t *>(base + idx * 2);
 }
 
 // Eight natural-order bf16 (pairs d0 = {x0,x1} .. d3 = {x6,x7}) reordered to
 // {x0,x4},{x1,x5},{x2,x6},{x3,x7}: the order in which a 4-bit code word
-// yields its codes two at a time (nibbles j and j+4 of `v >> 4j`).
+// yields its codes two at a time (nibbles j and j+4 of `v >> 4j`).  One
+// v_perm_b32 per pair: selector bytes 0-3 pick from the second operand,
+// 4-7 from the first.
 __device__ __forceinline__ u32x4_t nibble_order(u32x4_t d) {
     u32x4_t o;
-    o[0] = (d[0] & 0xFFFFu) | (d[2] << 16);
-    o[1] = (d[0] >> 16) | (d[2] & 0xFFFF0000u);
-    o[2] = (d[1] & 0xFFFFu) | (d[3] << 16);
-    o[3] = (d[1] >> 16) | (d[3] & 0xFFFF0000u);
+    o[0] = __builtin_amdgcn_perm(d[2], d[0], 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(d[2], d[0], 0x07060302u);
+    o[2] = __builtin_amdgcn_perm(d[3], d[1], 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(d[3], d[1], 0x07060302u);
     return o;
-}
-
-__device__ __forceinline__ uint32_t and_or_u32(uint32_t v, uint32_t mask, uint32_t magic) {
-    return (v & mask) | magic;
 }
 
 // 8 codes of one 4-bit word as bf16 (16 + q: the code in the top four
 // mantissa bits of 16.0), in nibble_order.
 __device__ __forceinline__ u32x4_t codes_q4(uint32_t w) {
     u32x4_t o;
-    o[0] = and_or_u32(w << 3, 0x00780078u, 0x41804180u);
-    o[1] = and_or_u32(w >> 1, 0x00780078u, 0x41804180u);
-    o[2] = and_or_u32(w >> 5, 0x00780078u, 0x41804180u);
-    o[3] = and_or_u32(w >> 9, 0x00780078u, 0x41804180u);
+    o[0] = and_or(w << 3, 0x00780078u, 0x41804180u);
+    o[1] = and_or(w >> 1, 0x00780078u, 0x41804180u);
+    o[2] = and_or(w >> 5, 0x00780078u, 0x41804180u);
+    o[3] = and_or(w >> 9, 0x00780078u, 0x41804180u);
     return o;
 }
 
@@ -189,21 +206,153 @@ struct BSlot {
     uint32_t s[2];                     // operand j: the raw scale of (row, group)
 };
 
-template <int BITS, int SRC, int MT, int EPI>
+// Eight consecutive group sums of one activation row, zeros past NG (the
+// row holds at least g + 8 entries: rows are padded to whole 32-group blocks).
+__device__ __forceinline__ void load_sums8(const float *row, int g, int NG, float (&v)[8]) {
+    const float4 x0 = *reinterpret_cast<const float4 *>(row + g);
+    const float4 x1 = *reinterpret_cast<const float4 *>(row + g + 4);
+    const float t[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = g + i < NG ? t[i] : 0.f;
+}
+
+// The bias term sum_g b'[n,g] X_g[m] on the group axis, added to acc.  b' is
+// exact as bf16 hi + lo (an fp16 bias less 16 fp16 scales); X_g as hi + mid +
+// lo; the five products above 2^-24 relative are accumulated.  xrow[mt]: the
+// group sums of this lane's A row (16 mt + n), rows padded to 32-group blocks.
+template <int BITS, int ST, int MT>
+__device__ __forceinline__ void bias_term(f32x4_t (&acc)[MT][2], const float *const (&xrow)[MT],
+                                          const uint8_t *const (&sbase)[2], const uint8_t *const (&bbase)[2],
+                                          const int64_t (&srow)[2], int NG, int rows, int kg) {
+#pragma unroll 1
+    for (int g0 = 0; g0 < NG; g0 += 32) {
+        // every load first (clamped indices), then the selects: a load under
+        // a branch would be waited for on its own
+        uint32_t braw[2][8], sraw[2][8];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int gi = min(g0 + 8 * kg + i, NG - 1);
+                braw[j][i] = scale_raw<ST>(bbase[j], srow[j] + gi);
+                if constexpr (BITS == 4) sraw[j][i] = scale_raw<ST>(sbase[j], srow[j] + gi);
+            }
+        float xv[MT][8];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) load_sums8(xrow[mt], g0 + 8 * kg, NG, xv[mt]);
+        u32x4_t bh[2], bl[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float bp = scale_of<ST>(braw[j][i]);
+                if constexpr (BITS == 4) bp = fmaf(-16.f, scale_of<ST>(sraw[j][i]), bp);
+                v[i] = g0 + 8 * kg + i < NG ? bp : 0.f;
+            }
+            split8(v, bh[j], bl[j]);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            if (16 * mt >= rows) break;
+            u32x4_t xh, xm, xl;
+            split8x3(xv[mt], xh, xm, xl);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                acc[mt][j] = mfma(xl, bh[j], acc[mt][j]);
+                acc[mt][j] = mfma(xm, bl[j], acc[mt][j]);
+                acc[mt][j] = mfma(xm, bh[j], acc[mt][j]);
+                acc[mt][j] = mfma(xh, bl[j], acc[mt][j]);
+                acc[mt][j] = mfma(xh, bh[j], acc[mt][j]);
+            }
+        }
+    }
+}
+
+// Position of column c in a row stored in nibble_order (within each 8).
+__device__ __forceinline__ int nibble_pos(int c) {
+    const int i = c & 7;
+    return (c & ~7) | (i < 4 ? 2 * i : 2 * i - 7);
+}
+
+// Epilogue: lane holds column n of rows 16 mt + 4 kg + r.  kEpiRows stores
+// f32 rows; kEpiSwiGLU stores h = silu(g) * u as bf16 hi + lo planes and the
+// group sum of h over the workgroup's 64 columns (one group of the down
+// projection's input).  Every thread of the workgroup calls it.
+template <int EPI, int MT>
+__device__ __forceinline__ void epilogue(const f32x4_t (&acc)[MT][2], const GemmArgs &a, const int (&col)[2], int N,
+                                         bool active, int row0, int rows, int nb, float *s_red) {
+    constexpr int ROWS = 16 * MT;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 15, kg = lane >> 4;
+    if constexpr (EPI == kEpiSwiGLU) {
+        const bool cok = active && col[0] < N;
+        const int pc = a.o_perm ? nibble_pos(col[0]) : col[0];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            if (16 * mt >= rows) break;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * mt + 4 * kg + r;
+                const float h = swiglu(acc[mt][0][r], acc[mt][1][r]);
+                uint32_t hi, lo;
+                split_pair(h, 0.f, hi, lo);
+                if (cok && row < rows) {
+                    const int64_t o = static_cast<int64_t>(row0 + row) * a.o_ld + pc;
+                    static_cast<uint16_t *>(a.o0)[o] = static_cast<uint16_t>(hi);
+                    static_cast<uint16_t *>(a.o1)[o] = static_cast<uint16_t>(lo);
+                }
+                const float hv = cok ? bf16_lo(hi) + bf16_lo(lo) : 0.f;
+                const float rs = segment_reduce(hv, 4);  // the wave's 16 columns
+                if (n == 0) s_red[wave * ROWS + row] = rs;
+            }
+        }
+        __syncthreads();
+        if (tid < rows) {
+            const float t = (s_red[tid] + s_red[ROWS + tid]) + (s_red[2 * ROWS + tid] + s_red[3 * ROWS + tid]);
+            a.xs_out[static_cast<int64_t>(row0 + tid) * a.xs_ld_out + nb] = t;
+        }
+    } else if (active) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            if (16 * mt >= rows) break;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * mt + 4 * kg + r;
+                if (row >= rows) continue;
+                const int64_t o = static_cast<int64_t>(row0 + row) * a.o_ld;
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    if (col[j] < N) static_cast<float *>(a.o0)[o + col[j]] = acc[mt][j][r];
+            }
+        }
+    }
+}
+
+// The grouped quantised GEMM: one workgroup computes a tile of up to 16*MT
+// activation rows against 4 waves x 2 operands x 16 matrix rows (output
+// columns); see the file comment for the arithmetic.  Rows past the tile
+// (`rows`) are staged from row 0 and never stored: the matrix cores keep rows
+// apart, so they cannot disturb the others.
+template <int BITS, int ST, int SRC, int MT, int EPI, int SUM>
 __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
     constexpr int ROWS = 16 * MT;
     constexpr int NPL = SRC == kSrcBF16 ? 1 : 2;
     constexpr int PIECES = ROWS * 8;
     constexpr int PPT = (PIECES + kPfThreads - 1) / kPfThreads;
     __shared__ __attribute__((aligned(16))) uint16_t s_a[2][NPL][ROWS * kLdsPitch];
-    __shared__ __attribute__((aligned(16))) float s_xs[ROWS * kXsPitch];
+    __shared__ __attribute__((aligned(16))) float s_xs[SUM == kSumStage ? ROWS * kXsPitch : 1];
+    __shared__ float s_red[EPI == kEpiSwiGLU ? 4 * ROWS : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, kg = lane >> 4;
 
-    const int wi = blockIdx.x;
-    const int ti = wi / a.nblk, nb = wi - ti * a.nblk;
+    // Workgroup b runs on XCD b % 8 (round-robin dispatch).  XCD x takes
+    // tiles x, x + 8, ...; the column blocks of one tile follow each other
+    // on the same XCD, so its activation rows come from HBM once and from
+    // that XCD's L2 afterwards.
+    const int xcd = blockIdx.x & (kXcds - 1), q = blockIdx.x >> 3;
+    const int ti = (q / a.nblk) * kXcds + xcd, nb = q % a.nblk;
     int expert = 0, row0, rows;
     if (a.tiles) {
         if (ti >= *a.n_tiles) return;
@@ -216,13 +365,13 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
             return;
     } else {
         row0 = ti * ROWS;
+        if (row0 >= a.rows_total) return;
         rows = min(ROWS, a.rows_total - row0);
     }
     const bool shared = expert == a.E;
     const int K = shared ? a.Ksh : a.K;
     const int N = shared ? a.Nsh : a.N;
     const int NG = K / kGroupK;
-    const int NG32 = (NG + 31) & ~31;
     const int wcol = nb * a.col_block + wave * a.col_wave;
     const bool active = wcol < N;
 
@@ -232,11 +381,9 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
     const uint8_t *bbase[2];
     int64_t srow[2];
     int col[2];
-    int stype[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const QMat &m = shared ? a.sh[j] : a.m[j];
-        stype[j] = m.stype;
         col[j] = wcol + j * a.col_op + n;
         const int R = min(col[j], N - 1);
         const int64_t eoff_w = shared ? 0 : static_cast<int64_t>(expert) * m.stride_w;
@@ -261,27 +408,24 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
                 sl.w[j][2] = v.z;
                 sl.w[j][3] = v.w;
             }
-            sl.s[j] = scale_raw(sbase[j], srow[j] + g, stype[j]);
+            sl.s[j] = scale_raw<ST>(sbase[j], srow[j] + g);
         }
     };
 
-    // ---- A staging
+    // ---- A staging (rows past the tile stage row 0)
     int64_t src[PPT];
-    bool pok[PPT];
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
         const int p = tid + kPfThreads * i;
         const int r = p >> 3;
-        pok[i] = p < PIECES && r < rows;
-        int64_t s = 0;
-        if (pok[i]) s = min(max(a.row_src ? a.row_src[row0 + r] : row0 + r, 0), a.a_rows - 1);
+        const int rr = p < PIECES && r < rows ? r : 0;
+        const int64_t s = min(max(a.row_src ? a.row_src[row0 + rr] : row0 + rr, 0), a.a_rows - 1);
         src[i] = s * a.a_ld + 8 * (p & 7);
     }
 
     auto load_a = [&](AStage<SRC, PPT> &st, int g) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
-            if (!pok[i]) continue;
             const int64_t e = src[i] + kGroupK * g;
             if constexpr (SRC == kSrcBF16) {
                 st.v[i][0] = *reinterpret_cast<const u32x4_t *>(static_cast<const uint16_t *>(a.a0) + e);
@@ -302,51 +446,41 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
             const int p = tid + kPfThreads * i;
             if (p >= PIECES) continue;  // whole waves
             const int r = p >> 3, c8 = p & 7;
-            u32x4_t hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
-            float sum = 0.f;
-            if (pok[i]) {
-                if constexpr (SRC == kSrcBF16) {
-                    hi = st.v[i][0];
-                    float t[4];
+            u32x4_t hi, lo = {0u, 0u, 0u, 0u};
+            if constexpr (SRC == kSrcBF16) {
+                hi = st.v[i][0];
+            } else if constexpr (SRC == kSrcF32) {
+                float v[8];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) t[q] = bf16_lo(hi[q]) + bf16_hi(hi[q]);
-                    sum = (t[0] + t[1]) + (t[2] + t[3]);
-                } else if constexpr (SRC == kSrcF32) {
-                    float v[8];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        v[q] = __uint_as_float(st.v[i][0][q]);
-                        v[4 + q] = __uint_as_float(st.v[i][1][q]);
-                    }
-                    split8(v, hi, lo);
-                } else {
-                    hi = st.v[i][0];
-                    lo = st.v[i][1];
+                for (int q = 0; q < 4; ++q) {
+                    v[q] = __uint_as_float(st.v[i][0][q]);
+                    v[4 + q] = __uint_as_float(st.v[i][1][q]);
                 }
-                if constexpr (SRC != kSrcBF16) {
-                    float t[4];
+                split8(v, hi, lo);
+            } else {
+                hi = st.v[i][0];
+                lo = st.v[i][1];
+            }
+            if constexpr (SUM == kSumStage) {
+                float t[4];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        t[q] = (bf16_lo(hi[q]) + bf16_lo(lo[q])) + (bf16_hi(hi[q]) + bf16_hi(lo[q]));
-                    sum = (t[0] + t[1]) + (t[2] + t[3]);
+                for (int q = 0; q < 4; ++q) {
+                    if constexpr (SRC == kSrcBF16) t[q] = bf16_lo(hi[q]) + bf16_hi(hi[q]);
+                    else t[q] = (bf16_lo(hi[q]) + bf16_lo(lo[q])) + (bf16_hi(hi[q]) + bf16_hi(lo[q]));
                 }
+                const float sum = segment_reduce((t[0] + t[1]) + (t[2] + t[3]), 3);  // 8 lanes of (row, group)
+                // the last column is a sink for the redundant groups the
+                // loop's tail stages (the bias term reads columns < 64)
+                if (c8 == 0) s_xs[r * kXsPitch + (g < NG ? g : kXsPitch - 1)] = sum;
             }
             if constexpr (BITS == 4) {
                 hi = nibble_order(hi);
-                lo = nibble_order(lo);
+                if constexpr (NPL == 2) lo = nibble_order(lo);
             }
             *reinterpret_cast<u32x4_t *>(&s_a[buf][0][r * kLdsPitch + 8 * c8]) = hi;
             if constexpr (NPL == 2) *reinterpret_cast<u32x4_t *>(&s_a[buf][1][r * kLdsPitch + 8 * c8]) = lo;
-            sum = segment_reduce(sum, 3);  // the 8 pieces of (row, group): 8 consecutive lanes
-            if (c8 == 0) s_xs[r * kXsPitch + g] = sum;
         }
     };
-
-    // zero the group-sum columns past NG that the bias MFMA reads
-    for (int i = tid; i < ROWS * (NG32 - NG); i += kPfThreads) {
-        const int r = i / (NG32 - NG), c = NG + i % (NG32 - NG);
-        s_xs[r * kXsPitch + c] = 0.f;
-    }
 
     f32x4_t acc[MT][2];
 #pragma unroll
@@ -355,7 +489,6 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
         for (int j = 0; j < 2; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     auto compute = [&](const BSlot<BITS> &sl, int buf) {
-        if (!active) return;
         u32x4_t bq[2][2];
         float sc[2];
 #pragma unroll
@@ -367,7 +500,7 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
                 bq[j][0] = codes_q8(sl.w[j][0], sl.w[j][1]);
                 bq[j][1] = codes_q8(sl.w[j][2], sl.w[j][3]);
             }
-            sc[j] = scale_of(sl.s[j], stype[j]);
+            sc[j] = scale_of<ST>(sl.s[j]);
         }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
@@ -396,102 +529,312 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
     };
 
     // ---- the K loop: A two groups ahead (registers, then LDS), B two groups
-    // ahead (registers); NG is even
+    // ahead (registers); NG is even.  Straight-line: every load is issued
+    // unconditionally (the tail re-loads group NG-1 and stages it into the
+    // buffer no later iteration reads), and waves whose columns lie past N
+    // compute on clamped rows and store nothing.
     AStage<SRC, PPT> sx, sy;
     BSlot<BITS> b0, b1;
     load_a(sx, 0);
-    if (active) load_b(b0, 0);
+    load_b(b0, 0);
     load_a(sy, 1);
-    if (active) load_b(b1, 1);
+    load_b(b1, 1);
     store_a(sx, 0, 0);
     __syncthreads();
 #pragma unroll 1
     for (int g = 0; g < NG; g += 2) {
-        if (g + 2 < NG) load_a(sx, g + 2);
+        const int g2 = min(g + 2, NG - 1), g3 = min(g + 3, NG - 1);
+        load_a(sx, g2);
         compute(b0, 0);
-        if (active && g + 2 < NG) load_b(b0, g + 2);
+        load_b(b0, g2);
         store_a(sy, 1, g + 1);
         __syncthreads();
-        if (g + 3 < NG) load_a(sy, g + 3);
+        load_a(sy, g3);
         compute(b1, 1);
-        if (active && g + 3 < NG) load_b(b1, g + 3);
-        if (g + 2 < NG) store_a(sx, 0, g + 2);
+        load_b(b1, g3);
+        store_a(sx, 0, g + 2);
         __syncthreads();
     }
 
-    if (!active) return;
+    // the router hands the group sums of x to gate/up (one column block does)
+    if constexpr (SUM == kSumStage) {
+        if (a.xs_out && nb == 0) {
+            for (int i = tid; i < rows * NG; i += kPfThreads) {
+                const int r = i / NG, g = i - r * NG;
+                a.xs_out[static_cast<int64_t>(row0 + r) * a.xs_ld_out + g] = s_xs[r * kXsPitch + g];
+            }
+        }
+    }
 
-    // ---- bias term: sum_g b'[n,g] X_g[m] on the group axis.  b' is exact as
-    // bf16 hi + lo (an fp16 bias less 16 fp16 scales); X_g as hi + mid + lo.
-    // The five products above 2^-24 relative are accumulated.
-#pragma unroll 1
-    for (int g0 = 0; g0 < NG32; g0 += 32) {
-        u32x4_t bh[2], bl[2];
+    if (active) {
+        const float *xrow[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int rr = min(16 * mt + n, rows - 1);
+            if constexpr (SUM == kSumLoad) {
+                const int64_t xr = a.row_src ? a.row_src[row0 + rr] : row0 + rr;
+                xrow[mt] = a.xs_in + xr * a.xs_ld;
+            } else {
+                xrow[mt] = &s_xs[(16 * mt + n) * kXsPitch];
+            }
+        }
+        bias_term<BITS, ST, MT>(acc, xrow, sbase, bbase, srow, NG, rows, kg);
+    }
+    epilogue<EPI, MT>(acc, a, col, N, active, row0, rows, nb, s_red);
+}
+
+// ---------------------------------------------------------------------------
+// the grouped GEMM on an LDS DMA ring (gate/up, down)
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// LDS DMA: lane L copies 16 (4) bytes from src to LDS byte address lds + 16 L
+// (4 L); M0 carries lds.  These writes are invisible to the compiler: the
+// kernel orders them by hand (vmcnt waits and barriers in ring_wait), and no
+// other code in these kernels uses M0.
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Wait until at most N of this wave's memory loads are in flight, then meet
+// the other waves: every wave's loads but its newest N have landed.
+template <int N>
+__device__ __forceinline__ void ring_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+// The grouped quantised GEMM of pf_gemm (same tile, lanes and arithmetic) fed
+// by an LDS ring D groups deep: per group, each wave's DMA brings in its
+// share of the 64 activation rows (NPL bf16 planes, already in the order the
+// codes need), its 2 x 16 code rows and their scale pairs; a group is used
+// D - 1 groups after its loads were issued.  Activation rows are 128 B; row r
+// keeps its 16 B chunk c in slot c ^ (r & 7) so the matrix-core reads of 16
+// rows at one chunk hit distinct banks.
+template <int BITS, int ST, int NPL, int EPI, int D>
+__global__ __launch_bounds__(kPfThreads) void pf_gemm_dma(const GemmArgs a) {
+    constexpr int MT = 4, ROWS = 64;
+    constexpr int A_BYTES = NPL * ROWS * 128;
+    constexpr int B_WAVE = BITS == 4 ? 1024 : 2048;  // code bytes per wave per group
+    constexpr int SLOT = A_BYTES + 4 * B_WAVE + 4 * 256;
+    constexpr int LS = 2 * NPL + B_WAVE / 1024 + 1;  // DMA instructions per wave per group
+    __shared__ __attribute__((aligned(16))) uint8_t s_ring[D * SLOT];
+    __shared__ float s_red[EPI == kEpiSwiGLU ? 4 * ROWS : 1];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15, kg = lane >> 4;
+
+    const int xcd = blockIdx.x & (kXcds - 1), q = blockIdx.x >> 3;
+    const int ti = (q / a.nblk) * kXcds + xcd, nb = q % a.nblk;
+    if (ti >= *a.n_tiles) return;
+    const Tile t = a.tiles[ti];
+    const int expert = t.expert, row0 = t.row0, rows = t.rows;
+    // a table from a workspace that skipped swq_moe_workspace_init
+    if (expert < 0 || expert > a.E || rows <= 0 || rows > ROWS || row0 < 0 || row0 + rows > a.rows_total) return;
+    const bool shared = expert == a.E;
+    const int K = shared ? a.Ksh : a.K;
+    const int N = shared ? a.Nsh : a.N;
+    const int NG = K / kGroupK;
+    const int wcol = nb * a.col_block + wave * a.col_wave;
+    const bool active = wcol < N;
+
+    // ---- matrices of the two operands (this lane's compute row n, clamped)
+    const uint8_t *wbase[2];
+    const uint8_t *sbase[2];
+    const uint8_t *bbase[2];
+    int64_t srow[2];
+    int col[2];
+    int row_bytes = 0, gpr = 0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const QMat &m = shared ? a.sh[j] : a.m[j];
+        col[j] = wcol + j * a.col_op + n;
+        const int64_t eoff_w = shared ? 0 : static_cast<int64_t>(expert) * m.stride_w;
+        const int64_t eoff_s = shared ? 0 : static_cast<int64_t>(expert) * m.stride_sb;
+        wbase[j] = m.w + eoff_w;
+        sbase[j] = m.s + eoff_s;
+        bbase[j] = m.b + eoff_s;
+        srow[j] = static_cast<int64_t>(min(col[j], N - 1)) * m.gpr;
+        row_bytes = m.row_bytes;
+        gpr = m.gpr;
+    }
+
+    // ---- DMA sources: activation rows 16 wave + 8 i + lane / 8 (rows past
+    // the tile read row 0), code rows and scale pairs of this wave's columns
+    const uint8_t *asrc[NPL][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = 16 * wave + 8 * i + (lane >> 3);
+        const int c = (lane & 7) ^ (r & 7);
+        const int rr = r < rows ? r : 0;
+        const int64_t sr = min(max(a.row_src ? a.row_src[row0 + rr] : row0 + rr, 0), a.a_rows - 1);
+        const int64_t e = sr * a.a_ld + 8 * c;
+        asrc[0][i] = static_cast<const uint8_t *>(a.a0) + 2 * e;
+        if constexpr (NPL == 2) asrc[1][i] = static_cast<const uint8_t *>(a.a1) + 2 * e;
+    }
+    const uint8_t *bsrc[BITS == 4 ? 1 : 2];
+    if constexpr (BITS == 4) {
+        const int j = lane >> 5, r = min(wcol + j * a.col_op + ((lane >> 1) & 15), N - 1);
+        bsrc[0] = (j ? wbase[1] : wbase[0]) + static_cast<int64_t>(r) * row_bytes + 16 * (lane & 1);
+    } else {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            float v[8];
+            const int r = min(wcol + j * a.col_op + (lane >> 2), N - 1);
+            bsrc[j] = wbase[j] + static_cast<int64_t>(r) * row_bytes + 16 * (lane & 3);
+        }
+    }
+    const uint8_t *ssrc;
+    {
+        const int j = lane >> 5, r = min(wcol + j * a.col_op + (lane & 15), N - 1);
+        ssrc = (j ? sbase[1] : sbase[0]) + static_cast<int64_t>(r) * gpr * (ST == SWQ_F32 ? 4 : 2);
+    }
+    const uint32_t ring0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_ring));
+
+    auto issue = [&](int slot, int g) {
+        const uint32_t base = ring0 + slot * SLOT;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int gg = g0 + 8 * kg + i;
-                float bp = 0.f;
-                if (gg < NG) {
-                    const float bb = load_scale(bbase[j], srow[j] + gg, stype[j]);
-                    if constexpr (BITS == 4) {
-                        const float ss = load_scale(sbase[j], srow[j] + gg, stype[j]);
-                        bp = fmaf(-16.f, ss, bb);
-                    } else {
-                        bp = bb;
-                    }
-                }
-                v[i] = bp;
+        for (int p = 0; p < NPL; ++p)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) dma16(asrc[p][i] + kGroupK * 2 * g, base + p * ROWS * 128 + (16 * wave + 8 * i) * 128);
+        if constexpr (BITS == 4) {
+            dma16(bsrc[0] + 32 * g, base + A_BYTES + wave * B_WAVE);
+        } else {
+            dma16(bsrc[0] + 64 * g, base + A_BYTES + wave * B_WAVE);
+            dma16(bsrc[1] + 64 * g, base + A_BYTES + wave * B_WAVE + 1024);
+        }
+        // 2-byte scales: the aligned pair holding group g (rows hold an even
+        // number of groups); f32: the scale itself
+        dma4(ssrc + (ST == SWQ_F32 ? 4 * g : 4 * (g >> 1)), base + A_BYTES + 4 * B_WAVE + wave * 256);
+    };
+
+    f32x4_t acc[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int slot, int g) {
+        const uint8_t *sl = s_ring + slot * SLOT;
+        u32x4_t bq[2][2];
+        float sc[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if constexpr (BITS == 4) {
+                const uint2 w = *reinterpret_cast<const uint2 *>(sl + A_BYTES + wave * B_WAVE + (j * 32 + n * 2) * 16 + 8 * kg);
+                bq[j][0] = codes_q4(w.x);
+                bq[j][1] = codes_q4(w.y);
+            } else {
+                const uint4 w = *reinterpret_cast<const uint4 *>(sl + A_BYTES + wave * B_WAVE + (j * 64 + n * 4 + kg) * 16);
+                bq[j][0] = codes_q8(w.x, w.y);
+                bq[j][1] = codes_q8(w.z, w.w);
             }
-            split8(v, bh[j], bl[j]);
+            const uint32_t raw = *reinterpret_cast<const uint32_t *>(sl + A_BYTES + 4 * B_WAVE + wave * 256 + (j * 32 + n) * 4);
+            if constexpr (ST == SWQ_F32) sc[j] = __uint_as_float(raw);
+            else sc[j] = scale_of<ST>((g & 1) ? raw >> 16 : raw & 0xFFFFu);
         }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             if (16 * mt >= rows) break;
-            const float *xr = &s_xs[(16 * mt + n) * kXsPitch + g0 + 8 * kg];
-            float v[8];
-            const float4 x0 = *reinterpret_cast<const float4 *>(xr);
-            const float4 x1 = *reinterpret_cast<const float4 *>(xr + 4);
-            v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-            v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
-            u32x4_t xh, xm, xl;
-            split8x3(v, xh, xm, xl);
+            const int m = 16 * mt + n;
+            const uint8_t *ar = sl + m * 128;
+            const int c0 = ((2 * kg) ^ (m & 7)) * 16, c1 = ((2 * kg + 1) ^ (m & 7)) * 16;
+            const u32x4_t a_0 = *reinterpret_cast<const u32x4_t *>(ar + c0);
+            const u32x4_t a_1 = *reinterpret_cast<const u32x4_t *>(ar + c1);
+            u32x4_t l_0, l_1;
+            if constexpr (NPL == 2) {
+                l_0 = *reinterpret_cast<const u32x4_t *>(ar + ROWS * 128 + c0);
+                l_1 = *reinterpret_cast<const u32x4_t *>(ar + ROWS * 128 + c1);
+            }
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                acc[mt][j] = mfma(xl, bh[j], acc[mt][j]);
-                acc[mt][j] = mfma(xm, bl[j], acc[mt][j]);
-                acc[mt][j] = mfma(xm, bh[j], acc[mt][j]);
-                acc[mt][j] = mfma(xh, bl[j], acc[mt][j]);
-                acc[mt][j] = mfma(xh, bh[j], acc[mt][j]);
+                f32x4_t c = mfma(a_0, bq[j][0], f32x4_t{0.f, 0.f, 0.f, 0.f});
+                c = mfma(a_1, bq[j][1], c);
+                if constexpr (NPL == 2) {
+                    c = mfma(l_0, bq[j][0], c);
+                    c = mfma(l_1, bq[j][1], c);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[mt][j][r] = fmaf(sc[j], c[r], acc[mt][j][r]);
+            }
+        }
+    };
+
+    // ---- the ring: groups 0 .. D-2 in flight before the loop; at group g
+    // wait for it, then refill the slot group g-1 used with group g+D-1
+    // (past NG: group NG-1 again, never read)
+#pragma unroll
+    for (int s = 0; s < D - 1; ++s) issue(s, min(s, NG - 1));
+#pragma unroll 1
+    for (int g0 = 0; g0 < NG; g0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int g = g0 + u;
+            if (g < NG) {
+                ring_wait<LS * (D - 2)>();
+                issue((u + D - 1) % D, min(g + D - 1, NG - 1));
+                compute(u, g);
             }
         }
     }
 
-    // ---- epilogue: lane holds column n of rows 16 mt + 4 kg + r
+    if (active) {
+        const float *xrow[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        if (16 * mt >= rows) break;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = 16 * mt + 4 * kg + r;
-            if (row >= rows) continue;
-            const int64_t o = static_cast<int64_t>(row0 + row) * a.o_ld;
-            if constexpr (EPI == kEpiSwiGLU) {
-                if (col[0] < N) {
-                    const float h = swiglu(acc[mt][0][r], acc[mt][1][r]);
-                    uint32_t hi, lo;
-                    split_pair(h, 0.f, hi, lo);
-                    static_cast<uint16_t *>(a.o0)[o + col[0]] = static_cast<uint16_t>(hi);
-                    static_cast<uint16_t *>(a.o1)[o + col[0]] = static_cast<uint16_t>(lo);
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    if (col[j] < N) static_cast<float *>(a.o0)[o + col[j]] = acc[mt][j][r];
-            }
+        for (int mt = 0; mt < MT; ++mt) {
+            const int rr = min(16 * mt + n, rows - 1);
+            const int64_t xr = a.row_src ? a.row_src[row0 + rr] : row0 + rr;
+            xrow[mt] = a.xs_in + xr * a.xs_ld;
         }
+        bias_term<BITS, ST, MT>(acc, xrow, sbase, bbase, srow, NG, rows, kg);
+    }
+    epilogue<EPI, MT>(acc, a, col, N, active, row0, rows, nb, s_red);
+}
+
+// ---------------------------------------------------------------------------
+// activation prep: x as the bf16 planes gate/up reads (hi, and lo for fp32 x;
+// in nibble_order for 4-bit gate/up codes) and its group sums
+
+struct PrepArgs {
+    const void *x;
+    uint16_t *p0, *p1;   // planes [T, H] (null p0: x itself is read, only the sums are made)
+    float *xs;           // group sums [T, xs_ld]
+    int32_t T, H, xdt, perm, xs_ld;
+};
+
+__global__ __launch_bounds__(kPfThreads) void pf_prep(const PrepArgs a) {
+    const int64_t pc = static_cast<int64_t>(blockIdx.x) * kPfThreads + threadIdx.x;  // 8-element piece
+    const int per_row = a.H / 8;
+    const bool ok = pc < static_cast<int64_t>(a.T) * per_row;  // whole 8-lane groups (per_row % 8 == 0)
+    const int64_t e = (ok ? pc : 0) * 8;
+    u32x4_t hi, lo = {0u, 0u, 0u, 0u};
+    if (a.xdt == SWQ_BF16) {
+        hi = *reinterpret_cast<const u32x4_t *>(static_cast<const uint16_t *>(a.x) + e);
+    } else {
+        const float4 x0 = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + e);
+        const float4 x1 = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + e + 4);
+        const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        split8(v, hi, lo);
+    }
+    float t[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) t[q] = (bf16_lo(hi[q]) + bf16_lo(lo[q])) + (bf16_hi(hi[q]) + bf16_hi(lo[q]));
+    const float sum = segment_reduce((t[0] + t[1]) + (t[2] + t[3]), 3);
+    if (!ok) return;
+    const int64_t row = pc / per_row;
+    const int c8 = static_cast<int>(pc - row * per_row);
+    if ((c8 & 7) == 0) a.xs[row * a.xs_ld + c8 / 8] = sum;
+    if (a.p0) {
+        if (a.perm) {
+            hi = nibble_order(hi);
+            lo = nibble_order(lo);
+        }
+        *reinterpret_cast<u32x4_t *>(a.p0 + e) = hi;
+        if (a.p1) *reinterpret_cast<u32x4_t *>(a.p1 + e) = lo;
     }
 }
 
@@ -508,8 +851,6 @@ struct RouteArgs {
     int32_t *user_ids;
     float *user_w;
     float *sg;                // [T]
-    int32_t *slot;            // [T, K]: rank of the pair within its expert
-    int32_t *counts;          // [E]: zero on entry; left zero
     uint32_t *done;           // finished workgroups: zero on entry; left zero
     int32_t *pos;             // [T, K]: sorted index of pair (t, k)
     int32_t *tok;             // [P + T]: token of each sorted row
@@ -546,20 +887,34 @@ __device__ float row_dot(const QMat &m, const void *x, int64_t x0, int lane) {
     return wave_sum(acc);
 }
 
-// The last workgroup: exclusive scans of the pair counts and of the tile
-// counts, the tile table, the sorted pair order; then counters back to zero.
+// The last workgroup: per-expert pair counts (LDS atomics over the ids),
+// exclusive scans of the pair counts and of the tile counts, the tile table,
+// and the sorted pair order (a second pass hands out the slots; the order of
+// pairs within an expert does not matter, every row is computed on its own).
 __device__ void group_pairs(const RouteArgs &a) {
-    __shared__ int32_t s_off[kMaxExperts];
-    __shared__ int32_t s_cnt[kMaxExperts];
+    __shared__ int32_t s_cnt[kMaxExperts];  // counts, then the next free slot
     __shared__ int32_t s_part[2][kPfThreads];
     const int tid = threadIdx.x;
+    const int P = a.T * a.K;
+    constexpr int kBatch = 8;  // ids per thread per pass, all in flight at once
+    for (int e = tid; e < a.E; e += kPfThreads) s_cnt[e] = 0;
+    __syncthreads();
+    for (int p0 = tid; p0 < P; p0 += kBatch * kPfThreads) {
+        int e[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) e[u] = a.ids[min(p0 + u * kPfThreads, P - 1)];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            if (p0 + u * kPfThreads < P) atomicAdd(&s_cnt[e[u]], 1);
+    }
+    __syncthreads();
     constexpr int EPT = kMaxExperts / kPfThreads;  // experts per thread
     int cnt[EPT], tl[EPT];
     int csum = 0, tsum = 0;
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
         const int e = tid * EPT + i;
-        cnt[i] = e < a.E ? __hip_atomic_load(&a.counts[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+        cnt[i] = e < a.E ? s_cnt[e] : 0;
         tl[i] = (cnt[i] + kTileRows - 1) / kTileRows;
         csum += cnt[i];
         tsum += tl[i];
@@ -582,16 +937,13 @@ __device__ void group_pairs(const RouteArgs &a) {
     for (int i = 0; i < EPT; ++i) {
         const int e = tid * EPT + i;
         if (e < a.E) {
-            s_off[e] = c0;
-            s_cnt[e] = cnt[i];
+            s_cnt[e] = c0;  // each thread rewrites only its own experts
             for (int q = 0; q < tl[i]; ++q)
                 a.tiles[t0 + q] = Tile{e, c0 + q * kTileRows, min(kTileRows, cnt[i] - q * kTileRows), 0};
-            a.counts[e] = 0;
         }
         c0 += cnt[i];
         t0 += tl[i];
     }
-    const int P = a.T * a.K;
     const int sh_tiles = a.has_shared ? (a.T + kTileRows - 1) / kTileRows : 0;
     for (int q = tid; q < sh_tiles; q += kPfThreads)
         a.tiles[routed_tiles + q] = Tile{a.E, P + q * kTileRows, min(kTileRows, a.T - q * kTileRows), 0};
@@ -600,14 +952,18 @@ __device__ void group_pairs(const RouteArgs &a) {
         *a.done = 0u;
     }
     __syncthreads();
-    for (int p = tid; p < P; p += kPfThreads) {
-        const int e = __hip_atomic_load(&a.ids[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int s = __hip_atomic_load(&a.slot[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (e < 0 || e >= a.E || s < 0 || s >= s_cnt[e]) continue;  // counters not zeroed on entry
-        const int q = s_off[e] + s;
-        if (q >= P) continue;
-        a.pos[p] = q;
-        a.tok[q] = p / a.K;
+    for (int p0 = tid; p0 < P; p0 += kBatch * kPfThreads) {
+        int e[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) e[u] = a.ids[min(p0 + u * kPfThreads, P - 1)];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int p = p0 + u * kPfThreads;
+            if (p >= P) continue;
+            const int q = atomicAdd(&s_cnt[e[u]], 1);
+            a.pos[p] = q;
+            a.tok[q] = p / a.K;
+        }
     }
     if (a.has_shared)
         for (int t = tid; t < a.T; t += kPfThreads) a.tok[P + t] = t;
@@ -633,17 +989,18 @@ __global__ __launch_bounds__(kPfThreads) void pf_route(const RouteArgs a) {
             a.wts[p] = my_w;
             if (a.user_ids) a.user_ids[p] = my_id;
             if (a.user_w) a.user_w[p] = my_w;
-            a.slot[p] = atomicAdd(&a.counts[my_id], 1);
         }
         if (a.has_shared) {
             const float v = row_dot<XDT>(a.seg, a.x, static_cast<int64_t>(t) * a.H, lane);
             if (lane == 0) a.sg[t] = v;
         }
     }
-    // the last workgroup to arrive groups the pairs
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    // the last workgroup to arrive groups the pairs: the barrier orders this
+    // workgroup's stores before thread 0's release, the release before its
+    // count, the last arrival's acquire before its loads
     __syncthreads();
     if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         const uint32_t prev = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = prev == gridDim.x - 1;
     }
@@ -709,8 +1066,8 @@ __global__ __launch_bounds__(kPfThreads) void pf_combine(const CombineArgs a) {
 // host side
 
 struct PfLayout {
-    size_t header, counts, logits, sg, ids, wts, slot, pos, tok, tiles, h_hi, h_lo, y, total;
-    int max_tiles, Ih;
+    size_t header, logits, sg, ids, wts, pos, tok, tiles, xs_x, xs_h, xa0, xa1, h_hi, h_lo, y, total;
+    int max_tiles, Ih, xs_ld_x, xs_ld_h;
 };
 
 PfLayout pf_layout(const swq_moe_layer *l, int T) {
@@ -728,15 +1085,19 @@ PfLayout pf_layout(const swq_moe_layer *l, int T) {
                   (l->has_shared ? (T + kTileRows - 1) / kTileRows : 0);
     w.Ih = std::max(l->moe_intermediate, l->has_shared ? l->shared_intermediate : 0);
     w.header = take(256);  // [0] finished route workgroups, [1] tile count
-    w.counts = take(static_cast<size_t>(l->num_experts) * 4);
     w.logits = take(static_cast<size_t>(T) * l->num_experts * 4);
     w.sg = take(static_cast<size_t>(T) * 4);
     w.ids = take(P * 4);
     w.wts = take(P * 4);
-    w.slot = take(P * 4);
     w.pos = take(P * 4);
     w.tok = take(rows * 4);
     w.tiles = take(static_cast<size_t>(w.max_tiles) * sizeof(Tile));
+    w.xs_ld_x = ((l->hidden / kGroupK) + 31) & ~31;  // whole 32-group blocks (the bias MFMA's k)
+    w.xs_ld_h = ((w.Ih / kGroupK) + 31) & ~31;
+    w.xs_x = take(static_cast<size_t>(T) * w.xs_ld_x * 4);
+    w.xs_h = take(rows * w.xs_ld_h * 4);
+    w.xa0 = take(static_cast<size_t>(T) * l->hidden * 2);  // x planes for gate/up
+    w.xa1 = take(static_cast<size_t>(T) * l->hidden * 2);
     w.h_hi = take(rows * w.Ih * 2);
     w.h_lo = take(rows * w.Ih * 2);
     w.y = take(rows * l->hidden * 4);
@@ -746,7 +1107,7 @@ PfLayout pf_layout(const swq_moe_layer *l, int T) {
 
 // A matrix on the MFMA path: 4/8-bit codes, group 64, rows of whole 128-input
 // blocks (an even number of groups), at most 4096 inputs, 16 B aligned rows.
-int check_mfma(const swq_qlinear *l, int out_dim, int in_dim, bool stacked, int E) {
+int check_mfma(const swq_qlinear *l, int out_dim, int in_dim, bool stacked, int E, bool dma = true) {
     int st = check_linear_shape(l);
     if (st != SWQ_OK) return st;
     if (l->out_dim != out_dim || l->in_dim != in_dim) return SWQ_ERR_BAD_SHAPE;
@@ -754,6 +1115,9 @@ int check_mfma(const swq_qlinear *l, int out_dim, int in_dim, bool stacked, int 
     if (l->group_size != kGroupK) return SWQ_ERR_LIMIT;
     if (in_dim % (2 * kGroupK) != 0 || in_dim > kGroupK * kMaxGroups) return SWQ_ERR_LIMIT;
     if (!vector_path_ok(l, 0, 0, 0)) return SWQ_ERR_MISALIGNED;
+    // the LDS DMA kernels fetch 2-byte scales as aligned 4-byte pairs
+    if (dma && (((reinterpret_cast<uintptr_t>(l->scales) + l->s_off) % 4 != 0) || l->expert_stride_sb % 4 != 0))
+        return SWQ_ERR_MISALIGNED;
     if (stacked && E > 1 && (l->expert_stride_w == 0 || l->expert_stride_sb == 0)) return SWQ_ERR_INVALID_ARGUMENT;
     return SWQ_OK;
 }
@@ -767,11 +1131,12 @@ int check_prefill_layer(const swq_moe_layer *l, int T) {
     if (static_cast<int64_t>(T) * l->top_k > (1 << 24)) return SWQ_ERR_LIMIT;
     const int H = l->hidden, E = l->num_experts, I = l->moe_intermediate;
     int st;
-    if ((st = check_mfma(&l->router, E, H, false, E)) != SWQ_OK) return st;
+    if ((st = check_mfma(&l->router, E, H, false, E, false)) != SWQ_OK) return st;
     if ((st = check_mfma(&l->gate, I, H, true, E)) != SWQ_OK) return st;
     if ((st = check_mfma(&l->up, I, H, true, E)) != SWQ_OK) return st;
     if ((st = check_mfma(&l->down, H, I, true, E)) != SWQ_OK) return st;
-    if (l->gate.bits != l->up.bits) return SWQ_ERR_LIMIT;
+    // one kernel instance per launch: one code width and one scale dtype
+    if (l->gate.bits != l->up.bits || l->gate.scales_type != l->up.scales_type) return SWQ_ERR_LIMIT;
     if (l->has_shared) {
         const int Is = l->shared_intermediate;
         if (Is <= 0) return SWQ_ERR_INVALID_ARGUMENT;
@@ -785,19 +1150,51 @@ int check_prefill_layer(const swq_moe_layer *l, int T) {
         if ((static_cast<int64_t>(H) * sg.bits) % 128 != 0 || (static_cast<int64_t>(sg.group_size) * sg.bits) % 128 != 0)
             return SWQ_ERR_BAD_SHAPE;
         if (!vector_path_ok(&sg, 0, 0, 0)) return SWQ_ERR_MISALIGNED;
-        // one kernel instantiation serves the routed and the shared tiles
         if (l->shared_gate.bits != l->gate.bits || l->shared_up.bits != l->gate.bits ||
             l->shared_down.bits != l->down.bits)
+            return SWQ_ERR_LIMIT;
+        if (l->shared_gate.scales_type != l->gate.scales_type || l->shared_up.scales_type != l->gate.scales_type ||
+            l->shared_down.scales_type != l->down.scales_type)
             return SWQ_ERR_LIMIT;
     }
     return SWQ_OK;
 }
 
-template <int SRC, int MT, int EPI>
-int launch_gemm(int bits, const GemmArgs &a, int blocks, hipStream_t s) {
+template <int BITS, int SRC, int MT, int EPI, int SUM>
+void launch_gemm_st(int stype, const GemmArgs &a, int blocks, hipStream_t s) {
+    if (stype == SWQ_F16)
+        hipLaunchKernelGGL((pf_gemm<BITS, SWQ_F16, SRC, MT, EPI, SUM>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+    else if (stype == SWQ_BF16)
+        hipLaunchKernelGGL((pf_gemm<BITS, SWQ_BF16, SRC, MT, EPI, SUM>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((pf_gemm<BITS, SWQ_F32, SRC, MT, EPI, SUM>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+}
+
+template <int SRC, int MT, int EPI, int SUM>
+int launch_gemm(const swq_qlinear &lin, const GemmArgs &a, int blocks, hipStream_t s) {
     if (blocks <= 0) return SWQ_OK;
-    if (bits == 4) hipLaunchKernelGGL((pf_gemm<4, SRC, MT, EPI>), dim3(blocks), dim3(kPfThreads), 0, s, a);
-    else hipLaunchKernelGGL((pf_gemm<8, SRC, MT, EPI>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+    if (lin.bits == 4) launch_gemm_st<4, SRC, MT, EPI, SUM>(lin.scales_type, a, blocks, s);
+    else launch_gemm_st<8, SRC, MT, EPI, SUM>(lin.scales_type, a, blocks, s);
+    return launch_status();
+}
+
+// LDS ring depth: four groups for one activation plane, three for two.
+template <int BITS, int NPL, int EPI>
+void launch_dma_st(int stype, const GemmArgs &a, int blocks, hipStream_t s) {
+    constexpr int D = NPL == 1 ? 4 : 3;
+    if (stype == SWQ_F16)
+        hipLaunchKernelGGL((pf_gemm_dma<BITS, SWQ_F16, NPL, EPI, D>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+    else if (stype == SWQ_BF16)
+        hipLaunchKernelGGL((pf_gemm_dma<BITS, SWQ_BF16, NPL, EPI, D>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((pf_gemm_dma<BITS, SWQ_F32, NPL, EPI, D>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+}
+
+template <int NPL, int EPI>
+int launch_dma(const swq_qlinear &lin, const GemmArgs &a, int blocks, hipStream_t s) {
+    if (blocks <= 0) return SWQ_OK;
+    if (lin.bits == 4) launch_dma_st<4, NPL, EPI>(lin.scales_type, a, blocks, s);
+    else launch_dma_st<8, NPL, EPI>(lin.scales_type, a, blocks, s);
     return launch_status();
 }
 
@@ -834,9 +1231,33 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
     uint16_t *h_hi = reinterpret_cast<uint16_t *>(wsb + wl.h_hi);
     uint16_t *h_lo = reinterpret_cast<uint16_t *>(wsb + wl.h_lo);
     float *y = reinterpret_cast<float *>(wsb + wl.y);
+    float *xs_x = reinterpret_cast<float *>(wsb + wl.xs_x);
+    float *xs_h = reinterpret_cast<float *>(wsb + wl.xs_h);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool bf16x = x_dtype == SWQ_BF16;
 
+    // 0. x planes for gate/up (nibble_order for 4-bit codes, hi/lo for fp32 x)
+    //    and the group sums of x
+    const bool perm_x = layer->gate.bits == 4;
+    const bool planes = perm_x || !bf16x;
+    uint16_t *xa0 = reinterpret_cast<uint16_t *>(wsb + wl.xa0);
+    uint16_t *xa1 = reinterpret_cast<uint16_t *>(wsb + wl.xa1);
+    {
+        PrepArgs pa{};
+        pa.x = x;
+        pa.p0 = planes ? xa0 : nullptr;
+        pa.p1 = planes && !bf16x ? xa1 : nullptr;
+        pa.xs = xs_x;
+        pa.T = T;
+        pa.H = H;
+        pa.xdt = x_dtype;
+        pa.perm = perm_x ? 1 : 0;
+        pa.xs_ld = wl.xs_ld_x;
+        const int64_t pieces = static_cast<int64_t>(T) * H / 8;
+        hipLaunchKernelGGL(pf_prep, dim3(static_cast<unsigned>((pieces + kPfThreads - 1) / kPfThreads)),
+                           dim3(kPfThreads), 0, s, pa);
+        if ((st = launch_status()) != SWQ_OK) return st;
+    }
     // 1. router logits
     {
         GemmArgs g{};
@@ -854,9 +1275,9 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         g.col_wave = 32;
         g.col_op = 16;
         g.nblk = (E + 127) / 128;
-        const int blocks = ((T + kRouterRows - 1) / kRouterRows) * g.nblk;
-        st = bf16x ? launch_gemm<kSrcBF16, 1, kEpiRows>(layer->router.bits, g, blocks, s)
-                   : launch_gemm<kSrcF32, 1, kEpiRows>(layer->router.bits, g, blocks, s);
+        const int blocks = gemm_blocks((T + kRouterRows - 1) / kRouterRows, g.nblk);
+        st = bf16x ? launch_gemm<kSrcBF16, 1, kEpiRows, kSumStage>(layer->router, g, blocks, s)
+                   : launch_gemm<kSrcF32, 1, kEpiRows, kSumStage>(layer->router, g, blocks, s);
         if (st != SWQ_OK) return st;
     }
     // 2. routing and grouping
@@ -871,8 +1292,6 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         r.user_ids = topk_ids;
         r.user_w = topk_weights;
         r.sg = sg;
-        r.slot = reinterpret_cast<int32_t *>(wsb + wl.slot);
-        r.counts = reinterpret_cast<int32_t *>(wsb + wl.counts);
         r.done = header;
         r.pos = pos;
         r.tok = tok;
@@ -898,7 +1317,8 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
             g.sh[0] = make_qmat(&layer->shared_gate);
             g.sh[1] = make_qmat(&layer->shared_up);
         }
-        g.a0 = x;
+        g.a0 = planes ? static_cast<const void *>(xa0) : x;
+        g.a1 = xa1;
         g.a_ld = H;
         g.row_src = tok;
         g.tiles = tiles;
@@ -906,8 +1326,13 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         g.o0 = h_hi;
         g.o1 = h_lo;
         g.o_ld = wl.Ih;
+        g.o_perm = layer->down.bits == 4 ? 1 : 0;
         g.rows_total = rows_sorted;
         g.a_rows = T;
+        g.xs_in = xs_x;
+        g.xs_out = xs_h;
+        g.xs_ld = wl.xs_ld_x;
+        g.xs_ld_out = wl.xs_ld_h;
         g.K = g.Ksh = H;
         g.N = I;
         g.Nsh = Is;
@@ -916,9 +1341,9 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         g.col_wave = 16;
         g.col_op = 0;
         g.nblk = (wl.Ih + 63) / 64;
-        const int blocks = wl.max_tiles * g.nblk;
-        st = bf16x ? launch_gemm<kSrcBF16, 4, kEpiSwiGLU>(layer->gate.bits, g, blocks, s)
-                   : launch_gemm<kSrcF32, 4, kEpiSwiGLU>(layer->gate.bits, g, blocks, s);
+        const int blocks = gemm_blocks(wl.max_tiles, g.nblk);
+        st = bf16x ? launch_dma<1, kEpiSwiGLU>(layer->gate, g, blocks, s)
+                   : launch_dma<2, kEpiSwiGLU>(layer->gate, g, blocks, s);
         if (st != SWQ_OK) return st;
     }
     // 4. down over the tiles
@@ -935,6 +1360,8 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         g.o_ld = H;
         g.rows_total = rows_sorted;
         g.a_rows = rows_sorted;
+        g.xs_in = xs_h;
+        g.xs_ld = wl.xs_ld_h;
         g.K = I;
         g.Ksh = Is;
         g.N = g.Nsh = H;
@@ -943,8 +1370,8 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         g.col_wave = 32;
         g.col_op = 16;
         g.nblk = (H + 127) / 128;
-        const int blocks = wl.max_tiles * g.nblk;
-        if ((st = launch_gemm<kSrcSplit, 4, kEpiRows>(layer->down.bits, g, blocks, s)) != SWQ_OK) return st;
+        const int blocks = gemm_blocks(wl.max_tiles, g.nblk);
+        if ((st = launch_dma<2, kEpiRows>(layer->down, g, blocks, s)) != SWQ_OK) return st;
     }
     // 5. weighted combine in pick order, then the gated shared expert
     {
