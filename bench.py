@@ -13,6 +13,13 @@ single-launch path), so the graph's average step is that kernel's average
 launch; for batches (three launches) the per-kernel durations come from graph
 replays of each stage on its own, timed with HIP events.  Prints one JSON
 line.
+
+The prefill workload (--config qwen3.6-35b-a3b-q4-prefill512) times one
+512-token chunk through swq_moe_prefill: router GEMM, top-k and grouping of
+the 4096 (token, expert) pairs, grouped gate/up and down on the bf16 matrix
+cores, combine.  A per-expert logit bias skews the expert load towards
+Zipf(1.1).  The decode line carries a summary of the same measurement under
+"prefill" (skip it with --no-prefill).
 """
 
 from __future__ import annotations
@@ -42,6 +49,14 @@ MEASURED_TRAFFIC = {
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 5_743_112,
 }
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
+
+# prefill workloads: name -> (shape key, tokens, Zipf seed of the logit bias)
+PREFILL_CONFIGS = {
+    "qwen3.6-35b-a3b-q4-prefill512": ("qwen3.6-35b-a3b-q4", 512, 2024),
+}
+PREFILL_STAGES = [("prep", 1), ("router", 2), ("route", 4), ("gate_up", 8), ("down", 16), ("combine", 32)]
+
 CONFIGS = {
     # name: (shape key, batch)
     "qwen3.6-35b-a3b-q4-b1": ("qwen3.6-35b-a3b-q4", 1),
@@ -56,7 +71,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=960)
     ap.add_argument("--warmup", type=int, default=96)
-    ap.add_argument("--config", default="qwen3.6-35b-a3b-q4-b1", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="qwen3.6-35b-a3b-q4-b1", choices=sorted(CONFIGS) + sorted(PREFILL_CONFIGS))
+    ap.add_argument("--no-prefill", action="store_true", help="decode line without the prefill summary")
+    ap.add_argument("--prefill-steps", type=int, default=40, help="prefill chunks timed")
+    ap.add_argument("--prefill-replicas", type=int, default=3, help="distinct layers the prefill chunks cycle")
     ap.add_argument("--replicas", type=int, default=48, help="distinct layers cycled through (MALL defeat)")
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
@@ -96,6 +114,14 @@ def main():
         from swiftlet_amd import build
         build.build()
     lib = _lib.load()
+
+    if args.config in PREFILL_CONFIGS:
+        res = prefill_measure(args, torch, lib, args.config)
+        line = prefill_line(args, res)
+        if not args.no_cpu_baseline:
+            line["cpu_baseline"] = prefill_cpu_baseline(args, res)
+        print(json.dumps(line), flush=True)
+        return
 
     shape_key, batch = CONFIGS[args.config]
     path = args.path if args.path != "auto" else ("fused" if batch == 1 else "staged")
@@ -258,7 +284,167 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, shape, batch, layers[0], xs_bits[0])
 
+    # ---- the prefill chunk, summarised --------------------------------------
+    if not args.no_prefill:
+        del layers, wss, graph
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        res = prefill_measure(args, torch, lib, "qwen3.6-35b-a3b-q4-prefill512")
+        line = prefill_line(args, res)
+        result["prefill"] = {k: line[k] for k in ("config", "value", "unit", "roofline", "kernel_us", "mfma")}
+
     print(json.dumps(result), flush=True)
+
+
+def prefill_measure(args, torch, lib, name):
+    """Time the prefill chunk: a graph of --prefill-steps full chunks cycling
+    --prefill-replicas layers, then each launch alone (graph replays of that
+    stage over the replicas, whose workspaces hold the earlier stages'
+    outputs)."""
+    from swiftlet_amd import _lib, moe, synth
+    from swiftlet_amd._lib import check
+
+    shape_key, T, zipf_seed = PREFILL_CONFIGS[name]
+    shape = synth.SHAPES[shape_key]
+    H, E, K = shape.hidden, shape.experts, shape.top_k
+    R = args.prefill_replicas
+    dev = "cuda"
+    layers = [moe.synth_layer(shape, args.seed, 100 + r, dev) for r in range(R)]
+    bias = torch.from_numpy(synth.zipf_logit_bias(zipf_seed, E)).to(dev)
+    xs_bits = synth.activations_bf16(args.seed + 11, R * T, H).reshape(R, T, H)
+    xs = torch.from_numpy(xs_bits.view(np.int16)).view(torch.bfloat16).to(dev)
+    wss = [l.new_prefill_workspace(T) for l in layers]
+    outs = torch.empty((R, T, H), dtype=torch.bfloat16, device=dev)
+    ids = torch.empty((R, T, K), dtype=torch.int32, device=dev)
+    wts = torch.empty((R, T, K), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    calls = [(ctypes.byref(l._c), ctypes.c_void_p(xs[r].data_ptr()), _lib.SWQ_BF16, T,
+              ctypes.c_void_p(outs[r].data_ptr()), _lib.SWQ_BF16, ctypes.c_void_p(ids[r].data_ptr()),
+              ctypes.c_void_p(wts[r].data_ptr()), ctypes.c_void_p(bias.data_ptr()),
+              ctypes.c_void_p(wss[r].data_ptr()), wss[r].numel(), 0) for r, l in enumerate(layers)]
+
+    def graph_of(n, mask):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for i in range(n):
+                check(lib.swq_moe_prefill_stages(*calls[i % R], mask, cap), "moe_prefill (capture)")
+        return g
+
+    def timed(g, n):
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / n
+
+    sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for r in range(R):
+        check(lib.swq_moe_prefill_stages(*calls[r], _lib.SWQ_PREFILL_ALL, sh), "moe_prefill")
+    torch.cuda.synchronize()
+    Kp = args.prefill_steps
+    us_chunk = timed(graph_of(Kp, _lib.SWQ_PREFILL_ALL), Kp)
+    n_st = 4 * R
+    stage_us = {nm: timed(graph_of(n_st, bit), n_st) for nm, bit in PREFILL_STAGES}
+
+    ids_h = ids.cpu().numpy()
+    counts = [np.bincount(ids_h[r].ravel(), minlength=E) for r in range(R)]
+    touched = float(np.mean([(c > 0).sum() for c in counts]))
+    tiles = float(np.mean([((c + 63) // 64).sum() for c in counts])) + (T + 63) // 64
+    I, Is = shape.inter, shape.shared_inter
+    mb, eb, rb = shape.matrix_bytes, shape.expert_bits, shape.router_bits
+    xb = T * H * 2
+    P = T * K
+    kbytes = {
+        "prep": xb,
+        "router": mb(E, H, rb) + xb,
+        "route": mb(1, H, rb) + xb,
+        "gate_up": touched * 2 * mb(I, H, eb) + 2 * mb(Is, H, eb) + xb,
+        "down": touched * mb(H, I, eb) + mb(H, Is, eb),
+        "combine": xb,
+    }
+    kflops = {
+        "router": 2.0 * T * E * H,
+        "gate_up": 2.0 * 2 * (P * I + T * Is) * H,
+        "down": 2.0 * (P * I + T * Is) * H,
+    }
+    chunk_bytes = touched * shape.expert_bytes() + shape.shared_bytes() + shape.router_bytes() \
+        + shape.seg_bytes() + 2 * xb
+    return {"name": name, "shape": shape, "T": T, "R": R, "zipf_seed": zipf_seed, "us_chunk": us_chunk,
+            "stage_us": stage_us, "kbytes": kbytes, "kflops": kflops, "chunk_bytes": chunk_bytes,
+            "touched": touched, "tiles": tiles, "max_count": int(np.max([c.max() for c in counts])),
+            "counts_sorted": sorted((int(v) for v in counts[0]), reverse=True)}
+
+
+def prefill_line(args, res):
+    shape, T = res["shape"], res["T"]
+    st, kb, kf = res["stage_us"], res["kbytes"], res["kflops"]
+    dom = max(st, key=st.get)
+    gbs = kb[dom] / (st[dom] * 1e-6) / 1e9
+    mfma = {k: {"tflops": round(kf[k] / (st[k] * 1e-6) / 1e12, 1),
+                "frac": round(kf[k] / (st[k] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)} for k in kf}
+    return {
+        "metric": "us per 512-token MoE-layer prefill chunk; achieved HBM GB/s and MFMA TFLOP/s as fractions of peak (1 GPU)",
+        "value": round(res["us_chunk"], 2),
+        "unit": "us/chunk",
+        "n_gpus": 1,
+        "steps": args.prefill_steps,
+        "warmup": res["R"],
+        "ms_per_step": round(res["us_chunk"] / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4-affine x bf16 on bf16 MFMA, fp32 accumulate",
+        "data": f"synthetic seeded weights (seed {args.seed}), {res['R']} distinct resident layers cycled, "
+                f"bf16 x ~N(0,1), Zipf(1.1) per-expert logit bias (seed {res['zipf_seed']})",
+        "config": {"workload": res["name"], "tokens": T, "hidden": shape.hidden, "experts": shape.experts,
+                   "top_k": shape.top_k, "moe_intermediate": shape.inter,
+                   "shared_intermediate": shape.shared_inter, "expert_bits": shape.expert_bits,
+                   "router_bits": shape.router_bits, "group": shape.group, "parallelism": "single GPU",
+                   "experts_touched": res["touched"], "tiles": res["tiles"], "max_expert_pairs": res["max_count"]},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": int(kb[dom]), "avg_launch_us": round(st[dom], 3)},
+        "mfma": mfma,
+        "kernel_us": {k: round(v, 3) for k, v in st.items()},
+        "chunk_bytes": int(res["chunk_bytes"]),
+        "chunk_gbs": round(res["chunk_bytes"] / (res["us_chunk"] * 1e-6) / 1e9, 1),
+        "expert_pairs_sorted": res["counts_sorted"][:32],
+    }
+
+
+def prefill_cpu_baseline(args, res):
+    """The C restatement of the reference's per-token path (each pick's expert
+    dequantised per token, QwenCPUModel.moeForward at S = 1, as the reference
+    runs a prompt token by token) on a 16-token sample of layer 0's shape,
+    scaled to the chunk."""
+    from oracle import cref
+    from swiftlet_amd import moe, synth
+
+    if not cref.LIB.exists():
+        import subprocess
+        subprocess.run(["make", "-C", os.path.join(ROOT, "oracle")], check=True, capture_output=True)
+    shape = res["shape"]
+    arrays = moe.host_layer_arrays(shape, args.seed, 0)
+    c = cref.CMoE(arrays, shape.hidden, shape.experts, shape.top_k, shape.inter, shape.shared_inter,
+                  shape.group, shape.norm_topk_prob)
+    xs = synth.bf16_to_f32(synth.activations_bf16(args.seed + 98, 16, shape.hidden))
+    times = []
+    t0 = time.perf_counter()
+    for i in range(16):
+        if time.perf_counter() - t0 > args.cpu_seconds:
+            break
+        t = time.perf_counter()
+        c.forward(xs[i:i + 1], 1)
+        times.append(time.perf_counter() - t)
+    per_tok = float(np.median(times)) * 1e6
+    return {"value": round(per_tok * res["T"], 1), "unit": "us/chunk", "cores": 1, "kind": "port",
+            "sample": f"{len(times)} single-token steps (median {per_tok:.1f} us) x {res['T']} tokens; "
+                      f"C restatement of QwenCPUModel.moeForward, experts dequantised per token",
+            "cpu": cpu_model(), "nproc": os.cpu_count()}
 
 
 def cpu_baseline(args, shape, batch, layer0, x0_bits):

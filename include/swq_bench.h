@@ -61,6 +61,17 @@ int swq_moe_prefill_biased(const swq_moe_layer *layer, const void *x, int x_dtyp
                            int out_dtype, int32_t *topk_ids, float *topk_weights, const float *logit_bias,
                            void *ws, size_t ws_bytes, int flags, void *stream);
 
+/* swq_moe_prefill_biased (logit_bias may be NULL: none) running only the
+ * launches whose bits are set in stage_mask: 1 activation prep, 2 router
+ * GEMM, 4 routing and grouping, 8 gate/up + SwiGLU, 16 down, 32 combine.  A
+ * launch reads what the earlier ones left in the workspace (a full call on
+ * the same inputs leaves everything each one needs). */
+enum { SWQ_PREFILL_ALL = 63 };
+
+int swq_moe_prefill_stages(const swq_moe_layer *layer, const void *x, int x_dtype, int tokens, void *out,
+                           int out_dtype, int32_t *topk_ids, float *topk_weights, const float *logit_bias,
+                           void *ws, size_t ws_bytes, int flags, int stage_mask, void *stream);
+
 /* One single-wave kernel that sleeps `iterations` times (s_sleep 127, about
  * 8k cycles each) and exits; iterations <= 1000000. */
 int swq_bench_stall(int iterations, void *stream);

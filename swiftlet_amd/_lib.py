@@ -26,6 +26,7 @@ SWQ_F32, SWQ_F16, SWQ_BF16 = 0, 1, 2
 SWQ_MAX_BATCH, SWQ_MAX_TOPK = 16, 16
 SWQ_MOE_ACCUMULATE = 1
 SWQ_STAGES_FUSED = 8  # swq_bench.h: the single-launch path
+SWQ_PREFILL_ALL = 63  # swq_bench.h: every launch of swq_moe_prefill_stages
 
 
 class SwqError(RuntimeError):
@@ -87,6 +88,7 @@ SIGNATURES = {
     "swq_moe_prefill_workspace_bytes": (_SZ, [_c.POINTER(MoELayer), _I]),
     "swq_moe_prefill": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _I, _P]),
     "swq_moe_prefill_biased": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _P, _SZ, _I, _P]),
+    "swq_moe_prefill_stages": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _P, _SZ, _I, _I, _P]),
 }
 
 _lib = None

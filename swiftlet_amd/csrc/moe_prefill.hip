@@ -35,6 +35,7 @@
 
 #include <algorithm>
 
+#include "../../include/swq_bench.h"
 #include "moe_host.hpp"
 #include "route.hpp"
 
@@ -1200,8 +1201,9 @@ int launch_dma(const swq_qlinear &lin, const GemmArgs &a, int blocks, hipStream_
 
 int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, void *out, int out_dtype,
                  int32_t *topk_ids, float *topk_weights, const float *logit_bias, void *ws, size_t ws_bytes,
-                 int flags, void *stream) {
+                 int flags, int stage_mask, void *stream) {
     if (x_dtype != SWQ_F32 && x_dtype != SWQ_BF16) return SWQ_ERR_UNSUPPORTED_DTYPE;
+    if (stage_mask <= 0 || stage_mask > SWQ_PREFILL_ALL) return SWQ_ERR_INVALID_ARGUMENT;
     int st = check_prefill_layer(layer, T);
     if (st != SWQ_OK) return st;
     if (!x || !out) return SWQ_ERR_INVALID_ARGUMENT;
@@ -1242,7 +1244,7 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
     const bool planes = perm_x || !bf16x;
     uint16_t *xa0 = reinterpret_cast<uint16_t *>(wsb + wl.xa0);
     uint16_t *xa1 = reinterpret_cast<uint16_t *>(wsb + wl.xa1);
-    {
+    if (stage_mask & 1) {
         PrepArgs pa{};
         pa.x = x;
         pa.p0 = planes ? xa0 : nullptr;
@@ -1259,7 +1261,7 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         if ((st = launch_status()) != SWQ_OK) return st;
     }
     // 1. router logits
-    {
+    if (stage_mask & 2) {
         GemmArgs g{};
         g.m[0] = g.m[1] = make_qmat(&layer->router);
         g.a0 = x;
@@ -1281,7 +1283,7 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         if (st != SWQ_OK) return st;
     }
     // 2. routing and grouping
-    {
+    if (stage_mask & 4) {
         RouteArgs r{};
         if (layer->has_shared) r.seg = make_qmat(&layer->shared_expert_gate);
         r.x = x;
@@ -1309,7 +1311,7 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         if ((st = launch_status()) != SWQ_OK) return st;
     }
     // 3. gate/up + SwiGLU over the tiles
-    {
+    if (stage_mask & 8) {
         GemmArgs g{};
         g.m[0] = make_qmat(&layer->gate);
         g.m[1] = make_qmat(&layer->up);
@@ -1347,7 +1349,7 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         if (st != SWQ_OK) return st;
     }
     // 4. down over the tiles
-    {
+    if (stage_mask & 16) {
         GemmArgs g{};
         g.m[0] = g.m[1] = make_qmat(&layer->down);
         if (layer->has_shared) g.sh[0] = g.sh[1] = make_qmat(&layer->shared_down);
@@ -1374,7 +1376,7 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         if ((st = launch_dma<2, kEpiRows>(layer->down, g, blocks, s)) != SWQ_OK) return st;
     }
     // 5. weighted combine in pick order, then the gated shared expert
-    {
+    if (stage_mask & 32) {
         CombineArgs c{};
         c.y = y;
         c.pos = pos;
@@ -1408,7 +1410,7 @@ extern "C" int swq_moe_prefill(const swq_moe_layer *layer, const void *x, int x_
                                int out_dtype, int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes,
                                int flags, void *stream) {
     return prefill_impl(layer, x, x_dtype, tokens, out, out_dtype, topk_ids, topk_weights, nullptr, ws, ws_bytes,
-                        flags, stream);
+                        flags, SWQ_PREFILL_ALL, stream);
 }
 
 extern "C" int swq_moe_prefill_biased(const swq_moe_layer *layer, const void *x, int x_dtype, int tokens,
@@ -1416,5 +1418,13 @@ extern "C" int swq_moe_prefill_biased(const swq_moe_layer *layer, const void *x,
                                       const float *logit_bias, void *ws, size_t ws_bytes, int flags, void *stream) {
     if (!logit_bias) return SWQ_ERR_INVALID_ARGUMENT;
     return prefill_impl(layer, x, x_dtype, tokens, out, out_dtype, topk_ids, topk_weights, logit_bias, ws, ws_bytes,
-                        flags, stream);
+                        flags, SWQ_PREFILL_ALL, stream);
+}
+
+extern "C" int swq_moe_prefill_stages(const swq_moe_layer *layer, const void *x, int x_dtype, int tokens, void *out,
+                                      int out_dtype, int32_t *topk_ids, float *topk_weights,
+                                      const float *logit_bias, void *ws, size_t ws_bytes, int flags, int stage_mask,
+                                      void *stream) {
+    return prefill_impl(layer, x, x_dtype, tokens, out, out_dtype, topk_ids, topk_weights, logit_bias, ws, ws_bytes,
+                        flags, stage_mask, stream);
 }
