@@ -96,6 +96,7 @@ struct GemmArgs {
     float *xs_out;
     int32_t xs_ld, xs_ld_out;
     int32_t o_perm;           // SwiGLU output in nibble_order within each 8 columns (4-bit down)
+    int32_t max_tiles;        // entries of the tile table
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -266,6 +267,82 @@ __device__ __forceinline__ void bias_term(f32x4_t (&acc)[MT][2], const float *co
                 acc[mt][j] = mfma(xh, bl[j], acc[mt][j]);
                 acc[mt][j] = mfma(xh, bh[j], acc[mt][j]);
             }
+        }
+    }
+}
+
+// Inputs of the bias term (one 32-group block: rows of at most 2048 inputs),
+// loaded before the K loop so that they arrive while it runs.
+template <int ST, int MT>
+struct BiasIn {
+    uint32_t b[2][ST == SWQ_F32 ? 8 : 4];  // operand j: biases of groups 8 kg .. +7 (raw; fp16 pairs)
+    uint32_t s[2][ST == SWQ_F32 ? 8 : 4];  // the scales of the same groups
+    float x[MT][8];                        // group sums of the lane's A rows 16 mt + n
+};
+
+template <int ST, int MT>
+__device__ __forceinline__ void load_bias_in(BiasIn<ST, MT> &bi, const float *const (&xrow)[MT],
+                                             const uint8_t *const (&sbase)[2], const uint8_t *const (&bbase)[2],
+                                             const int64_t (&srow)[2], int NG, int kg) {
+    constexpr int W = ST == SWQ_F32 ? 8 : 4;
+    constexpr int EB = ST == SWQ_F32 ? 4 : 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+            // group index of the word, clamped into the row (rows hold an even number of groups)
+            const int gi = min(8 * kg + (ST == SWQ_F32 ? i : 2 * i), NG - (ST == SWQ_F32 ? 1 : 2));
+            bi.b[j][i] = *reinterpret_cast<const uint32_t *>(bbase[j] + (srow[j] + gi) * EB);
+            bi.s[j][i] = *reinterpret_cast<const uint32_t *>(sbase[j] + (srow[j] + gi) * EB);
+        }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const float4 x0 = *reinterpret_cast<const float4 *>(xrow[mt] + 8 * kg);
+        const float4 x1 = *reinterpret_cast<const float4 *>(xrow[mt] + 8 * kg + 4);
+        bi.x[mt][0] = x0.x; bi.x[mt][1] = x0.y; bi.x[mt][2] = x0.z; bi.x[mt][3] = x0.w;
+        bi.x[mt][4] = x1.x; bi.x[mt][5] = x1.y; bi.x[mt][6] = x1.z; bi.x[mt][7] = x1.w;
+    }
+}
+
+// bias_term on preloaded inputs (NG <= 32).
+template <int BITS, int ST, int MT>
+__device__ __forceinline__ void bias_term_pre(f32x4_t (&acc)[MT][2], const BiasIn<ST, MT> &bi, int NG, int rows,
+                                              int kg) {
+    u32x4_t bh[2], bl[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t rb, rs;
+            if constexpr (ST == SWQ_F32) {
+                rb = bi.b[j][i];
+                rs = bi.s[j][i];
+            } else {
+                rb = (i & 1) ? bi.b[j][i >> 1] >> 16 : bi.b[j][i >> 1] & 0xFFFFu;
+                rs = (i & 1) ? bi.s[j][i >> 1] >> 16 : bi.s[j][i >> 1] & 0xFFFFu;
+            }
+            float bp = scale_of<ST>(rb);
+            if constexpr (BITS == 4) bp = fmaf(-16.f, scale_of<ST>(rs), bp);
+            v[i] = 8 * kg + i < NG ? bp : 0.f;
+        }
+        split8(v, bh[j], bl[j]);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        if (16 * mt >= rows) break;
+        float xv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = 8 * kg + i < NG ? bi.x[mt][i] : 0.f;
+        u32x4_t xh, xm, xl;
+        split8x3(xv, xh, xm, xl);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            acc[mt][j] = mfma(xl, bh[j], acc[mt][j]);
+            acc[mt][j] = mfma(xm, bl[j], acc[mt][j]);
+            acc[mt][j] = mfma(xm, bh[j], acc[mt][j]);
+            acc[mt][j] = mfma(xh, bl[j], acc[mt][j]);
+            acc[mt][j] = mfma(xh, bh[j], acc[mt][j]);
         }
     }
 }
@@ -632,8 +709,10 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_dma(const GemmArgs a) {
 
     const int xcd = blockIdx.x & (kXcds - 1), q = blockIdx.x >> 3;
     const int ti = (q / a.nblk) * kXcds + xcd, nb = q % a.nblk;
-    if (ti >= *a.n_tiles) return;
-    const Tile t = a.tiles[ti];
+    // the count and the entry in one round trip
+    const int n_tiles = *a.n_tiles;
+    const Tile t = a.tiles[min(ti, a.max_tiles - 1)];
+    if (ti >= n_tiles) return;
     const int expert = t.expert, row0 = t.row0, rows = t.rows;
     // a table from a workspace that skipped swq_moe_workspace_init
     if (expert < 0 || expert > a.E || rows <= 0 || rows > ROWS || row0 < 0 || row0 + rows > a.rows_total) return;
@@ -765,6 +844,21 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_dma(const GemmArgs a) {
         }
     };
 
+    // ---- the bias term's inputs, issued before the ring so that they are
+    // older than every DMA (ring_wait's counts stay exact) and arrive during
+    // the loop
+    BiasIn<ST, MT> bi;
+    {
+        const float *xrow[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int rr = min(16 * mt + n, rows - 1);
+            const int64_t xr = a.row_src ? a.row_src[row0 + rr] : row0 + rr;
+            xrow[mt] = a.xs_in + xr * a.xs_ld;
+        }
+        load_bias_in<ST, MT>(bi, xrow, sbase, bbase, srow, NG, kg);
+    }
+
     // ---- the ring: groups 0 .. D-2 in flight before the loop; at group g
     // wait for it, then refill the slot group g-1 used with group g+D-1
     // (past NG: group NG-1 again, never read)
@@ -783,16 +877,7 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_dma(const GemmArgs a) {
         }
     }
 
-    if (active) {
-        const float *xrow[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const int rr = min(16 * mt + n, rows - 1);
-            const int64_t xr = a.row_src ? a.row_src[row0 + rr] : row0 + rr;
-            xrow[mt] = a.xs_in + xr * a.xs_ld;
-        }
-        bias_term<BITS, ST, MT>(acc, xrow, sbase, bbase, srow, NG, rows, kg);
-    }
+    if (active) bias_term_pre<BITS, ST, MT>(acc, bi, NG, rows, kg);
     epilogue<EPI, MT>(acc, a, col, N, active, row0, rows, nb, s_red);
 }
 
@@ -1116,8 +1201,11 @@ int check_mfma(const swq_qlinear *l, int out_dim, int in_dim, bool stacked, int 
     if (l->group_size != kGroupK) return SWQ_ERR_LIMIT;
     if (in_dim % (2 * kGroupK) != 0 || in_dim > kGroupK * kMaxGroups) return SWQ_ERR_LIMIT;
     if (!vector_path_ok(l, 0, 0, 0)) return SWQ_ERR_MISALIGNED;
-    // the LDS DMA kernels fetch 2-byte scales as aligned 4-byte pairs
-    if (dma && (((reinterpret_cast<uintptr_t>(l->scales) + l->s_off) % 4 != 0) || l->expert_stride_sb % 4 != 0))
+    // the LDS DMA kernels fetch 2-byte scales and biases as aligned 4-byte
+    // pairs, and take the bias term over one block of 32 groups
+    if (dma && in_dim > 32 * kGroupK) return SWQ_ERR_LIMIT;
+    if (dma && (((reinterpret_cast<uintptr_t>(l->scales) + l->s_off) % 4 != 0) ||
+                ((reinterpret_cast<uintptr_t>(l->biases) + l->b_off) % 4 != 0) || l->expert_stride_sb % 4 != 0))
         return SWQ_ERR_MISALIGNED;
     if (stacked && E > 1 && (l->expert_stride_w == 0 || l->expert_stride_sb == 0)) return SWQ_ERR_INVALID_ARGUMENT;
     return SWQ_OK;
@@ -1343,6 +1431,7 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         g.col_wave = 16;
         g.col_op = 0;
         g.nblk = (wl.Ih + 63) / 64;
+        g.max_tiles = wl.max_tiles;
         const int blocks = gemm_blocks(wl.max_tiles, g.nblk);
         st = bf16x ? launch_dma<1, kEpiSwiGLU>(layer->gate, g, blocks, s)
                    : launch_dma<2, kEpiSwiGLU>(layer->gate, g, blocks, s);
@@ -1372,6 +1461,7 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         g.col_wave = 32;
         g.col_op = 16;
         g.nblk = (H + 127) / 128;
+        g.max_tiles = wl.max_tiles;
         const int blocks = gemm_blocks(wl.max_tiles, g.nblk);
         if ((st = launch_dma<2, kEpiRows>(layer->down, g, blocks, s)) != SWQ_OK) return st;
     }
