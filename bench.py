@@ -47,6 +47,8 @@ MEASURED_TRAFFIC = {
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_692_148,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 14_590_849,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 5_743_112,
+    ("qwen3.6-35b-a3b-q4-prefill512", "gate_up"): 353_769_995,
+    ("qwen3.6-35b-a3b-q4-prefill512", "down"): 210_206_539,
 }
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
@@ -115,6 +117,15 @@ def main():
         build.build()
     lib = _lib.load()
 
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     if args.config in PREFILL_CONFIGS:
         res = prefill_measure(args, torch, lib, args.config)
         line = prefill_line(args, res)
@@ -133,14 +144,6 @@ def main():
     stream = torch.cuda.current_stream()
     sh = ctypes.c_void_p(stream.cuda_stream)
 
-    if args.copy_calibration:
-        n = args.copy_calibration << 20
-        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
 
     # ---- resident weights: R distinct layers, all experts --------------
     layers = [moe.synth_layer(shape, args.seed, r, dev) for r in range(R)]
@@ -406,7 +409,8 @@ def prefill_line(args, res):
                    "router_bits": shape.router_bits, "group": shape.group, "parallelism": "single GPU",
                    "experts_touched": res["touched"], "tiles": res["tiles"], "max_expert_pairs": res["max_count"]},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": MEASURED_TRAFFIC.get((res["name"], dom)),
                      "algorithmic_bytes_per_launch": int(kb[dom]), "avg_launch_us": round(st[dom], 3)},
         "mfma": mfma,
         "kernel_us": {k: round(v, 3) for k, v in st.items()},
