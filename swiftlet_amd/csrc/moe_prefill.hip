@@ -271,19 +271,19 @@ __device__ __forceinline__ void bias_term(f32x4_t (&acc)[MT][2], const float *co
     }
 }
 
-// Inputs of the bias term (one 32-group block: rows of at most 2048 inputs),
-// loaded before the K loop so that they arrive while it runs.
-template <int ST, int MT>
-struct BiasIn {
-    uint32_t b[2][ST == SWQ_F32 ? 8 : 4];  // operand j: biases of groups 8 kg .. +7 (raw; fp16 pairs)
-    uint32_t s[2][ST == SWQ_F32 ? 8 : 4];  // the scales of the same groups
-    float x[MT][8];                        // group sums of the lane's A rows 16 mt + n
+// Biases and scales of the bias term (one 32-group block: rows of at most
+// 2048 inputs): this lane's groups 8 kg .. +7 of both operands, raw (fp16 or
+// bf16 in pairs, or f32), loaded before the K loop so they arrive during it.
+template <int ST>
+struct BiasBS {
+    uint32_t b[2][ST == SWQ_F32 ? 8 : 4];
+    uint32_t s[2][ST == SWQ_F32 ? 8 : 4];
 };
 
-template <int ST, int MT>
-__device__ __forceinline__ void load_bias_in(BiasIn<ST, MT> &bi, const float *const (&xrow)[MT],
-                                             const uint8_t *const (&sbase)[2], const uint8_t *const (&bbase)[2],
-                                             const int64_t (&srow)[2], int NG, int kg) {
+template <int ST>
+__device__ __forceinline__ void load_bias_bs(BiasBS<ST> &bi, const uint8_t *const (&sbase)[2],
+                                             const uint8_t *const (&bbase)[2], const int64_t (&srow)[2], int NG,
+                                             int kg) {
     constexpr int W = ST == SWQ_F32 ? 8 : 4;
     constexpr int EB = ST == SWQ_F32 ? 4 : 2;
 #pragma unroll
@@ -295,19 +295,13 @@ __device__ __forceinline__ void load_bias_in(BiasIn<ST, MT> &bi, const float *co
             bi.b[j][i] = *reinterpret_cast<const uint32_t *>(bbase[j] + (srow[j] + gi) * EB);
             bi.s[j][i] = *reinterpret_cast<const uint32_t *>(sbase[j] + (srow[j] + gi) * EB);
         }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const float4 x0 = *reinterpret_cast<const float4 *>(xrow[mt] + 8 * kg);
-        const float4 x1 = *reinterpret_cast<const float4 *>(xrow[mt] + 8 * kg + 4);
-        bi.x[mt][0] = x0.x; bi.x[mt][1] = x0.y; bi.x[mt][2] = x0.z; bi.x[mt][3] = x0.w;
-        bi.x[mt][4] = x1.x; bi.x[mt][5] = x1.y; bi.x[mt][6] = x1.z; bi.x[mt][7] = x1.w;
-    }
 }
 
-// bias_term on preloaded inputs (NG <= 32).
+// bias_term from preloaded biases/scales and the lane's group sums xv[mt]
+// (NG <= 32).
 template <int BITS, int ST, int MT>
-__device__ __forceinline__ void bias_term_pre(f32x4_t (&acc)[MT][2], const BiasIn<ST, MT> &bi, int NG, int rows,
-                                              int kg) {
+__device__ __forceinline__ void bias_term_bs(f32x4_t (&acc)[MT][2], const BiasBS<ST> &bi, const float (&xv)[MT][8],
+                                             int NG, int rows, int kg) {
     u32x4_t bh[2], bl[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -331,11 +325,11 @@ __device__ __forceinline__ void bias_term_pre(f32x4_t (&acc)[MT][2], const BiasI
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
         if (16 * mt >= rows) break;
-        float xv[8];
+        float x[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xv[i] = 8 * kg + i < NG ? bi.x[mt][i] : 0.f;
+        for (int i = 0; i < 8; ++i) x[i] = 8 * kg + i < NG ? xv[mt][i] : 0.f;
         u32x4_t xh, xm, xl;
-        split8x3(xv, xh, xm, xl);
+        split8x3(x, xh, xm, xl);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             acc[mt][j] = mfma(xl, bh[j], acc[mt][j]);
@@ -357,7 +351,7 @@ __device__ __forceinline__ int nibble_pos(int c) {
 // f32 rows; kEpiSwiGLU stores h = silu(g) * u as bf16 hi + lo planes and the
 // group sum of h over the workgroup's 64 columns (one group of the down
 // projection's input).  Every thread of the workgroup calls it.
-template <int EPI, int MT>
+template <int EPI, int MT, int WAVES = 4>
 __device__ __forceinline__ void epilogue(const f32x4_t (&acc)[MT][2], const GemmArgs &a, const int (&col)[2], int N,
                                          bool active, int row0, int rows, int nb, float *s_red) {
     constexpr int ROWS = 16 * MT;
@@ -385,9 +379,13 @@ __device__ __forceinline__ void epilogue(const f32x4_t (&acc)[MT][2], const Gemm
             }
         }
         __syncthreads();
-        if (tid < rows) {
-            const float t = (s_red[tid] + s_red[ROWS + tid]) + (s_red[2 * ROWS + tid] + s_red[3 * ROWS + tid]);
-            a.xs_out[static_cast<int64_t>(row0 + tid) * a.xs_ld_out + nb] = t;
+        // waves 4 q .. 4 q + 3 cover group (nb * col_block / 64 + q) of h (16 columns each)
+        constexpr int NQ = WAVES / 4;
+        for (int i = tid; i < rows * NQ; i += 64 * WAVES) {
+            const int gq = i / rows, r = i - gq * rows;
+            const float *sr = s_red + 4 * gq * ROWS + r;
+            const float t = (sr[0] + sr[ROWS]) + (sr[2 * ROWS] + sr[3 * ROWS]);
+            a.xs_out[static_cast<int64_t>(row0 + r) * a.xs_ld_out + nb * (a.col_block / 64) + gq] = t;
         }
     } else if (active) {
 #pragma unroll
@@ -693,15 +691,22 @@ __device__ __forceinline__ void ring_wait() {
 // D - 1 groups after its loads were issued.  Activation rows are 128 B; row r
 // keeps its 16 B chunk c in slot c ^ (r & 7) so the matrix-core reads of 16
 // rows at one chunk hit distinct banks.
-template <int BITS, int ST, int NPL, int EPI, int D>
-__global__ __launch_bounds__(kPfThreads) void pf_gemm_dma(const GemmArgs a) {
+template <int BITS, int ST, int NPL, int EPI, int DA, int DB, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4))) void pf_gemm_dma(const GemmArgs a) {
+    // B(g) must be issued before A(g) for the wait on A(g) to cover it
+    static_assert(DA >= 2 && DB > DA, "ring depths");
+    static_assert(WAVES == 4 || WAVES == 8, "waves per workgroup");
     constexpr int MT = 4, ROWS = 64;
-    constexpr int A_BYTES = NPL * ROWS * 128;
+    constexpr int AW = 8 / WAVES;                    // 8-row slabs each wave brings in per plane
+    constexpr int A_SLOT = NPL * ROWS * 128;         // activation rows of one group
     constexpr int B_WAVE = BITS == 4 ? 1024 : 2048;  // code bytes per wave per group
-    constexpr int SLOT = A_BYTES + 4 * B_WAVE + 4 * 256;
-    constexpr int LS = 2 * NPL + B_WAVE / 1024 + 1;  // DMA instructions per wave per group
-    __shared__ __attribute__((aligned(16))) uint8_t s_ring[D * SLOT];
-    __shared__ float s_red[EPI == kEpiSwiGLU ? 4 * ROWS : 1];
+    constexpr int B_SLOT = WAVES * (B_WAVE + 256);   // codes + scale pairs of one group
+    // DMA instructions per wave per group: activations, codes, scales
+    constexpr int LA = AW * NPL, LB = B_WAVE / 1024, LSC = 1, L = LA + LB + LSC;
+    __shared__ __attribute__((aligned(16))) uint8_t s_ring_a[DA * A_SLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t s_ring_b[DB * B_SLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t s_xs[ROWS * 128];  // group sums of the rows
+    __shared__ float s_red[EPI == kEpiSwiGLU ? WAVES * ROWS : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -744,18 +749,22 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_dma(const GemmArgs a) {
         gpr = m.gpr;
     }
 
-    // ---- DMA sources: activation rows 16 wave + 8 i + lane / 8 (rows past
-    // the tile read row 0), code rows and scale pairs of this wave's columns
-    const uint8_t *asrc[NPL][2];
+    // ---- DMA sources: activation rows 8 (AW wave + i) + lane / 8 (rows
+    // past the tile read row 0) and their group sums (128 B rows, chunks
+    // swizzled like the activations), code rows and scale pairs of this
+    // wave's columns
+    const uint8_t *asrc[NPL][AW];
+    const uint8_t *xsrc[AW];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int r = 16 * wave + 8 * i + (lane >> 3);
+    for (int i = 0; i < AW; ++i) {
+        const int r = 8 * (AW * wave + i) + (lane >> 3);
         const int c = (lane & 7) ^ (r & 7);
         const int rr = r < rows ? r : 0;
         const int64_t sr = min(max(a.row_src ? a.row_src[row0 + rr] : row0 + rr, 0), a.a_rows - 1);
         const int64_t e = sr * a.a_ld + 8 * c;
         asrc[0][i] = static_cast<const uint8_t *>(a.a0) + 2 * e;
         if constexpr (NPL == 2) asrc[1][i] = static_cast<const uint8_t *>(a.a1) + 2 * e;
+        xsrc[i] = reinterpret_cast<const uint8_t *>(a.xs_in + sr * a.xs_ld) + 16 * c;
     }
     const uint8_t *bsrc[BITS == 4 ? 1 : 2];
     if constexpr (BITS == 4) {
@@ -773,23 +782,30 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_dma(const GemmArgs a) {
         const int j = lane >> 5, r = min(wcol + j * a.col_op + (lane & 15), N - 1);
         ssrc = (j ? sbase[1] : sbase[0]) + static_cast<int64_t>(r) * gpr * (ST == SWQ_F32 ? 4 : 2);
     }
-    const uint32_t ring0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_ring));
+    const uint32_t ring_a = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_ring_a));
+    const uint32_t ring_b = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_ring_b));
 
-    auto issue = [&](int slot, int g) {
-        const uint32_t base = ring0 + slot * SLOT;
+    // group g's activation rows into A slot sa (LA instructions per wave)
+    auto issue_a = [&](int sa, int g) {
+        const uint32_t base = ring_a + sa * A_SLOT;
 #pragma unroll
         for (int p = 0; p < NPL; ++p)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) dma16(asrc[p][i] + kGroupK * 2 * g, base + p * ROWS * 128 + (16 * wave + 8 * i) * 128);
+            for (int i = 0; i < AW; ++i)
+                dma16(asrc[p][i] + kGroupK * 2 * g, base + p * ROWS * 128 + 8 * (AW * wave + i) * 128);
+    };
+    // group g's code rows and scale pairs into B slot sb (LB + LSC instructions per wave)
+    auto issue_b = [&](int sb, int g) {
+        const uint32_t base = ring_b + sb * B_SLOT;
         if constexpr (BITS == 4) {
-            dma16(bsrc[0] + 32 * g, base + A_BYTES + wave * B_WAVE);
+            dma16(bsrc[0] + 32 * g, base + wave * B_WAVE);
         } else {
-            dma16(bsrc[0] + 64 * g, base + A_BYTES + wave * B_WAVE);
-            dma16(bsrc[1] + 64 * g, base + A_BYTES + wave * B_WAVE + 1024);
+            dma16(bsrc[0] + 64 * g, base + wave * B_WAVE);
+            dma16(bsrc[1] + 64 * g, base + wave * B_WAVE + 1024);
         }
         // 2-byte scales: the aligned pair holding group g (rows hold an even
         // number of groups); f32: the scale itself
-        dma4(ssrc + (ST == SWQ_F32 ? 4 * g : 4 * (g >> 1)), base + A_BYTES + 4 * B_WAVE + wave * 256);
+        dma4(ssrc + (ST == SWQ_F32 ? 4 * g : 4 * (g >> 1)), base + WAVES * B_WAVE + wave * 256);
     };
 
     f32x4_t acc[MT][2];
@@ -798,22 +814,23 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_dma(const GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](int slot, int g) {
-        const uint8_t *sl = s_ring + slot * SLOT;
+    auto compute = [&](int sa, int sb, int g) {
+        const uint8_t *sl = s_ring_a + sa * A_SLOT;
+        const uint8_t *bl = s_ring_b + sb * B_SLOT;
         u32x4_t bq[2][2];
         float sc[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             if constexpr (BITS == 4) {
-                const uint2 w = *reinterpret_cast<const uint2 *>(sl + A_BYTES + wave * B_WAVE + (j * 32 + n * 2) * 16 + 8 * kg);
+                const uint2 w = *reinterpret_cast<const uint2 *>(bl + wave * B_WAVE + (j * 32 + n * 2) * 16 + 8 * kg);
                 bq[j][0] = codes_q4(w.x);
                 bq[j][1] = codes_q4(w.y);
             } else {
-                const uint4 w = *reinterpret_cast<const uint4 *>(sl + A_BYTES + wave * B_WAVE + (j * 64 + n * 4 + kg) * 16);
+                const uint4 w = *reinterpret_cast<const uint4 *>(bl + wave * B_WAVE + (j * 64 + n * 4 + kg) * 16);
                 bq[j][0] = codes_q8(w.x, w.y);
                 bq[j][1] = codes_q8(w.z, w.w);
             }
-            const uint32_t raw = *reinterpret_cast<const uint32_t *>(sl + A_BYTES + 4 * B_WAVE + wave * 256 + (j * 32 + n) * 4);
+            const uint32_t raw = *reinterpret_cast<const uint32_t *>(bl + WAVES * B_WAVE + wave * 256 + (j * 32 + n) * 4);
             if constexpr (ST == SWQ_F32) sc[j] = __uint_as_float(raw);
             else sc[j] = scale_of<ST>((g & 1) ? raw >> 16 : raw & 0xFFFFu);
         }
@@ -844,41 +861,65 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm_dma(const GemmArgs a) {
         }
     };
 
-    // ---- the bias term's inputs, issued before the ring so that they are
-    // older than every DMA (ring_wait's counts stay exact) and arrive during
+    // ---- the bias term's inputs (biases and scales in registers, group
+    // sums by DMA into LDS), issued before the ring so that they are older
+    // than every ring load (ring_wait's counts stay exact) and arrive during
     // the loop
-    BiasIn<ST, MT> bi;
+    BiasBS<ST> bi;
+    load_bias_bs<ST>(bi, sbase, bbase, srow, NG, kg);
     {
-        const float *xrow[MT];
+        const uint32_t xb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_xs));
+#pragma unroll
+        for (int i = 0; i < AW; ++i) dma16(xsrc[i], xb + 8 * (AW * wave + i) * 128);
+    }
+
+    // ---- the rings: codes and scales DB-1 groups ahead, activation rows
+    // (mostly L2 hits) DA-1 groups ahead.  Before the loop: B groups 0..DB-2,
+    // then A groups 0..DA-2.  At group g: wait until A(g) has landed (B(g)
+    // is older), then refill the slots group g-1 used with A(g+DA-1) and
+    // B(g+DB-1) (past NG: group NG-1 again, never read), then compute g.
+    // Loads return in order, so "at most N of this wave's loads in flight"
+    // with N = the loads issued after A(g) means A(g) and everything before
+    // it have landed; N is the same for every group from DA-1 on, and the
+    // first DA-1 groups are peeled with their own counts.
+#pragma unroll
+    for (int s = 0; s < DB - 1; ++s) issue_b(s, min(s, NG - 1));
+#pragma unroll
+    for (int s = 0; s < DA - 1; ++s) issue_a(s, min(s, NG - 1));
+    auto step = [&](int g, int sa, int sb) {
+        issue_a(sa == 0 ? DA - 1 : sa - 1, min(g + DA - 1, NG - 1));
+        issue_b(sb == 0 ? DB - 1 : sb - 1, min(g + DB - 1, NG - 1));
+        compute(sa, sb, g);
+    };
+    static_assert(DA <= 4, "peeled prologue");
+    if (0 < NG) { ring_wait<(DA - 2) * LA>(); step(0, 0, 0); }
+    if constexpr (DA >= 3) if (1 < NG) { ring_wait<(DA - 3) * LA + 1 * L>(); step(1, 1, 1); }
+    if constexpr (DA >= 4) if (2 < NG) { ring_wait<(DA - 4) * LA + 2 * L>(); step(2, 2, 2); }
+    {
+        int sa = (DA - 1) % DA, sb = (DA - 1) % DB;
+#pragma unroll 1
+        for (int g = DA - 1; g < NG; ++g) {
+            ring_wait<LB + LSC + (DA - 2) * L>();
+            step(g, sa, sb);
+            sa = sa + 1 == DA ? 0 : sa + 1;
+            sb = sb + 1 == DB ? 0 : sb + 1;
+        }
+    }
+
+    if (active) {
+        float xv[MT][8];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            const int rr = min(16 * mt + n, rows - 1);
-            const int64_t xr = a.row_src ? a.row_src[row0 + rr] : row0 + rr;
-            xrow[mt] = a.xs_in + xr * a.xs_ld;
+            const int m = 16 * mt + n;
+            const uint8_t *xr = s_xs + m * 128;
+            const float4 x0 = *reinterpret_cast<const float4 *>(xr + 16 * ((2 * kg) ^ (m & 7)));
+            const float4 x1 = *reinterpret_cast<const float4 *>(xr + 16 * ((2 * kg + 1) ^ (m & 7)));
+            xv[mt][0] = x0.x; xv[mt][1] = x0.y; xv[mt][2] = x0.z; xv[mt][3] = x0.w;
+            xv[mt][4] = x1.x; xv[mt][5] = x1.y; xv[mt][6] = x1.z; xv[mt][7] = x1.w;
         }
-        load_bias_in<ST, MT>(bi, xrow, sbase, bbase, srow, NG, kg);
+        bias_term_bs<BITS, ST, MT>(acc, bi, xv, NG, rows, kg);
     }
-
-    // ---- the ring: groups 0 .. D-2 in flight before the loop; at group g
-    // wait for it, then refill the slot group g-1 used with group g+D-1
-    // (past NG: group NG-1 again, never read)
-#pragma unroll
-    for (int s = 0; s < D - 1; ++s) issue(s, min(s, NG - 1));
-#pragma unroll 1
-    for (int g0 = 0; g0 < NG; g0 += D) {
-#pragma unroll
-        for (int u = 0; u < D; ++u) {
-            const int g = g0 + u;
-            if (g < NG) {
-                ring_wait<LS * (D - 2)>();
-                issue((u + D - 1) % D, min(g + D - 1, NG - 1));
-                compute(u, g);
-            }
-        }
-    }
-
-    if (active) bias_term_pre<BITS, ST, MT>(acc, bi, NG, rows, kg);
-    epilogue<EPI, MT>(acc, a, col, N, active, row0, rows, nb, s_red);
+    epilogue<EPI, MT, WAVES>(acc, a, col, N, active, row0, rows, nb, s_red);
 }
 
 // ---------------------------------------------------------------------------
@@ -1267,16 +1308,24 @@ int launch_gemm(const swq_qlinear &lin, const GemmArgs &a, int blocks, hipStream
     return launch_status();
 }
 
-// LDS ring depth: four groups for one activation plane, three for two.
+// Waves per workgroup and ring depths of the DMA GEMMs, chosen so that two
+// workgroups fit in a CU's 160 KB of LDS: 8 waves (128 gate/up or 256 down
+// columns per workgroup: the tile's activation rows are shared by twice the
+// columns) except for 8-bit codes with two activation planes.
+int dma_waves(int bits, int npl) { return bits == 8 && npl == 2 ? 4 : 8; }
+
 template <int BITS, int NPL, int EPI>
 void launch_dma_st(int stype, const GemmArgs &a, int blocks, hipStream_t s) {
-    constexpr int D = NPL == 1 ? 4 : 3;
+    constexpr int W = BITS == 8 && NPL == 2 ? 4 : 8;
+    constexpr int DA = BITS == 4 && NPL == 1 ? 3 : 2;
+    constexpr int DB = DA + 1;
+    const dim3 th(64 * W);
     if (stype == SWQ_F16)
-        hipLaunchKernelGGL((pf_gemm_dma<BITS, SWQ_F16, NPL, EPI, D>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_dma<BITS, SWQ_F16, NPL, EPI, DA, DB, W>), dim3(blocks), th, 0, s, a);
     else if (stype == SWQ_BF16)
-        hipLaunchKernelGGL((pf_gemm_dma<BITS, SWQ_BF16, NPL, EPI, D>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_dma<BITS, SWQ_BF16, NPL, EPI, DA, DB, W>), dim3(blocks), th, 0, s, a);
     else
-        hipLaunchKernelGGL((pf_gemm_dma<BITS, SWQ_F32, NPL, EPI, D>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_dma<BITS, SWQ_F32, NPL, EPI, DA, DB, W>), dim3(blocks), th, 0, s, a);
 }
 
 template <int NPL, int EPI>
@@ -1427,10 +1476,10 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         g.N = I;
         g.Nsh = Is;
         g.E = E;
-        g.col_block = 64;
         g.col_wave = 16;
+        g.col_block = 16 * dma_waves(layer->gate.bits, bf16x ? 1 : 2);
         g.col_op = 0;
-        g.nblk = (wl.Ih + 63) / 64;
+        g.nblk = (wl.Ih + g.col_block - 1) / g.col_block;
         g.max_tiles = wl.max_tiles;
         const int blocks = gemm_blocks(wl.max_tiles, g.nblk);
         st = bf16x ? launch_dma<1, kEpiSwiGLU>(layer->gate, g, blocks, s)
@@ -1457,10 +1506,10 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         g.Ksh = Is;
         g.N = g.Nsh = H;
         g.E = E;
-        g.col_block = 128;
         g.col_wave = 32;
+        g.col_block = 32 * dma_waves(layer->down.bits, 2);
         g.col_op = 16;
-        g.nblk = (H + 127) / 128;
+        g.nblk = (H + g.col_block - 1) / g.col_block;
         g.max_tiles = wl.max_tiles;
         const int blocks = gemm_blocks(wl.max_tiles, g.nblk);
         if ((st = launch_dma<2, kEpiRows>(layer->down, g, blocks, s)) != SWQ_OK) return st;
