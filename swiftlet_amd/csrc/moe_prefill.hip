@@ -749,15 +749,19 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
         gpr = m.gpr;
     }
 
-    // ---- DMA sources: activation rows 8 (AW wave + i) + lane / 8 (rows
-    // past the tile read row 0) and their group sums (128 B rows, chunks
-    // swizzled like the activations), code rows and scale pairs of this
-    // wave's columns
+    // ---- DMA sources: activation rows 8 (AW wave + i) + lane / 8 and their
+    // group sums (128 B rows, chunks swizzled like the activations), code
+    // rows and scale pairs of this wave's columns
     const uint8_t *asrc[NPL][AW];
     const uint8_t *xsrc[AW];
+    // rows past the tile are not fetched (their LDS rows hold stale values,
+    // which stay in those rows of the matrix-core results, never stored);
+    // lane 0 always fetches so that no copy is empty
+    bool afetch[AW];
 #pragma unroll
     for (int i = 0; i < AW; ++i) {
         const int r = 8 * (AW * wave + i) + (lane >> 3);
+        afetch[i] = r < rows || lane == 0;
         const int c = (lane & 7) ^ (r & 7);
         const int rr = r < rows ? r : 0;
         const int64_t sr = min(max(a.row_src ? a.row_src[row0 + rr] : row0 + rr, 0), a.a_rows - 1);
@@ -792,7 +796,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
         for (int p = 0; p < NPL; ++p)
 #pragma unroll
             for (int i = 0; i < AW; ++i)
-                dma16(asrc[p][i] + kGroupK * 2 * g, base + p * ROWS * 128 + 8 * (AW * wave + i) * 128);
+            {
+                // the LDS address in a scalar register before the branch
+                const uint32_t d = __builtin_amdgcn_readfirstlane(base + p * ROWS * 128 + 8 * (AW * wave + i) * 128);
+                if (afetch[i]) dma16(asrc[p][i] + kGroupK * 2 * g, d);
+            }
     };
     // group g's code rows and scale pairs into B slot sb (LB + LSC instructions per wave)
     auto issue_b = [&](int sb, int g) {
@@ -870,7 +878,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
     {
         const uint32_t xb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_xs));
 #pragma unroll
-        for (int i = 0; i < AW; ++i) dma16(xsrc[i], xb + 8 * (AW * wave + i) * 128);
+        for (int i = 0; i < AW; ++i) {
+            const uint32_t d = __builtin_amdgcn_readfirstlane(xb + 8 * (AW * wave + i) * 128);
+            if (afetch[i]) dma16(xsrc[i], d);
+        }
     }
 
     // ---- the rings: codes and scales DB-1 groups ahead, activation rows
@@ -1015,12 +1026,14 @@ __device__ float row_dot(const QMat &m, const void *x, int64_t x0, int lane) {
 }
 
 // The last workgroup: per-expert pair counts (LDS atomics over the ids),
-// exclusive scans of the pair counts and of the tile counts, the tile table,
-// and the sorted pair order (a second pass hands out the slots; the order of
-// pairs within an expert does not matter, every row is computed on its own).
+// exclusive scans of the pair counts and of the tile counts, the tile table
+// (by decreasing row count), and the sorted pair order (a second pass hands
+// out the slots; the order of pairs within an expert does not matter, every
+// row is computed on its own).
 __device__ void group_pairs(const RouteArgs &a) {
     __shared__ int32_t s_cnt[kMaxExperts];  // counts, then the next free slot
     __shared__ int32_t s_part[2][kPfThreads];
+    __shared__ int32_t s_rows[kTileRows + 1];  // tiles of each row count, then their next slot
     const int tid = threadIdx.x;
     const int P = a.T * a.K;
     constexpr int kBatch = 8;  // ids per thread per pass, all in flight at once
@@ -1058,22 +1071,51 @@ __device__ void group_pairs(const RouteArgs &a) {
         s_part[1][tid] += t;
         __syncthreads();
     }
-    int c0 = s_part[0][tid] - csum, t0 = s_part[1][tid] - tsum;
+    int c0 = s_part[0][tid] - csum;
     const int routed_tiles = s_part[1][kPfThreads - 1];
+    const int sh_tiles = a.has_shared ? (a.T + kTileRows - 1) / kTileRows : 0;
+    // The tile table in decreasing row count (the GEMMs start the heaviest
+    // tiles first, so the light ones fill in at the end): tiles per row
+    // count, their first slots, then each tile into the next slot of its count.
+    for (int r = tid; r <= kTileRows; r += kPfThreads) s_rows[r] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        if (tid * EPT + i < a.E && cnt[i] > 0) {
+            if (cnt[i] >= kTileRows) atomicAdd(&s_rows[kTileRows], cnt[i] / kTileRows);
+            if (cnt[i] % kTileRows) atomicAdd(&s_rows[cnt[i] % kTileRows], 1);
+        }
+    }
+    if (tid == 0 && sh_tiles > 0) {
+        if (a.T >= kTileRows) atomicAdd(&s_rows[kTileRows], a.T / kTileRows);
+        if (a.T % kTileRows) atomicAdd(&s_rows[a.T % kTileRows], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int next = 0;
+        for (int r = kTileRows; r >= 1; --r) {
+            const int n = s_rows[r];
+            s_rows[r] = next;
+            next += n;
+        }
+    }
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
         const int e = tid * EPT + i;
         if (e < a.E) {
             s_cnt[e] = c0;  // each thread rewrites only its own experts
-            for (int q = 0; q < tl[i]; ++q)
-                a.tiles[t0 + q] = Tile{e, c0 + q * kTileRows, min(kTileRows, cnt[i] - q * kTileRows), 0};
+            for (int q = 0; q < tl[i]; ++q) {
+                const int rows = min(kTileRows, cnt[i] - q * kTileRows);
+                a.tiles[atomicAdd(&s_rows[rows], 1)] = Tile{e, c0 + q * kTileRows, rows, 0};
+            }
         }
         c0 += cnt[i];
-        t0 += tl[i];
     }
-    const int sh_tiles = a.has_shared ? (a.T + kTileRows - 1) / kTileRows : 0;
-    for (int q = tid; q < sh_tiles; q += kPfThreads)
-        a.tiles[routed_tiles + q] = Tile{a.E, P + q * kTileRows, min(kTileRows, a.T - q * kTileRows), 0};
+    for (int q = tid; q < sh_tiles; q += kPfThreads) {
+        const int rows = min(kTileRows, a.T - q * kTileRows);
+        a.tiles[atomicAdd(&s_rows[rows], 1)] = Tile{a.E, P + q * kTileRows, rows, 0};
+    }
     if (tid == 0) {
         *a.n_tiles = routed_tiles + sh_tiles;
         *a.done = 0u;
