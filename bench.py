@@ -47,8 +47,8 @@ MEASURED_TRAFFIC = {
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_692_148,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 14_590_849,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 5_743_112,
-    ("qwen3.6-35b-a3b-q4-prefill512", "gate_up"): 353_769_995,
-    ("qwen3.6-35b-a3b-q4-prefill512", "down"): 210_206_539,
+    ("qwen3.6-35b-a3b-q4-prefill512", "gate_up"): 402_625_363,
+    ("qwen3.6-35b-a3b-q4-prefill512", "down"): 209_861_891,
 }
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
