@@ -151,6 +151,21 @@ int swq_encode_silu_mul(float *buf, int count, int64_t g_off, int64_t u_off,
 int swq_dequantize(const swq_qlinear *lin, int64_t row0, int64_t rows,
                    float *out, void *stream);
 
+/* ---- layer tail --------------------------------------------------------- */
+
+/* For each of `rows` rows of `dim` floats: h += residual (when residual is
+ * not NULL; h is updated in place), then
+ *     out = h * (scale * weight),  scale = 1 / sqrt(mean(h^2) + eps)
+ * (weight NULL: h * scale).  weight: [dim] of weight_dtype (SWQ_F32 / SWQ_F16
+ * / SWQ_BF16); out: [rows, dim] of out_dtype (SWQ_F32 / SWQ_BF16; bf16 is
+ * rounded to nearest even).  This is the MoE input of a decoder layer; the MoE
+ * step's own residual add is SWQ_MOE_ACCUMULATE into h.
+ * Replaces add_inplace + norm_copy (Kernels.metal.txt:425-452) as
+ * QwenMetalModel.swift:938-951 encodes them around the MoE block, with the
+ * numerics of QwenCPUModel.rmsNorm (QwenCPUModel.swift:47-59, :276-277). */
+int swq_rmsnorm(float *h, const float *residual, const void *weight, int weight_dtype, float eps,
+                int rows, int dim, void *out, int out_dtype, void *stream);
+
 /* ---- MoE layer decode ------------------------------------------------- */
 
 /* Workspace bytes swq_moe_decode needs for `batch` tokens (0 on bad input). */

@@ -77,6 +77,7 @@ SIGNATURES = {
     "swq_encode_gemv": (_I, [_c.POINTER(QLinear), _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
     "swq_encode_silu_mul": (_I, [_P, _I, _I64, _I64, _I64, _P]),
     "swq_dequantize": (_I, [_c.POINTER(QLinear), _I64, _I64, _P, _P]),
+    "swq_rmsnorm": (_I, [_P, _P, _P, _I, _c.c_float, _I, _I, _P, _I, _P]),
     "swq_moe_decode_workspace_bytes": (_SZ, [_c.POINTER(MoELayer), _I]),
     "swq_moe_workspace_init": (_I, [_P, _SZ, _P]),
     "swq_moe_decode": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _I, _P]),

@@ -136,6 +136,30 @@ class HipEngine:
         check(self.lib.swq_encode_silu_mul(buf.data_ptr(), count, g_off, u_off, dst_off,
                                            _stream_handle(stream)), "encode_silu_mul")
 
+    # add_inplace + norm_copy (Kernels.metal.txt:425-452) around the MoE block
+    # (QwenMetalModel.swift:938-951), numerics of QwenCPUModel.rmsNorm (:47-59).
+    def rms_norm(self, h, weight, eps: float, residual=None, out=None, out_dtype=None, stream=None):
+        """h [rows, dim] f32 device tensor: h += residual (in place, when
+        given), then returns rmsnorm(h) * weight as out_dtype (f32 / bf16)."""
+        torch = _torch()
+        assert h.dtype == torch.float32 and h.is_contiguous()
+        if h.dim() == 1:
+            h = h.unsqueeze(0)
+        rows, dim = h.shape
+        if out is None:
+            out = torch.empty((rows, dim), dtype=out_dtype or torch.float32, device=h.device)
+        odt = {torch.float32: SWQ_F32, torch.bfloat16: SWQ_BF16}[out.dtype]
+        wdt, wptr = SWQ_F32, None
+        if weight is not None:
+            wdt = {torch.float32: SWQ_F32, torch.float16: SWQ_F16, torch.bfloat16: SWQ_BF16}[weight.dtype]
+            assert weight.numel() == dim
+            wptr = weight.data_ptr()
+        if residual is not None:
+            assert residual.dtype == torch.float32 and residual.numel() == h.numel()
+        check(self.lib.swq_rmsnorm(h.data_ptr(), residual.data_ptr() if residual is not None else None, wptr,
+                                   wdt, eps, rows, dim, out.data_ptr(), odt, _stream_handle(stream)), "rmsnorm")
+        return out
+
     # Checkpoint.moduleWeightSlice (Checkpoint.swift:148-155): rows of the
     # flattened [experts*out, in] weight as fp32.
     def dequantize(self, lin: GPULinear, row0: int, rows: int, stream=None):

@@ -1,6 +1,6 @@
 """The C ABI without a GPU: libswq.so loads, exports every symbol the headers
 declare, and its host-side validation returns the documented status codes
-before touching a device (SURVEY-listed failure modes: in % group, bits
+before touching a device (the boundary's failure modes: in % group, bits
 outside {2,4,8}, top_k > E, misaligned pointers, short workspace)."""
 
 import ctypes
@@ -119,6 +119,17 @@ def test_gemv_validation(lib):
     assert lib.swq_encode_gemv(ctypes.byref(ok), 0, 0, 0, 0, 0, 0, FAKE, 0, None) == _lib.SWQ_ERR_INVALID_ARGUMENT
     assert lib.swq_dequantize(ctypes.byref(ok), 10, 10, FAKE, None) == _lib.SWQ_ERR_BAD_SHAPE  # past out_dim
     assert lib.swq_encode_silu_mul(FAKE, 0, 0, 0, 0, None) == _lib.SWQ_ERR_INVALID_ARGUMENT
+
+
+def test_rmsnorm_validation(lib):
+    F = _lib.SWQ_F32
+    assert lib.swq_rmsnorm(0, None, None, F, 1e-6, 1, 64, FAKE, F, None) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert lib.swq_rmsnorm(FAKE, None, None, F, 1e-6, 0, 64, FAKE, F, None) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert lib.swq_rmsnorm(FAKE, None, None, F, -1.0, 1, 64, FAKE, F, None) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert lib.swq_rmsnorm(FAKE, None, FAKE, 7, 1e-6, 1, 64, FAKE, F, None) == _lib.SWQ_ERR_UNSUPPORTED_DTYPE
+    assert lib.swq_rmsnorm(FAKE, None, None, F, 1e-6, 1, 64, FAKE, _lib.SWQ_F16, None) == _lib.SWQ_ERR_UNSUPPORTED_DTYPE
+    assert lib.swq_rmsnorm(FAKE + 2, None, None, F, 1e-6, 1, 64, FAKE, F, None) == _lib.SWQ_ERR_MISALIGNED
+    assert lib.swq_rmsnorm(FAKE, None, FAKE + 1, _lib.SWQ_BF16, 1e-6, 1, 64, FAKE, F, None) == _lib.SWQ_ERR_MISALIGNED
 
 
 def test_no_device_reported(lib):
