@@ -226,6 +226,39 @@ def main():
     t_eager1.record()
     torch.cuda.synchronize()
     eager_us_per_step = t_eager0.elapsed_time(t_eager1) * 1000.0 / n_st
+    # ---- the layer tail: attention residual add + post-attention RMSNorm
+    # (swq_rmsnorm), then the MoE step adding into the f32 residual stream,
+    # as a graph over the same resident layers
+    hs = torch.randn((R, batch, shape.hidden), dtype=torch.float32, device=dev)
+    rs = torch.randn((R, batch, shape.hidden), dtype=torch.float32, device=dev)
+    wnorm = (1.0 + 0.1 * torch.randn(shape.hidden, device=dev)).to(torch.bfloat16)
+    xn = torch.empty((R, batch, shape.hidden), dtype=torch.bfloat16, device=dev)
+    tail_calls = []
+    for r, l in enumerate(layers):
+        tail_calls.append((
+            (ctypes.c_void_p(hs[r].data_ptr()), ctypes.c_void_p(rs[r].data_ptr()), ctypes.c_void_p(wnorm.data_ptr()),
+             _lib.SWQ_BF16, ctypes.c_float(1e-6), batch, shape.hidden, ctypes.c_void_p(xn[r].data_ptr()), _lib.SWQ_BF16),
+            (ctypes.byref(l._c), ctypes.c_void_p(xn[r].data_ptr()), _lib.SWQ_BF16, batch,
+             ctypes.c_void_p(hs[r].data_ptr()), _lib.SWQ_F32, ctypes.c_void_p(ids[r].data_ptr()),
+             ctypes.c_void_p(wts[r].data_ptr()), ctypes.c_void_p(wss[r].data_ptr()), wss[r].numel(),
+             _lib.SWQ_MOE_ACCUMULATE)))
+    gt = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gt):
+        cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for i in range(K):
+            nrm, dec = tail_calls[i % R]
+            check(lib.swq_rmsnorm(*nrm, cap), "rmsnorm (capture)")
+            check(lib.swq_moe_decode_stages(*dec, MASK, cap), "moe_decode (capture)")
+    gt.replay()
+    torch.cuda.synchronize()
+    b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    b0.record()
+    gt.replay()
+    b1.record()
+    torch.cuda.synchronize()
+    tail_us = b0.elapsed_time(b1) * 1000.0 / K
+    del gt
+
     # unique experts per step (batch > 1 reads each distinct expert once)
     ids_h = ids.cpu().numpy()
     uniq = [len(np.unique(ids_h[r])) for r in range(R)]
@@ -280,6 +313,7 @@ def main():
         "step_gbs_wall": round(step_bytes / (us_per_step * 1e-6) / 1e9, 1),
         "step_gbs_kernels": round(step_bytes / (sum(stage_us) * 1e-6) / 1e9, 1),
         "eager_us_per_step": round(eager_us_per_step, 3),
+        "layer_tail_us": round(tail_us, 3),
         "unique_experts_per_step": mean_uniq,
     }
 
