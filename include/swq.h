@@ -166,6 +166,37 @@ int swq_dequantize(const swq_qlinear *lin, int64_t row0, int64_t rows,
 int swq_rmsnorm(float *h, const float *residual, const void *weight, int weight_dtype, float eps,
                 int rows, int dim, void *out, int out_dtype, void *stream);
 
+/* ---- next-token sampling ------------------------------------------------ */
+
+/* GenerationOptions (SwiftletSession.swift:19-41). */
+typedef struct {
+    float temperature;        /* <= 0: greedy (the first maximum) */
+    int32_t top_k;            /* candidates when sampling, 1..64 */
+    float top_p;              /* nucleus cut; >= 1: none */
+    float presence_penalty;   /* >= 0, subtracted once from every seen token */
+    float frequency_penalty;  /* >= 0, times the token's count */
+} swq_sample_options;
+
+/* Workspace bytes of swq_sample for `vocab` logits (0: vocab above 524288).
+ * The workspace starts zeroed (swq_moe_workspace_init zeroes any workspace)
+ * and swq_sample leaves it zeroed again. */
+size_t swq_sample_workspace_bytes(int vocab);
+
+/* One next token from `vocab` f32 logits (device), entirely on the device:
+ * banned_ids (the suppressed ids, plus EOS while it is banned) become -inf,
+ * each seen_ids[i] loses presence + frequency * seen_counts[i]; then the
+ * first maximum (temperature <= 0), or the top_k candidates by logit (ties
+ * to the lower id), p_i = exp((l_i - l_0) / temperature), the top-p cut and
+ * the draw r = u * sum p, the first i with r - (p_0 + .. + p_i) <= 0.
+ * u in [0, 1) is the caller's uniform number (the reference draws
+ * Float.random).  out_token: one int32 on the device.  Id lists and counts
+ * are device arrays.  Replaces SwiftletSession.sample
+ * (SwiftletSession.swift:226-273). */
+int swq_sample(const float *logits, int vocab, const swq_sample_options *options,
+               const int32_t *seen_ids, const int32_t *seen_counts, int n_seen,
+               const int32_t *banned_ids, int n_banned, float u, int32_t *out_token,
+               void *ws, size_t ws_bytes, void *stream);
+
 /* ---- MoE layer decode ------------------------------------------------- */
 
 /* Workspace bytes swq_moe_decode needs for `batch` tokens (0 on bad input). */

@@ -49,6 +49,11 @@ class QLinear(ctypes.Structure):
     ]
 
 
+class SampleOptions(ctypes.Structure):
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int32), ("top_p", ctypes.c_float),
+                ("presence_penalty", ctypes.c_float), ("frequency_penalty", ctypes.c_float)]
+
+
 class MoELayer(ctypes.Structure):
     _fields_ = [
         ("router", QLinear), ("gate", QLinear), ("up", QLinear), ("down", QLinear),
@@ -78,6 +83,8 @@ SIGNATURES = {
     "swq_encode_silu_mul": (_I, [_P, _I, _I64, _I64, _I64, _P]),
     "swq_dequantize": (_I, [_c.POINTER(QLinear), _I64, _I64, _P, _P]),
     "swq_rmsnorm": (_I, [_P, _P, _P, _I, _c.c_float, _I, _I, _P, _I, _P]),
+    "swq_sample_workspace_bytes": (_SZ, [_I]),
+    "swq_sample": (_I, [_P, _I, _c.POINTER(SampleOptions), _P, _P, _I, _P, _I, _c.c_float, _P, _P, _SZ, _P]),
     "swq_moe_decode_workspace_bytes": (_SZ, [_c.POINTER(MoELayer), _I]),
     "swq_moe_workspace_init": (_I, [_P, _SZ, _P]),
     "swq_moe_decode": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _I, _P]),

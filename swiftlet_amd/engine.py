@@ -160,6 +160,35 @@ class HipEngine:
                                    wdt, eps, rows, dim, out.data_ptr(), odt, _stream_handle(stream)), "rmsnorm")
         return out
 
+    # SwiftletSession.sample (SwiftletSession.swift:226-273) on the device.
+    def new_sample_workspace(self, vocab: int, device="cuda"):
+        torch = _torch()
+        n = self.lib.swq_sample_workspace_bytes(vocab)
+        if n == 0:
+            raise SwqError(_lib.SWQ_ERR_LIMIT, "sample_workspace_bytes")
+        return torch.zeros(n, dtype=torch.uint8, device=device)
+
+    def sample(self, logits, temperature: float, top_k: int, top_p: float, presence: float = 0.0,
+               frequency: float = 0.0, seen: dict | None = None, banned=(), u: float = 0.0, ws=None,
+               stream=None) -> int:
+        """The next token from f32 device logits [vocab]; u in [0, 1) is the
+        draw's uniform number.  Blocking (reads the token back)."""
+        torch = _torch()
+        dev = logits.device
+        vocab = logits.numel()
+        if ws is None:
+            ws = self.new_sample_workspace(vocab, dev)
+        seen = seen or {}
+        ids = torch.tensor(list(seen.keys()) or [0], dtype=torch.int32, device=dev)
+        cnt = torch.tensor(list(seen.values()) or [0], dtype=torch.int32, device=dev)
+        ban = torch.tensor(list(banned) or [0], dtype=torch.int32, device=dev)
+        out = torch.empty(1, dtype=torch.int32, device=dev)
+        opt = _lib.SampleOptions(temperature, top_k, top_p, presence, frequency)
+        check(self.lib.swq_sample(logits.data_ptr(), vocab, ctypes.byref(opt), ids.data_ptr(), cnt.data_ptr(),
+                                  len(seen), ban.data_ptr(), len(banned), u, out.data_ptr(), ws.data_ptr(),
+                                  ws.numel(), _stream_handle(stream)), "sample")
+        return int(out.item())
+
     # Checkpoint.moduleWeightSlice (Checkpoint.swift:148-155): rows of the
     # flattened [experts*out, in] weight as fp32.
     def dequantize(self, lin: GPULinear, row0: int, rows: int, stream=None):
