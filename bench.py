@@ -75,6 +75,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=96)
     ap.add_argument("--config", default="qwen3.6-35b-a3b-q4-b1", choices=sorted(CONFIGS) + sorted(PREFILL_CONFIGS))
     ap.add_argument("--no-prefill", action="store_true", help="decode line without the prefill summary")
+    ap.add_argument("--no-lmhead", action="store_true", help="decode line without the lm_head + sampling summary")
     ap.add_argument("--prefill-steps", type=int, default=40, help="prefill chunks timed")
     ap.add_argument("--prefill-replicas", type=int, default=3, help="distinct layers the prefill chunks cycle")
     ap.add_argument("--replicas", type=int, default=48, help="distinct layers cycled through (MALL defeat)")
@@ -321,6 +322,10 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, shape, batch, layers[0], xs_bits[0])
 
+    # ---- the token tail: final norm, lm_head GEMV, sampling -----------------
+    if not args.no_lmhead and shape_key.startswith("qwen3.6-35b"):
+        result["lm_head"] = lmhead_measure(args, torch, lib, shape.hidden)
+
     # ---- the prefill chunk, summarised --------------------------------------
     if not args.no_prefill:
         del layers, wss, graph
@@ -331,6 +336,75 @@ def main():
         result["prefill"] = {k: line[k] for k in ("config", "value", "unit", "roofline", "kernel_us", "mfma")}
 
     print(json.dumps(result), flush=True)
+
+
+LMHEAD_VOCAB = 248320  # qwen3.6-35b vocab_size (model config)
+
+
+def lmhead_measure(args, torch, lib, hidden):
+    """Final RMSNorm (swq_rmsnorm), the q4 lm_head GEMV (swq_encode_gemv) and
+    Qwen's default sampling (swq_sample: T 0.7, top-k 20, top-p 0.8, presence
+    1.5, frequency 0.5, 64 seen tokens) per token, as a graph over two
+    resident lm_heads (2 x 286 MB, more than the 256 MB MALL)."""
+    from swiftlet_amd import _lib, moe
+    from swiftlet_amd._lib import check
+    dev = "cuda"
+    V, R, K = LMHEAD_VOCAB, 2, 64
+    heads = [moe.synth_linear(args.seed, 900 + r, "router", None, V, hidden, 4, 64, dev) for r in range(R)]
+    h = torch.randn((R, hidden), dtype=torch.float32, device=dev)
+    wn = (1.0 + 0.1 * torch.randn(hidden, device=dev)).to(torch.bfloat16)
+    x = torch.empty((R, hidden), dtype=torch.float32, device=dev)
+    logits = torch.empty((R, V), dtype=torch.float32, device=dev)
+    n_ws = lib.swq_sample_workspace_bytes(V)
+    wss = [torch.zeros(n_ws, dtype=torch.uint8, device=dev) for _ in range(R)]
+    seen = torch.arange(0, 64 * 997, 997, dtype=torch.int32, device=dev) % V
+    counts = torch.ones(64, dtype=torch.int32, device=dev)
+    banned = torch.tensor([V - 1], dtype=torch.int32, device=dev)
+    toks = torch.empty(R, dtype=torch.int32, device=dev)
+    opt = _lib.SampleOptions(0.7, 20, 0.8, 1.5, 0.5)
+    cs = [c.c() for c in heads]
+
+    def graph_of(parts):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for i in range(K):
+                r = i % R
+                if "norm" in parts:
+                    check(lib.swq_rmsnorm(h[r].data_ptr(), None, wn.data_ptr(), _lib.SWQ_BF16, ctypes.c_float(1e-6),
+                                          1, hidden, x[r].data_ptr(), _lib.SWQ_F32, cap), "rmsnorm")
+                if "gemv" in parts:
+                    check(lib.swq_encode_gemv(ctypes.byref(cs[r]), 0, 0, 0, 0, x[r].data_ptr(), 0,
+                                              logits[r].data_ptr(), 0, cap), "lm_head gemv")
+                if "sample" in parts:
+                    check(lib.swq_sample(logits[r].data_ptr(), V, ctypes.byref(opt), seen.data_ptr(),
+                                         counts.data_ptr(), 64, banned.data_ptr(), 1, ctypes.c_float(0.5),
+                                         toks[r:].data_ptr(), wss[r].data_ptr(), n_ws, cap), "sample")
+        return g
+
+    def timed(g):
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / K
+
+    us_step = timed(graph_of(("norm", "gemv", "sample")))
+    us_gemv = timed(graph_of(("gemv",)))
+    us_sample = timed(graph_of(("sample",)))
+    gemv_bytes = heads[0].matrix_bytes + hidden * 4 + V * 4
+    gbs = gemv_bytes / (us_gemv * 1e-6) / 1e9
+    del heads
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return {"vocab": V, "us_per_token": round(us_step, 3), "gemv_us": round(us_gemv, 3),
+            "sample_us": round(us_sample, 3), "gemv_bytes": int(gemv_bytes), "gemv_gbs": round(gbs, 1),
+            "gemv_frac": round(gbs / 8000.0, 4),
+            "note": "final norm + q4 lm_head GEMV + top-k/top-p sampling per token, graph of 64 tokens "
+                    "over 2 resident lm_heads; gemv_us from a graph of the GEMV alone"}
 
 
 def prefill_measure(args, torch, lib, name):

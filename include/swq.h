@@ -177,9 +177,7 @@ typedef struct {
     float frequency_penalty;  /* >= 0, times the token's count */
 } swq_sample_options;
 
-/* Workspace bytes of swq_sample for `vocab` logits (0: vocab above 524288).
- * The workspace starts zeroed (swq_moe_workspace_init zeroes any workspace)
- * and swq_sample leaves it zeroed again. */
+/* Workspace bytes of swq_sample for `vocab` logits (0: vocab above 524288). */
 size_t swq_sample_workspace_bytes(int vocab);
 
 /* One next token from `vocab` f32 logits (device), entirely on the device:
