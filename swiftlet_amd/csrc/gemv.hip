@@ -1,6 +1,7 @@
 // Quantized GEMV, SwiGLU and dequantisation entry points: the operator
 // layer of MetalEngine (MetalEngine.swift:95-232) and Checkpoint's MLX
 // affine dequantisation (Checkpoint.swift:168-209), on gfx950.
+#include <algorithm>
 #include <vector>
 
 #include "internal.hpp"
@@ -10,27 +11,44 @@ namespace swq {
 
 constexpr int kGemvThreads = 256;
 
-// Vectorised GEMV: one wave computes a tile of rows (4/CPL passes of 64/LPR
-// rows) over fp32 activations.
+// Vectorised GEMV over fp32 activations: each wave loads its slice of x once
+// and walks tiles of rows (4/CPL passes of 64/LPR rows) t, t + W, t + 2W, ...
+// (W: the grid's waves), the loads of the next two tiles in flight while the
+// current tile's dot products run.  Prefetches past the end repeat the last
+// tile (clamped, never used), so no load depends on a branch.
+constexpr int kGemvMaxBlocks = 1024;  // 4096 waves: 16 per CU
+
 template <int BITS, int CPL, int ES>
 __global__ __launch_bounds__(kGemvThreads) void gemv_vec_kernel(QMat m, int rows, const float *x, float *y) {
     constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const LaneMap lm = lane_map(m.lpr_log2, lane);
-    const int row0 = (blockIdx.x * (kGemvThreads / kWave) + wave) * RI * lm.rpw;
-    if (row0 >= rows) return;
-    RowTile<BITS, CPL, ES> rt;
-    load_tile(rt, m, 0, lm, row0, rows);
+    const int tile_rows = RI * lm.rpw;
+    const int ntiles = (rows + tile_rows - 1) / tile_rows;
+    const int nw = gridDim.x * (kGemvThreads / kWave);
+    int t = blockIdx.x * (kGemvThreads / kWave) + wave;
+    if (t >= ntiles) return;
     XSlice<BITS, CPL, kXF32> xs;
     load_xslice<SWQ_F32>(xs, m, lm, x, 0);
-    float res[RI];
-    dot_tile(res, rt, xs, m, lm);
-    if (lm.j == lm.lpr - 1) {
+    RowTile<BITS, CPL, ES> cur, next, next2;
+    load_tile(cur, m, 0, lm, t * tile_rows, rows);
+    load_tile(next, m, 0, lm, min(t + nw, ntiles - 1) * tile_rows, rows);
+    for (;;) {
+        const int tn = t + nw;
+        load_tile(next2, m, 0, lm, min(tn + nw, ntiles - 1) * tile_rows, rows);
+        float res[RI];
+        dot_tile(res, cur, xs, m, lm);
+        if (lm.j == lm.lpr - 1) {
 #pragma unroll
-        for (int i = 0; i < RI; ++i) {
-            const int row = row0 + i * lm.rpw + lm.q;
-            if (row < rows) y[row] = res[i];
+            for (int i = 0; i < RI; ++i) {
+                const int row = t * tile_rows + i * lm.rpw + lm.q;
+                if (row < rows) y[row] = res[i];
+            }
         }
+        if (tn >= ntiles) break;
+        cur = next;
+        next = next2;
+        t = tn;
     }
 }
 
@@ -119,7 +137,7 @@ static int launch_gemv(const swq_qlinear *l, int rows, int64_t w_extra, int64_t 
         QMat m = make_qmat(l, w_extra, s_extra, b_extra);
         if (plan_fits(m)) {
             const int rows_per_block = (kGemvThreads / kWave) * (4 / m.cpl) * (kWave >> m.lpr_log2);
-            const dim3 grid((rows + rows_per_block - 1) / rows_per_block);
+            const dim3 grid(std::min((rows + rows_per_block - 1) / rows_per_block, kGemvMaxBlocks));
 #define SWQ_GEMV_LAUNCH(B, C, E) \
     hipLaunchKernelGGL((gemv_vec_kernel<B, C, E>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y)
             const bool f32s = m.stype == SWQ_F32;
