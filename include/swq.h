@@ -45,7 +45,10 @@ enum {
     SWQ_ERR_EXPERT_RANGE = -7,      /* top_k outside [1, num_experts]         */
     SWQ_ERR_HIP = -8,               /* a HIP runtime call failed              */
     SWQ_ERR_NO_DEVICE = -9,         /* MetalEngine.Error.noDevice             */
-    SWQ_ERR_LIMIT = -10             /* batch / top_k above compiled maximum   */
+    SWQ_ERR_LIMIT = -10,            /* batch / top_k above compiled maximum   */
+    SWQ_ERR_MISSING_TENSOR = -11,   /* Checkpoint.Error.missingTensor         */
+    SWQ_ERR_IO = -12,               /* a file could not be opened or read     */
+    SWQ_ERR_FORMAT = -13            /* malformed safetensors / JSON / qpack   */
 };
 
 /* Scale, bias and activation dtypes.  The values equal
@@ -194,6 +197,106 @@ int swq_sample(const float *logits, int vocab, const swq_sample_options *options
                const int32_t *seen_ids, const int32_t *seen_counts, int n_seen,
                const int32_t *banned_ids, int n_banned, float u, int32_t *out_token,
                void *ws, size_t ws_bytes, void *stream);
+
+/* ---- checkpoint and .qpack loading ----------------------------------- */
+
+enum { SWQ_MAX_DIMS = 8 };
+
+/* A stored tensor: safetensors dtype name ("U32", "F16", "BF16", "F32", ...),
+ * shape and byte size (SafetensorsFile.TensorInfo). */
+typedef struct {
+    char dtype[8];
+    int32_t ndim;
+    int64_t shape[SWQ_MAX_DIMS];
+    int64_t nbytes;
+} swq_tensor_info;
+
+/* An mlx-lm checkpoint directory: model.safetensors, or the shards that
+ * model.safetensors.index.json maps, and config.json's "quantization" block.
+ * Replaces Checkpoint (Checkpoint.swift:28-72).  Not thread-safe. */
+typedef struct swq_checkpoint swq_checkpoint;
+
+int swq_checkpoint_open(const char *dir, swq_checkpoint **out);
+void swq_checkpoint_close(swq_checkpoint *ckpt);
+
+/* Checkpoint.tensorNames: count, and name i (valid until close). */
+int swq_checkpoint_tensor_count(const swq_checkpoint *ckpt);
+const char *swq_checkpoint_tensor_name(const swq_checkpoint *ckpt, int i);
+
+/* Tensor info; "language_model."-prefixed names resolve as
+ * Checkpoint.resolve (Checkpoint.swift:76-80).  SWQ_ERR_MISSING_TENSOR if absent. */
+int swq_checkpoint_tensor(const swq_checkpoint *ckpt, const char *name, swq_tensor_info *info);
+
+/* Checkpoint.quantSpec(for:) (Checkpoint.swift:111-120) of module `path`
+ * (e.g. "model.layers.0.mlp.gate"): SWQ_ERR_MISSING_TENSOR when the module
+ * is not stored quantized or no spec applies.  Of several matching
+ * per-module overrides the longest key wins. */
+int swq_checkpoint_quant(const swq_checkpoint *ckpt, const char *path, int *group_size, int *bits);
+
+/* Raw stored bytes into host memory (Checkpoint.rawTensor, :86-90). */
+int swq_checkpoint_read(const swq_checkpoint *ckpt, const char *name, void *dst, int64_t dst_bytes);
+
+/* Raw stored bytes into device memory through pinned staging; returns when
+ * the copy has completed.  For norms, embeddings and other plain tensors. */
+int swq_checkpoint_load(swq_checkpoint *ckpt, const char *name, void *dst, int64_t dst_bytes, void *stream);
+
+/* Device bytes swq_checkpoint_linear needs for module `path` (>= 0), or a
+ * negative status. */
+int64_t swq_checkpoint_linear_bytes(const swq_checkpoint *ckpt, const char *path);
+
+/* A quantized module (path.weight/.scales/.biases) resident in one device
+ * buffer (codes at 0, scales and biases at the next 256-byte boundaries;
+ * dst 256-byte aligned) and its descriptor.  rows_per_expert > 0 describes a
+ * stacked switch_mlp tensor as an expert stack with out_dim rows per expert
+ * (ExpertStack strides, QwenMetalModel.swift:167-188).  Unquantized modules:
+ * SWQ_ERR_UNSUPPORTED_BITS.  Replaces MetalShardStore.residentLinear
+ * (MetalShardStore.swift:67-118); the file-backed gpuLinear (:120-158) has no
+ * counterpart: weights always live in HBM. */
+int swq_checkpoint_linear(swq_checkpoint *ckpt, const char *path, int rows_per_expert, void *dst,
+                          int64_t dst_bytes, swq_qlinear *out, void *stream);
+
+/* A .qpack container (Qpack.swift:3-17): packed_experts/layout.json,
+ * manifest.json and packed_experts/layer_NN.bin, one fixed-stride blob per
+ * expert.  Replaces QpackExpertReader (Qpack.swift:168-203).  Not thread-safe. */
+typedef struct swq_qpack swq_qpack;
+
+typedef struct {
+    int32_t expert_count, layer_count;  /* Qpack.Layout (Qpack.swift:30-36)  */
+    int64_t expert_stride;              /* bytes per blob, 16 KiB multiple    */
+    int32_t quant_bits, quant_group_size; /* Qpack.Manifest; 0 if absent     */
+    int32_t section_count;
+} swq_qpack_layout_info;
+
+int swq_qpack_open(const char *container_dir, swq_qpack **out);
+void swq_qpack_close(swq_qpack *qp);
+int swq_qpack_layout(const swq_qpack *qp, swq_qpack_layout_info *info);
+
+/* Layout.linearLayers[layer]: 1 / 0, or a negative status. */
+int swq_qpack_is_linear_layer(const swq_qpack *qp, int layer);
+
+/* Section i (Qpack.Section, Qpack.swift:22-28): name (valid until close),
+ * byte offset inside a blob, dtype and per-expert shape. */
+int swq_qpack_section(const swq_qpack *qp, int index, const char **name, int64_t *offset,
+                      swq_tensor_info *info);
+/* QpackExpertReader.section(_:) (Qpack.swift:199-201): the section's index. */
+int swq_qpack_find_section(const swq_qpack *qp, const char *name);
+
+/* One blob into host memory, one pread of expert_stride bytes
+ * (QpackExpertReader.readExpert, Qpack.swift:185-197). */
+int swq_qpack_read_expert(swq_qpack *qp, int layer, int expert, void *dst, int64_t dst_bytes);
+
+/* Blobs [first_expert, first_expert + count) of a layer into device memory,
+ * byte for byte (count * expert_stride bytes); the whole layer is
+ * first_expert 0, count expert_count.  Returns when the copy has completed.
+ * Replaces ExpertCache's slot fill (ExpertCache.swift:66-69). */
+int swq_qpack_load_experts(swq_qpack *qp, int layer, int first_expert, int count, void *dst,
+                           int64_t dst_bytes, void *stream);
+
+/* The expert stack of projection `proj` ("gate_proj", "up_proj", "down_proj")
+ * inside blobs resident at `base` (blob 0 of the loaded range): offsets are
+ * the sections', expert_stride_w = expert_stride_sb = expert_stride, bits and
+ * group from the manifest.  Replaces ExpertProj (QwenMetalModel.swift:137-165). */
+int swq_qpack_expert_linear(const swq_qpack *qp, const void *base, const char *proj, swq_qlinear *out);
 
 /* ---- MoE layer decode ------------------------------------------------- */
 

@@ -21,6 +21,9 @@ SWQ_ERR_EXPERT_RANGE = -7
 SWQ_ERR_HIP = -8
 SWQ_ERR_NO_DEVICE = -9
 SWQ_ERR_LIMIT = -10
+SWQ_ERR_MISSING_TENSOR = -11
+SWQ_ERR_IO = -12
+SWQ_ERR_FORMAT = -13
 
 SWQ_F32, SWQ_F16, SWQ_BF16 = 0, 1, 2
 SWQ_MAX_BATCH, SWQ_MAX_TOPK = 16, 16
@@ -54,6 +57,20 @@ class SampleOptions(ctypes.Structure):
                 ("presence_penalty", ctypes.c_float), ("frequency_penalty", ctypes.c_float)]
 
 
+SWQ_MAX_DIMS = 8
+
+
+class TensorInfo(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_char * 8), ("ndim", ctypes.c_int32),
+                ("shape", ctypes.c_int64 * SWQ_MAX_DIMS), ("nbytes", ctypes.c_int64)]
+
+
+class QpackLayoutInfo(ctypes.Structure):
+    _fields_ = [("expert_count", ctypes.c_int32), ("layer_count", ctypes.c_int32),
+                ("expert_stride", ctypes.c_int64), ("quant_bits", ctypes.c_int32),
+                ("quant_group_size", ctypes.c_int32), ("section_count", ctypes.c_int32)]
+
+
 class MoELayer(ctypes.Structure):
     _fields_ = [
         ("router", QLinear), ("gate", QLinear), ("up", QLinear), ("down", QLinear),
@@ -85,6 +102,25 @@ SIGNATURES = {
     "swq_rmsnorm": (_I, [_P, _P, _P, _I, _c.c_float, _I, _I, _P, _I, _P]),
     "swq_sample_workspace_bytes": (_SZ, [_I]),
     "swq_sample": (_I, [_P, _I, _c.POINTER(SampleOptions), _P, _P, _I, _P, _I, _c.c_float, _P, _P, _SZ, _P]),
+    "swq_checkpoint_open": (_I, [_c.c_char_p, _c.POINTER(_P)]),
+    "swq_checkpoint_close": (None, [_P]),
+    "swq_checkpoint_tensor_count": (_I, [_P]),
+    "swq_checkpoint_tensor_name": (_c.c_char_p, [_P, _I]),
+    "swq_checkpoint_tensor": (_I, [_P, _c.c_char_p, _c.POINTER(TensorInfo)]),
+    "swq_checkpoint_quant": (_I, [_P, _c.c_char_p, _c.POINTER(_I), _c.POINTER(_I)]),
+    "swq_checkpoint_read": (_I, [_P, _c.c_char_p, _P, _I64]),
+    "swq_checkpoint_load": (_I, [_P, _c.c_char_p, _P, _I64, _P]),
+    "swq_checkpoint_linear_bytes": (_I64, [_P, _c.c_char_p]),
+    "swq_checkpoint_linear": (_I, [_P, _c.c_char_p, _I, _P, _I64, _c.POINTER(QLinear), _P]),
+    "swq_qpack_open": (_I, [_c.c_char_p, _c.POINTER(_P)]),
+    "swq_qpack_close": (None, [_P]),
+    "swq_qpack_layout": (_I, [_P, _c.POINTER(QpackLayoutInfo)]),
+    "swq_qpack_is_linear_layer": (_I, [_P, _I]),
+    "swq_qpack_section": (_I, [_P, _I, _c.POINTER(_c.c_char_p), _c.POINTER(_I64), _c.POINTER(TensorInfo)]),
+    "swq_qpack_find_section": (_I, [_P, _c.c_char_p]),
+    "swq_qpack_read_expert": (_I, [_P, _I, _I, _P, _I64]),
+    "swq_qpack_load_experts": (_I, [_P, _I, _I, _I, _P, _I64, _P]),
+    "swq_qpack_expert_linear": (_I, [_P, _P, _c.c_char_p, _c.POINTER(QLinear)]),
     "swq_moe_decode_workspace_bytes": (_SZ, [_c.POINTER(MoELayer), _I]),
     "swq_moe_workspace_init": (_I, [_P, _SZ, _P]),
     "swq_moe_decode": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _I, _P]),

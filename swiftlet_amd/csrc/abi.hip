@@ -14,6 +14,9 @@ extern "C" const char *swq_strerror(int status) {
         case SWQ_ERR_HIP: return "HIP runtime error";
         case SWQ_ERR_NO_DEVICE: return "no HIP device";
         case SWQ_ERR_LIMIT: return "size above compiled limit";
+        case SWQ_ERR_MISSING_TENSOR: return "tensor or section not found";
+        case SWQ_ERR_IO: return "file open or read failed";
+        case SWQ_ERR_FORMAT: return "malformed checkpoint, JSON or qpack layout";
         default: return "unknown status";
     }
 }
