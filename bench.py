@@ -76,6 +76,7 @@ def parse():
     ap.add_argument("--config", default="qwen3.6-35b-a3b-q4-b1", choices=sorted(CONFIGS) + sorted(PREFILL_CONFIGS))
     ap.add_argument("--no-prefill", action="store_true", help="decode line without the prefill summary")
     ap.add_argument("--no-lmhead", action="store_true", help="decode line without the lm_head + sampling summary")
+    ap.add_argument("--no-load", action="store_true", help="decode line without the qpack layer-load rate")
     ap.add_argument("--prefill-steps", type=int, default=40, help="prefill chunks timed")
     ap.add_argument("--prefill-replicas", type=int, default=3, help="distinct layers the prefill chunks cycle")
     ap.add_argument("--replicas", type=int, default=48, help="distinct layers cycled through (MALL defeat)")
@@ -326,6 +327,10 @@ def main():
     if not args.no_lmhead and shape_key.startswith("qwen3.6-35b"):
         result["lm_head"] = lmhead_measure(args, torch, lib, shape.hidden)
 
+    # ---- loading: one .qpack layer file into HBM ----------------------------
+    if not args.no_load and shape_key.startswith("qwen3.6-35b"):
+        result["qpack_load"] = qpack_load_measure(torch, lib, shape)
+
     # ---- the prefill chunk, summarised --------------------------------------
     if not args.no_prefill:
         del layers, wss, graph
@@ -336,6 +341,68 @@ def main():
         result["prefill"] = {k: line[k] for k in ("config", "value", "unit", "roofline", "kernel_us", "mfma")}
 
     print(json.dumps(result), flush=True)
+
+
+PCIE_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
+
+
+def qpack_load_measure(torch, lib, shape, reps=3):
+    """One layer file of a .qpack container (E blobs of the layer's gate, up
+    and down codes, scales and biases, 16 KiB-aligned) read from the page
+    cache and copied into HBM by swq_qpack_load_experts: pread into two
+    pinned 16 MiB staging buffers, host-to-device copies overlapped with the
+    next read.  The file is written to a temporary directory first (synthetic
+    bytes) and read once untimed."""
+    import shutil
+    import tempfile
+
+    from swiftlet_amd._lib import check
+    H, I, E, bits = shape.hidden, shape.inter, shape.experts, shape.expert_bits
+    g = shape.group
+    sections, off = [], 0
+    for proj, rows, cols in (("gate_proj", I, H), ("up_proj", I, H), ("down_proj", H, I)):
+        for part, dt, per_shape, size in (("weight", "U32", [rows, cols * bits // 32], rows * cols * bits // 8),
+                                          ("scales", "F16", [rows, cols // g], rows * cols // g * 2),
+                                          ("biases", "F16", [rows, cols // g], rows * cols // g * 2)):
+            sections.append({"name": f"{proj}.{part}", "dtype": dt, "shape": per_shape, "offset": off, "size": size})
+            off += size
+    stride = (off + 16383) // 16384 * 16384
+    d = tempfile.mkdtemp(prefix="swq-qpack-", dir="/tmp")
+    try:
+        os.makedirs(os.path.join(d, "packed_experts"))
+        with open(os.path.join(d, "packed_experts", "layout.json"), "w") as f:
+            json.dump({"expertCount": E, "layerCount": 1, "expertStride": stride, "sections": sections,
+                       "linearLayers": [True]}, f)
+        with open(os.path.join(d, "manifest.json"), "w") as f:
+            json.dump({"magic": "QPACK", "version": 1, "modelName": "synthetic", "sourceCheckpoint": "synthetic",
+                       "quantBits": bits, "quantGroupSize": g, "files": {}}, f)
+        blob = np.arange(stride // 4, dtype=np.uint32).tobytes()
+        with open(os.path.join(d, "packed_experts", "layer_00.bin"), "wb") as f:
+            for _ in range(E):
+                f.write(blob)
+        n = E * stride
+        h = ctypes.c_void_p()
+        check(lib.swq_qpack_open(d.encode(), ctypes.byref(h)), "qpack open")
+        dst = torch.empty(n, dtype=torch.uint8, device="cuda")
+        times = []
+        for i in range(reps + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            check(lib.swq_qpack_load_experts(h, 0, 0, E, ctypes.c_void_p(dst.data_ptr()), n, None), "load")
+            torch.cuda.synchronize()
+            if i:
+                times.append(time.perf_counter() - t0)
+        lib.swq_qpack_close(h)
+        ok = bytes(dst[:stride].cpu().numpy()) == blob
+        del dst
+        best = min(times)
+        return {"layer_file_bytes": n, "expert_stride": stride, "ms": round(best * 1e3, 2),
+                "gbs": round(n / best / 1e9, 2), "pcie_peak_gbs": PCIE_PEAK_GBS,
+                "frac": round(n / best / 1e9 / PCIE_PEAK_GBS, 3), "first_blob_intact": ok,
+                "note": "one 35B-shape layer file (E blobs), page-cache warm, best of "
+                        f"{reps}: pread into pinned staging + host-to-device copies"}
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
 
 
 LMHEAD_VOCAB = 248320  # qwen3.6-35b vocab_size (model config)

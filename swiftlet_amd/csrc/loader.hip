@@ -32,6 +32,7 @@
 #include <map>
 #include <new>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "internal.hpp"
@@ -70,6 +71,30 @@ bool read_exact(int fd, void *dst, int64_t n, int64_t off) {
         n -= r;
     }
     return true;
+}
+
+// read_exact split over up to kReadThreads threads (slices of >= 2 MiB): a
+// page-cache read is a memory copy, and one thread's copy rate is below
+// what the host link takes.
+constexpr int kReadThreads = 4;
+
+bool read_parallel(int fd, void *dst, int64_t n, int64_t off) {
+    const int64_t slice = std::max<int64_t>(2 << 20, (n + kReadThreads - 1) / kReadThreads);
+    const int parts = static_cast<int>(std::min<int64_t>(kReadThreads, (n + slice - 1) / slice));
+    if (parts <= 1) return read_exact(fd, dst, n, off);
+    bool ok[kReadThreads];
+    std::thread th[kReadThreads];
+    for (int i = 1; i < parts; ++i) {
+        const int64_t b = i * slice, len = std::min(slice, n - b);
+        th[i] = std::thread([&, i, b, len] { ok[i] = read_exact(fd, static_cast<uint8_t *>(dst) + b, len, off + b); });
+    }
+    ok[0] = read_exact(fd, dst, std::min(slice, n), off);
+    bool all = ok[0];
+    for (int i = 1; i < parts; ++i) {
+        th[i].join();
+        all = all && ok[i];
+    }
+    return all;
 }
 
 bool read_text(const std::string &path, std::string &out) {
@@ -166,7 +191,7 @@ struct Staging {
             const int b = k & 1;
             if (used[b] && hipEventSynchronize(ev[b]) != hipSuccess) return SWQ_ERR_HIP;
             const int64_t len = std::min<int64_t>(n - done, static_cast<int64_t>(kStageBytes));
-            if (!read_exact(fd, buf[b], len, off + done)) {
+            if (!read_parallel(fd, buf[b], len, off + done)) {
                 drain();
                 return SWQ_ERR_IO;
             }
