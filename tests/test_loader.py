@@ -48,6 +48,21 @@ def test_tensor_infos_and_bytes_match_the_files(ckpt_dir):
         assert c.raw_tensor(name) == raw, name
 
 
+@pytest.mark.parametrize("name", ["tiny-model-q4/model.safetensors", "tiny-model/model.safetensors",
+                                  "tiny_forward_q4.safetensors"])
+def test_oracle_reader_matches_the_safetensors_package(name):
+    """The test-side parse itself, against the safetensors package's loader."""
+    import numpy as np
+    from safetensors.numpy import load_file
+    want = load_file(str(FIXTURES / name))
+    got = Q.read_safetensors(FIXTURES / name)
+    assert sorted(got) == sorted(want)
+    for k, arr in want.items():
+        dtype, shape, raw = got[k]
+        assert list(arr.shape) == shape and arr.dtype.itemsize == Q.ELEM[dtype], k
+        assert np.ascontiguousarray(arr).tobytes() == raw, k
+
+
 def test_quant_specs_follow_config():
     c = Checkpoint(Q4)
     cfg = json.loads((Q4 / "config.json").read_text())["quantization"]
