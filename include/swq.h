@@ -198,6 +198,54 @@ int swq_sample(const float *logits, int vocab, const swq_sample_options *options
                const int32_t *banned_ids, int n_banned, float u, int32_t *out_token,
                void *ws, size_t ws_bytes, void *stream);
 
+/* ---- gated DeltaNet decode step ---------------------------------------- */
+
+/* Layouts of the DeltaNet input projections (QwenConfig.DeltaProjectionLayout). */
+enum {
+    /* qwen3_next: in_proj_qkvz per key head [q(dk) k(dk) v(rep*dv) z(rep*dv)],
+     * in_proj_ba per key head [b(rep) a(rep)] (QwenCPUModel.swift:386-410). */
+    SWQ_DELTA_INTERLEAVED = 0,
+    /* qwen3_5: in_proj_qkv [q | k | v] followed by in_proj_z [z] in one
+     * buffer; in_proj_b [b] followed by in_proj_a [a] (:411-415). */
+    SWQ_DELTA_SPLIT = 1
+};
+
+/* One gated DeltaNet block (linear_attn) between its input projections and
+ * out_proj.  The small parameters are f32 device arrays, as the reference
+ * holds them (QwenMetalModel FastLayer convW/aLog/dtBias/deltaNormW). */
+typedef struct swq_deltanet_layer {
+    int32_t num_key_heads;       /* nk                                        */
+    int32_t num_value_heads;     /* nv, a multiple of nk                      */
+    int32_t key_head_dim;        /* dk: 8, 16, 32, 64, 128 or 256             */
+    int32_t value_head_dim;      /* dv <= 1024                                */
+    int32_t conv_kernel;         /* K <= 8 (linear_conv_kernel_dim)           */
+    int32_t layout;              /* SWQ_DELTA_INTERLEAVED / SWQ_DELTA_SPLIT   */
+    float norm_eps;              /* rms_norm_eps of the gated norm            */
+    int32_t reserved;            /* must be 0                                 */
+    const float *conv_weight;    /* conv1d.weight [2*nk*dk + nv*dv][K]        */
+    const float *a_log;          /* A_log [nv]                                */
+    const float *dt_bias;        /* dt_bias [nv]                              */
+    const float *norm_weight;    /* norm.weight [dv]                          */
+} swq_deltanet_layer;
+
+/* Bytes of one sequence's DeltaNet state for this layer (0 on bad input): the
+ * conv history as a ring of K rows [K][convD] f32, then (at the next 256-byte
+ * boundary) the recurrent state [nv][dv][dk] f32.  All zeros is a fresh
+ * session (the reference's resetGPUState / empty DecodeState). */
+size_t swq_deltanet_state_bytes(const swq_deltanet_layer *layer);
+
+/* One token: qkvz / ba are the input projections' outputs (f32, device) in
+ * the layer's layout; position is the number of tokens already in `state`
+ * (the row of position p lives in ring slot p % K).  out: [nv*dv] f32, the
+ * gated-normed output, the input of out_proj.  Updates `state` in place.
+ * Replaces encDeltaLayer's deinterleave_qkvz, conv_step, delta_pre,
+ * rmsnorm_rows (q, k), gated_delta_step and gated_norm_mul
+ * (QwenMetalModel.swift:989-1084; Kernels.metal.txt:126-214, :305-422,
+ * :497-519) with the numerics of QwenCPUModel.deltaNetForward for one token
+ * (QwenCPUModel.swift:417-493). */
+int swq_deltanet_step(const swq_deltanet_layer *layer, const float *qkvz, const float *ba, void *state,
+                      size_t state_bytes, int64_t position, float *out, void *stream);
+
 /* ---- checkpoint and .qpack loading ----------------------------------- */
 
 enum { SWQ_MAX_DIMS = 8 };

@@ -26,6 +26,7 @@ from pathlib import Path
 import numpy as np
 from safetensors.numpy import load_file
 
+from . import deltanet_ref as D
 from . import moe_ref as R
 
 f32 = np.float32
@@ -166,68 +167,27 @@ class TinyQwen:
         return (out @ ck.module_weight(p + "o_proj").T).astype(f32)
 
     # -- gated DeltaNet, fused interleaved layout (QwenCPUModel.swift:371-496)
-    def deltanet_forward(self, x: np.ndarray, i: int) -> np.ndarray:
+    def deltanet_params(self, i: int):
+        """Layer i's DeltaNet shapes and small parameters for deltanet_core."""
         c, ck = self.c, self.ck
         p = f"model.layers.{i}.linear_attn."
-        nk, nv = c["linear_num_key_heads"], c["linear_num_value_heads"]
-        dk, dv = c["linear_key_head_dim"], c["linear_value_head_dim"]
-        rep = nv // nk
-        keyD, valD = nk * dk, nv * dv
-        convD = 2 * keyD + valD
-        Kc = c["linear_conv_kernel_dim"]
-        S = x.shape[0]
-        qkvz = x @ ck.module_weight(p + "in_proj_qkvz").T
-        ba = x @ ck.module_weight(p + "in_proj_ba").T
-        chunk = 2 * dk + 2 * rep * dv
-        mixed = np.zeros((S, convD), f32)
-        z = np.zeros((S, valD), f32)
-        bA = np.zeros((S, nv), f32)
-        aA = np.zeros((S, nv), f32)
-        for hk in range(nk):
-            src = qkvz[:, hk * chunk:(hk + 1) * chunk]
-            mixed[:, hk * dk:(hk + 1) * dk] = src[:, :dk]
-            mixed[:, keyD + hk * dk:keyD + (hk + 1) * dk] = src[:, dk:2 * dk]
-            for ri in range(rep):
-                hv = hk * rep + ri
-                mixed[:, 2 * keyD + hv * dv:2 * keyD + (hv + 1) * dv] = src[:, 2 * dk + ri * dv:2 * dk + (ri + 1) * dv]
-                z[:, hv * dv:(hv + 1) * dv] = src[:, 2 * dk + rep * dv + ri * dv:2 * dk + rep * dv + (ri + 1) * dv]
-            bsrc = ba[:, hk * 2 * rep:(hk + 1) * 2 * rep]
-            bA[:, hk * rep:(hk + 1) * rep] = bsrc[:, :rep]
-            aA[:, hk * rep:(hk + 1) * rep] = bsrc[:, rep:]
-        conv_w = ck.tensor(p + "conv1d.weight").reshape(convD, Kc)
-        padded = np.concatenate([np.zeros((Kc - 1, convD), f32), mixed], axis=0)
-        conv = np.zeros((S, convD), f32)
-        for s in range(S):
-            acc = np.zeros(convD, f32)
-            for j in range(Kc):
-                acc = acc + conv_w[:, j] * padded[s + j]
-            conv[s] = acc
-        conv = R.silu(conv)
-        qh = rms_norm(conv[:, :keyD].reshape(S, nk, dk), None, 1e-6)
-        kh = rms_norm(conv[:, keyD:2 * keyD].reshape(S, nk, dk), None, 1e-6)
-        vh = conv[:, 2 * keyD:].reshape(S, nv, dv)
-        inv = f32(1) / np.sqrt(f32(dk))
-        qh = qh * (inv * inv)
-        kh = kh * inv
-        a_log, dt_bias = ck.tensor(p + "A_log"), ck.tensor(p + "dt_bias")
-        state = np.zeros((nv, dv, dk), f32)
-        out = np.zeros((S, nv, dv), f32)
-        for s in range(S):
-            for hv in range(nv):
-                hk = hv // rep
-                v_ = aA[s, hv] + dt_bias[hv]
-                softplus = v_ if v_ > 20 else np.log1p(np.exp(v_))
-                g = np.exp(-np.exp(a_log[hv]) * softplus).astype(f32)
-                beta = R.sigmoid(bA[s, hv])
-                st = state[hv] * g
-                kv_mem = st @ kh[s, hk]
-                delta = (vh[s, hv] - kv_mem) * beta
-                st = st + np.outer(delta, kh[s, hk])
-                state[hv] = st
-                out[s, hv] = st @ qh[s, hk]
-        normed = rms_norm(out, ck.tensor(p + "norm.weight"), self.eps).reshape(S, valD)
-        normed = normed * R.silu(z)
-        return (normed @ ck.module_weight(p + "out_proj").T).astype(f32)
+        return dict(conv_w=ck.tensor(p + "conv1d.weight"), a_log=ck.tensor(p + "A_log"),
+                    dt_bias=ck.tensor(p + "dt_bias"), norm_w=ck.tensor(p + "norm.weight"),
+                    nk=c["linear_num_key_heads"], nv=c["linear_num_value_heads"],
+                    dk=c["linear_key_head_dim"], dv=c["linear_value_head_dim"], eps=self.eps)
+
+    def deltanet_projections(self, x: np.ndarray, i: int):
+        """The fused projections' outputs (in_proj_qkvz, in_proj_ba)."""
+        p = f"model.layers.{i}.linear_attn."
+        return (x @ self.ck.module_weight(p + "in_proj_qkvz").T).astype(f32), \
+            (x @ self.ck.module_weight(p + "in_proj_ba").T).astype(f32)
+
+    def deltanet_forward(self, x: np.ndarray, i: int) -> np.ndarray:
+        prm = self.deltanet_params(i)
+        qkvz, ba = self.deltanet_projections(x, i)
+        mixed, z, b, a = D.deinterleave(qkvz, ba, prm["nk"], prm["nv"], prm["dk"], prm["dv"])
+        y, _, _ = D.deltanet_core(mixed, z, b, a, **prm)
+        return (y @ self.ck.module_weight(f"model.layers.{i}.linear_attn.out_proj").T).astype(f32)
 
     # -- layer / model ------------------------------------------------------
     def layer_forward(self, h: np.ndarray, i: int) -> np.ndarray:

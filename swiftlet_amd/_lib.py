@@ -71,6 +71,19 @@ class QpackLayoutInfo(ctypes.Structure):
                 ("quant_group_size", ctypes.c_int32), ("section_count", ctypes.c_int32)]
 
 
+SWQ_DELTA_INTERLEAVED, SWQ_DELTA_SPLIT = 0, 1
+
+
+class DeltaNetLayer(ctypes.Structure):
+    _fields_ = [
+        ("num_key_heads", ctypes.c_int32), ("num_value_heads", ctypes.c_int32),
+        ("key_head_dim", ctypes.c_int32), ("value_head_dim", ctypes.c_int32),
+        ("conv_kernel", ctypes.c_int32), ("layout", ctypes.c_int32), ("norm_eps", ctypes.c_float),
+        ("reserved", ctypes.c_int32), ("conv_weight", ctypes.c_void_p), ("a_log", ctypes.c_void_p),
+        ("dt_bias", ctypes.c_void_p), ("norm_weight", ctypes.c_void_p),
+    ]
+
+
 class MoELayer(ctypes.Structure):
     _fields_ = [
         ("router", QLinear), ("gate", QLinear), ("up", QLinear), ("down", QLinear),
@@ -102,6 +115,8 @@ SIGNATURES = {
     "swq_rmsnorm": (_I, [_P, _P, _P, _I, _c.c_float, _I, _I, _P, _I, _P]),
     "swq_sample_workspace_bytes": (_SZ, [_I]),
     "swq_sample": (_I, [_P, _I, _c.POINTER(SampleOptions), _P, _P, _I, _P, _I, _c.c_float, _P, _P, _SZ, _P]),
+    "swq_deltanet_state_bytes": (_SZ, [_c.POINTER(DeltaNetLayer)]),
+    "swq_deltanet_step": (_I, [_c.POINTER(DeltaNetLayer), _P, _P, _P, _SZ, _I64, _P, _P]),
     "swq_checkpoint_open": (_I, [_c.c_char_p, _c.POINTER(_P)]),
     "swq_checkpoint_close": (None, [_P]),
     "swq_checkpoint_tensor_count": (_I, [_P]),

@@ -187,3 +187,32 @@ def test_prefill_call_validation(lib):
     n = lib.swq_moe_prefill_workspace_bytes(ctypes.byref(L), 64)
     assert lib.swq_moe_prefill_biased(ctypes.byref(L), FAKE, _lib.SWQ_BF16, 64, FAKE, _lib.SWQ_F32, None, None,
                                       None, FAKE, n, 0, None) == _lib.SWQ_ERR_INVALID_ARGUMENT
+
+
+def test_deltanet_validation(lib):
+    """swq_deltanet_step's failure modes, returned before any launch."""
+    from swiftlet_amd._lib import DeltaNetLayer
+    ok = dict(num_key_heads=16, num_value_heads=32, key_head_dim=128, value_head_dim=128, conv_kernel=4,
+              layout=_lib.SWQ_DELTA_SPLIT, norm_eps=1e-6, reserved=0, conv_weight=FAKE, a_log=FAKE, dt_bias=FAKE,
+              norm_weight=FAKE)
+    L = DeltaNetLayer(**ok)
+    n = lib.swq_deltanet_state_bytes(ctypes.byref(L))
+    assert n == 4 * (2 * 16 * 128 + 32 * 128) * 4 + 32 * 128 * 128 * 4  # ring [K][convD] + state [nv][dv][dk]
+
+    def step(layer, state_bytes=n, position=0, state=FAKE, qkvz=FAKE):
+        return lib.swq_deltanet_step(ctypes.byref(layer), qkvz, FAKE, state, state_bytes, position, FAKE, None)
+
+    for field, value, code in [("num_value_heads", 31, _lib.SWQ_ERR_BAD_SHAPE),
+                               ("key_head_dim", 96, _lib.SWQ_ERR_LIMIT),
+                               ("value_head_dim", 2048, _lib.SWQ_ERR_LIMIT),
+                               ("conv_kernel", 9, _lib.SWQ_ERR_LIMIT),
+                               ("layout", 2, _lib.SWQ_ERR_INVALID_ARGUMENT),
+                               ("reserved", 1, _lib.SWQ_ERR_INVALID_ARGUMENT),
+                               ("a_log", None, _lib.SWQ_ERR_INVALID_ARGUMENT)]:
+        bad = DeltaNetLayer(**dict(ok, **{field: value}))
+        assert step(bad) == code, field
+        assert lib.swq_deltanet_state_bytes(ctypes.byref(bad)) == 0, field
+    assert step(L, state_bytes=n - 1) == _lib.SWQ_ERR_WORKSPACE
+    assert step(L, position=-1) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert step(L, state=FAKE + 16) == _lib.SWQ_ERR_MISALIGNED
+    assert step(L, qkvz=None) == _lib.SWQ_ERR_INVALID_ARGUMENT
