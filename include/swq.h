@@ -246,6 +246,45 @@ size_t swq_deltanet_state_bytes(const swq_deltanet_layer *layer);
 int swq_deltanet_step(const swq_deltanet_layer *layer, const float *qkvz, const float *ba, void *state,
                       size_t state_bytes, int64_t position, float *out, void *stream);
 
+/* ---- gated GQA attention decode step ------------------------------------ */
+
+/* One full-attention block (self_attn) between q/k/v_proj and o_proj. */
+typedef struct swq_attention_layer {
+    int32_t num_heads;           /* H                                         */
+    int32_t num_kv_heads;        /* KVH; H / KVH <= 16                        */
+    int32_t head_dim;            /* hd: 16, 32, 64, 128 or 256                */
+    int32_t rotary_dims;         /* even, <= hd (QwenConfig.rotaryDims)       */
+    float rope_theta;
+    float norm_eps;              /* rms_norm_eps of q_norm / k_norm           */
+    int32_t max_positions;       /* rows of the KV cache                      */
+    int32_t reserved;            /* must be 0                                 */
+    const float *q_norm_weight;  /* q_norm.weight [hd] f32 (device)           */
+    const float *k_norm_weight;  /* k_norm.weight [hd] f32 (device)           */
+} swq_attention_layer;
+
+/* Bytes of one sequence's KV cache: k then v (at a 256-byte boundary), each
+ * f32 [max_positions][KVH][hd], rows in position order as the reference
+ * appends them (DecodeState.kv).  0 on bad input. */
+size_t swq_attention_cache_bytes(const swq_attention_layer *layer);
+
+/* Workspace bytes of swq_attention_step (per-split partial results). */
+size_t swq_attention_workspace_bytes(const swq_attention_layer *layer);
+
+/* One token at `position` (= the cached positions): q_proj [H][2*hd] (per
+ * head the query, then the output gate), k_proj / v_proj [KVH*hd], f32
+ * device vectors.  q and k are RMS-normalised with their weights and rotated
+ * (partial NeoX RoPE on the first rotary_dims, angle = position *
+ * theta^(-2j/rotary_dims)); k and v are appended to the cache at `position`;
+ * each head attends over positions 0..position of its kv head (head / (H/KVH))
+ * with scale 1/sqrt(hd); out [H*hd] = attention * sigmoid(gate), the input of
+ * o_proj.  position >= max_positions: SWQ_ERR_LIMIT.  Two launches; the
+ * launch shape depends on `position` (a captured graph holds one position).
+ * Replaces attnCoreCPU (QwenMetalModel.swift:1086-1134) with the numerics of
+ * QwenCPUModel.attentionForward for one token (QwenCPUModel.swift:285-367). */
+int swq_attention_step(const swq_attention_layer *layer, const float *q_proj, const float *k_proj,
+                       const float *v_proj, void *cache, size_t cache_bytes, int64_t position, float *out,
+                       void *ws, size_t ws_bytes, void *stream);
+
 /* ---- checkpoint and .qpack loading ----------------------------------- */
 
 enum { SWQ_MAX_DIMS = 8 };

@@ -26,6 +26,7 @@ from pathlib import Path
 import numpy as np
 from safetensors.numpy import load_file
 
+from . import attention_ref as A
 from . import deltanet_ref as D
 from . import moe_ref as R
 
@@ -126,45 +127,25 @@ class TinyQwen:
             top_k=self.c["num_experts_per_tok"], norm_topk_prob=bool(self.c.get("norm_topk_prob", False)))
 
     # -- attention (QwenCPUModel.swift:285-345) ---------------------------
-    def apply_rope(self, x: np.ndarray) -> np.ndarray:
-        c = self.c
-        hd = c["head_dim"]
-        rot = int(hd * c.get("partial_rotary_factor", 0.25))
-        half = rot // 2
-        S = x.shape[0]
-        j = np.arange(half)
-        inv = np.power(f32(c["rope_theta"]), (-(2 * j).astype(f32) / f32(rot)).astype(f32)).astype(f32)
-        ang = (np.arange(S, dtype=f32)[:, None] * inv[None, :]).astype(f32)
-        cs, sn = np.cos(ang).astype(f32)[:, None, :], np.sin(ang).astype(f32)[:, None, :]
-        out = x.copy()
-        a, b = x[..., :half], x[..., half:rot]
-        out[..., :half] = a * cs - b * sn
-        out[..., half:rot] = b * cs + a * sn
-        return out
-
-    def attention_forward(self, x: np.ndarray, i: int) -> np.ndarray:
+    def attention_params(self, i: int):
+        """Layer i's attention shapes and norm weights for attention_core."""
         c, ck = self.c, self.ck
         p = f"model.layers.{i}.self_attn."
-        H, KVH, hd = c["num_attention_heads"], c["num_key_value_heads"], c["head_dim"]
-        S = x.shape[0]
-        q_out = (x @ ck.module_weight(p + "q_proj").T).reshape(S, H, 2 * hd)
-        q, gate = q_out[..., :hd], q_out[..., hd:].reshape(S, H * hd)
-        k = (x @ ck.module_weight(p + "k_proj").T).reshape(S, KVH, hd)
-        v = (x @ ck.module_weight(p + "v_proj").T).reshape(S, KVH, hd)
-        q = rms_norm(q, ck.tensor(p + "q_norm.weight"), self.eps)
-        k = rms_norm(k, ck.tensor(p + "k_norm.weight"), self.eps)
-        q, k = self.apply_rope(q), self.apply_rope(k)
-        scale = f32(1) / np.sqrt(f32(hd))
-        out = np.zeros((S, H, hd), f32)
-        group = H // KVH
-        for h in range(H):
-            kv = h // group
-            for si in range(S):
-                sc = (k[: si + 1, kv, :] @ q[si, h, :]) * scale
-                pr = R.softmax_row(sc)
-                out[si, h] = pr @ v[: si + 1, kv, :]
-        out = out.reshape(S, H * hd) * R.sigmoid(gate)
-        return (out @ ck.module_weight(p + "o_proj").T).astype(f32)
+        hd = c["head_dim"]
+        return dict(q_norm_w=ck.tensor(p + "q_norm.weight"), k_norm_w=ck.tensor(p + "k_norm.weight"),
+                    H=c["num_attention_heads"], KVH=c["num_key_value_heads"], hd=hd,
+                    rot=int(hd * c.get("partial_rotary_factor", 0.25)), theta=float(c["rope_theta"]), eps=self.eps)
+
+    def attention_projections(self, x: np.ndarray, i: int):
+        """q_proj (query | gate per head), k_proj and v_proj outputs."""
+        p = f"model.layers.{i}.self_attn."
+        ck = self.ck
+        return tuple((x @ ck.module_weight(p + n).T).astype(f32) for n in ("q_proj", "k_proj", "v_proj"))
+
+    def attention_forward(self, x: np.ndarray, i: int) -> np.ndarray:
+        q_out, k, v = self.attention_projections(x, i)
+        out, _, _ = A.attention_core(q_out, k, v, **self.attention_params(i))
+        return (out @ self.ck.module_weight(f"model.layers.{i}.self_attn.o_proj").T).astype(f32)
 
     # -- gated DeltaNet, fused interleaved layout (QwenCPUModel.swift:371-496)
     def deltanet_params(self, i: int):

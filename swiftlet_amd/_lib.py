@@ -84,6 +84,15 @@ class DeltaNetLayer(ctypes.Structure):
     ]
 
 
+class AttentionLayer(ctypes.Structure):
+    _fields_ = [
+        ("num_heads", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("rotary_dims", ctypes.c_int32), ("rope_theta", ctypes.c_float), ("norm_eps", ctypes.c_float),
+        ("max_positions", ctypes.c_int32), ("reserved", ctypes.c_int32),
+        ("q_norm_weight", ctypes.c_void_p), ("k_norm_weight", ctypes.c_void_p),
+    ]
+
+
 class MoELayer(ctypes.Structure):
     _fields_ = [
         ("router", QLinear), ("gate", QLinear), ("up", QLinear), ("down", QLinear),
@@ -117,6 +126,9 @@ SIGNATURES = {
     "swq_sample": (_I, [_P, _I, _c.POINTER(SampleOptions), _P, _P, _I, _P, _I, _c.c_float, _P, _P, _SZ, _P]),
     "swq_deltanet_state_bytes": (_SZ, [_c.POINTER(DeltaNetLayer)]),
     "swq_deltanet_step": (_I, [_c.POINTER(DeltaNetLayer), _P, _P, _P, _SZ, _I64, _P, _P]),
+    "swq_attention_cache_bytes": (_SZ, [_c.POINTER(AttentionLayer)]),
+    "swq_attention_workspace_bytes": (_SZ, [_c.POINTER(AttentionLayer)]),
+    "swq_attention_step": (_I, [_c.POINTER(AttentionLayer), _P, _P, _P, _P, _SZ, _I64, _P, _P, _SZ, _P]),
     "swq_checkpoint_open": (_I, [_c.c_char_p, _c.POINTER(_P)]),
     "swq_checkpoint_close": (None, [_P]),
     "swq_checkpoint_tensor_count": (_I, [_P]),

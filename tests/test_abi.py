@@ -216,3 +216,36 @@ def test_deltanet_validation(lib):
     assert step(L, position=-1) == _lib.SWQ_ERR_INVALID_ARGUMENT
     assert step(L, state=FAKE + 16) == _lib.SWQ_ERR_MISALIGNED
     assert step(L, qkvz=None) == _lib.SWQ_ERR_INVALID_ARGUMENT
+
+
+def test_attention_validation(lib):
+    """swq_attention_step's failure modes, returned before any launch."""
+    from swiftlet_amd._lib import AttentionLayer
+    ok = dict(num_heads=16, num_kv_heads=2, head_dim=256, rotary_dims=64, rope_theta=1e7, norm_eps=1e-6,
+              max_positions=100, reserved=0, q_norm_weight=FAKE, k_norm_weight=FAKE)
+    L = AttentionLayer(**ok)
+    n = lib.swq_attention_cache_bytes(ctypes.byref(L))
+    assert n == 2 * 100 * 2 * 256 * 4
+    w = lib.swq_attention_workspace_bytes(ctypes.byref(L))
+    assert w >= 16 * (256 + 2) * 4
+
+    def step(layer, position=0, cache_bytes=n, ws_bytes=w, cache=FAKE):
+        return lib.swq_attention_step(ctypes.byref(layer), FAKE, FAKE, FAKE, cache, cache_bytes, position, FAKE,
+                                      FAKE, ws_bytes, None)
+
+    for field, value, code in [("num_kv_heads", 3, _lib.SWQ_ERR_BAD_SHAPE),
+                               ("num_heads", 64, _lib.SWQ_ERR_LIMIT),
+                               ("head_dim", 96, _lib.SWQ_ERR_LIMIT),
+                               ("rotary_dims", 63, _lib.SWQ_ERR_BAD_SHAPE),
+                               ("rotary_dims", 512, _lib.SWQ_ERR_BAD_SHAPE),
+                               ("max_positions", 0, _lib.SWQ_ERR_INVALID_ARGUMENT),
+                               ("reserved", 1, _lib.SWQ_ERR_INVALID_ARGUMENT),
+                               ("k_norm_weight", None, _lib.SWQ_ERR_INVALID_ARGUMENT)]:
+        bad = AttentionLayer(**dict(ok, **{field: value}))
+        assert step(bad) == code, field
+        assert lib.swq_attention_cache_bytes(ctypes.byref(bad)) == 0, field
+    assert step(L, position=100) == _lib.SWQ_ERR_LIMIT
+    assert step(L, position=-1) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert step(L, cache_bytes=n - 1) == _lib.SWQ_ERR_WORKSPACE
+    assert step(L, ws_bytes=w - 1) == _lib.SWQ_ERR_WORKSPACE
+    assert step(L, cache=FAKE + 64) == _lib.SWQ_ERR_MISALIGNED
