@@ -77,6 +77,9 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="decode line without the prefill summary")
     ap.add_argument("--no-lmhead", action="store_true", help="decode line without the lm_head + sampling summary")
     ap.add_argument("--no-load", action="store_true", help="decode line without the qpack layer-load rate")
+    ap.add_argument("--no-deltanet", action="store_true", help="decode line without the DeltaNet layer summary")
+    ap.add_argument("--no-attention", action="store_true", help="decode line without the attention layer summary")
+    ap.add_argument("--attention-context", type=int, default=4096, help="cached positions of the attention summary")
     ap.add_argument("--prefill-steps", type=int, default=40, help="prefill chunks timed")
     ap.add_argument("--prefill-replicas", type=int, default=3, help="distinct layers the prefill chunks cycle")
     ap.add_argument("--replicas", type=int, default=48, help="distinct layers cycled through (MALL defeat)")
@@ -327,6 +330,14 @@ def main():
     if not args.no_lmhead and shape_key.startswith("qwen3.6-35b"):
         result["lm_head"] = lmhead_measure(args, torch, lib, shape.hidden)
 
+    # ---- the DeltaNet layer (the layer type of 30 of the 40 layers) ---------
+    if not args.no_deltanet and shape_key.startswith("qwen3.6-35b"):
+        result["deltanet"] = deltanet_measure(args, torch, lib, shape.hidden)
+
+    # ---- the full-attention layer (every 4th layer) -------------------------
+    if not args.no_attention and shape_key.startswith("qwen3.6-35b"):
+        result["attention"] = attention_measure(args, torch, lib, shape.hidden)
+
     # ---- loading: one .qpack layer file into HBM ----------------------------
     if not args.no_load and shape_key.startswith("qwen3.6-35b"):
         result["qpack_load"] = qpack_load_measure(torch, lib, shape)
@@ -341,6 +352,190 @@ def main():
         result["prefill"] = {k: line[k] for k in ("config", "value", "unit", "roofline", "kernel_us", "mfma")}
 
     print(json.dumps(result), flush=True)
+
+
+DN_LAYERS = 30  # qwen3.6-35b: 40 layers, every 4th one full attention
+
+
+def deltanet_measure(args, torch, lib, hidden, tokens=8):
+    """The 35B DeltaNet layer per token (split projections, nk 16, nv 32,
+    dk = dv = 128, conv 4; q4 group-64 projections with fp16 scales): input
+    RMSNorm, in_proj_qkv / z / b / a GEMVs, swq_deltanet_step, out_proj GEMV,
+    residual add + post-attention RMSNorm — a graph over 30 resident layers
+    (537 MB of projections, more than the 256 MB MALL) and 8 tokens; and the
+    step kernel alone from a graph of the same steps."""
+    from swiftlet_amd import _lib, moe
+    from swiftlet_amd._lib import check
+    from swiftlet_amd.deltanet import DeltaNetGPU
+    dev = "cuda"
+    nk, nv, dk, dv, K = 16, 32, 128, 128, 4
+    convD, valD = 2 * nk * dk + nv * dv, nv * dv
+    g = torch.Generator(device="cpu").manual_seed(args.seed)
+    layers = []
+    for r in range(DN_LAYERS):
+        projs = [moe.synth_linear(args.seed, 3000 + 8 * r + j, "router", None, rows, hidden, 4, 64, dev)
+                 for j, rows in enumerate((convD, valD, nv, nv))]
+        out = moe.synth_linear(args.seed, 3000 + 8 * r + 4, "router", None, hidden, valD, 4, 64, dev)
+        blk = DeltaNetGPU(nk, nv, dk, dv, K, _lib.SWQ_DELTA_SPLIT, 1e-6,
+                          torch.randn(convD * K, generator=g) * 0.3, torch.randn(nv, generator=g) * 0.5,
+                          torch.randn(nv, generator=g) * 0.5, 1.0 + 0.1 * torch.randn(dv, generator=g),
+                          projections=projs, out_proj=out, device=dev)
+        layers.append((blk, blk.new_state(), (1.0 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(dev),
+                       (1.0 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(dev)))
+    h = torch.randn((DN_LAYERS, hidden), generator=g).to(dev)
+    x = torch.empty((DN_LAYERS, hidden), dtype=torch.float32, device=dev)
+    qkvz = torch.empty((DN_LAYERS, convD + valD), dtype=torch.float32, device=dev)
+    ba = torch.empty((DN_LAYERS, 2 * nv), dtype=torch.float32, device=dev)
+    y = torch.empty((DN_LAYERS, valD), dtype=torch.float32, device=dev)
+    rr = torch.empty((DN_LAYERS, hidden), dtype=torch.float32, device=dev)
+    x2 = torch.empty((DN_LAYERS, hidden), dtype=torch.float32, device=dev)
+    eps = ctypes.c_float(1e-6)
+
+    def graph_of(step_only):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for t in range(tokens):
+                for r, (blk, st, w_in, w_post) in enumerate(layers):
+                    if not step_only:
+                        check(lib.swq_rmsnorm(h[r].data_ptr(), None, w_in.data_ptr(), _lib.SWQ_BF16, eps, 1, hidden,
+                                              x[r].data_ptr(), _lib.SWQ_F32, cap), "rmsnorm")
+                        for lin, dst, off in ((blk.projections[0], qkvz[r], 0), (blk.projections[1], qkvz[r], convD),
+                                              (blk.projections[2], ba[r], 0), (blk.projections[3], ba[r], nv)):
+                            c = lin.c()
+                            check(lib.swq_encode_gemv(ctypes.byref(c), 0, 0, 0, 0, x[r].data_ptr(), 0,
+                                                      dst.data_ptr(), off, cap), "gemv")
+                    check(lib.swq_deltanet_step(ctypes.byref(blk._c), qkvz[r].data_ptr(), ba[r].data_ptr(),
+                                                st.data_ptr(), st.numel(), t, y[r].data_ptr(), cap), "deltanet")
+                    if not step_only:
+                        c = blk.out_proj.c()
+                        check(lib.swq_encode_gemv(ctypes.byref(c), 0, 0, 0, 0, y[r].data_ptr(), 0,
+                                                  rr[r].data_ptr(), 0, cap), "out_proj")
+                        check(lib.swq_rmsnorm(h[r].data_ptr(), rr[r].data_ptr(), w_post.data_ptr(), _lib.SWQ_BF16,
+                                              eps, 1, hidden, x2[r].data_ptr(), _lib.SWQ_F32, cap), "post norm")
+        return gr
+
+    def timed(gr):
+        gr.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / (tokens * DN_LAYERS)
+
+    qkvz.normal_()
+    ba.normal_()
+    step_us = timed(graph_of(True))
+    layer_us = timed(graph_of(False))
+    step_bytes = (2 * nv * dv * dk + (K - 1) * convD + convD + convD * K + convD + valD + 2 * nv + valD) * 4
+    proj_bytes = sum(lin.matrix_bytes for lin in layers[0][0].projections) + layers[0][0].out_proj.matrix_bytes
+    layer_bytes = proj_bytes + step_bytes + 2 * hidden * 4 * 4
+    gbs = step_bytes / (step_us * 1e-6) / 1e9
+    del layers
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return {"step_us": round(step_us, 3), "step_bytes": int(step_bytes), "step_gbs": round(gbs, 1),
+            "step_frac": round(gbs / HBM_PEAK_GBS, 4), "layer_us": round(layer_us, 3),
+            "layer_bytes": int(layer_bytes),
+            "layer_gbs": round(layer_bytes / (layer_us * 1e-6) / 1e9, 1),
+            "note": "35B DeltaNet layer per token (split layout, q4 projections), graph over 30 resident layers "
+                    "x 8 tokens: norm + 4 GEMVs + swq_deltanet_step + out_proj + residual/post-norm; "
+                    "step_us from a graph of the step alone (state 2 MB read + written per layer)"}
+
+
+ATTN_LAYERS = 10  # qwen3.6-35b: every 4th of 40 layers
+
+
+def attention_measure(args, torch, lib, hidden, reps=8):
+    """The 35B full-attention layer per token at a cache of
+    --attention-context positions (16 query heads over 2 kv heads, hd 256,
+    64 rotary dims; q4 group-64 projections): input RMSNorm, q/k/v_proj
+    GEMVs, swq_attention_step, o_proj GEMV, residual add + post-attention
+    RMSNorm — a graph over 10 resident layers x 8 repetitions of the same
+    position; and the step alone (two launches) from a graph of the steps."""
+    from swiftlet_amd import _lib, moe
+    from swiftlet_amd._lib import check
+    from swiftlet_amd.attention import AttentionGPU
+    dev = "cuda"
+    H, KVH, hd, rot = 16, 2, 256, 64
+    pos = args.attention_context - 1
+    g = torch.Generator(device="cpu").manual_seed(args.seed + 1)
+    layers = []
+    for r in range(ATTN_LAYERS):
+        projs = [moe.synth_linear(args.seed, 4000 + 8 * r + j, "router", None, rows, hidden, 4, 64, dev)
+                 for j, rows in enumerate((H * 2 * hd, KVH * hd, KVH * hd))]
+        o = moe.synth_linear(args.seed, 4000 + 8 * r + 3, "router", None, hidden, H * hd, 4, 64, dev)
+        blk = AttentionGPU(H, KVH, hd, rot, 1e7, 1e-6, pos + 1, 1.0 + 0.1 * torch.randn(hd, generator=g),
+                           1.0 + 0.1 * torch.randn(hd, generator=g), projections=projs, o_proj=o, device=dev)
+        cache = blk.new_cache()
+        ck, cv = blk.cache_views(cache)
+        ck[:pos].normal_(0.0, 0.5)
+        cv[:pos].normal_()
+        layers.append((blk, cache, blk.new_workspace(),
+                       (1.0 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(dev),
+                       (1.0 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(dev)))
+    n = ATTN_LAYERS
+    h = torch.randn((n, hidden), generator=g).to(dev)
+    x = torch.empty((n, hidden), dtype=torch.float32, device=dev)
+    q = torch.randn((n, H * 2 * hd), generator=g).to(dev)
+    kk = torch.randn((n, KVH * hd), generator=g).to(dev)
+    vv = torch.randn((n, KVH * hd), generator=g).to(dev)
+    att = torch.empty((n, H * hd), dtype=torch.float32, device=dev)
+    rr = torch.empty((n, hidden), dtype=torch.float32, device=dev)
+    x2 = torch.empty((n, hidden), dtype=torch.float32, device=dev)
+    eps = ctypes.c_float(1e-6)
+
+    def graph_of(step_only):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for _ in range(reps):
+                for r, (blk, cache, ws, w_in, w_post) in enumerate(layers):
+                    if not step_only:
+                        check(lib.swq_rmsnorm(h[r].data_ptr(), None, w_in.data_ptr(), _lib.SWQ_BF16, eps, 1, hidden,
+                                              x[r].data_ptr(), _lib.SWQ_F32, cap), "rmsnorm")
+                        for lin, dst in zip(blk.projections, (q[r], kk[r], vv[r])):
+                            c = lin.c()
+                            check(lib.swq_encode_gemv(ctypes.byref(c), 0, 0, 0, 0, x[r].data_ptr(), 0,
+                                                      dst.data_ptr(), 0, cap), "gemv")
+                    check(lib.swq_attention_step(ctypes.byref(blk._c), q[r].data_ptr(), kk[r].data_ptr(),
+                                                 vv[r].data_ptr(), cache.data_ptr(), cache.numel(), pos,
+                                                 att[r].data_ptr(), ws.data_ptr(), ws.numel(), cap), "attention")
+                    if not step_only:
+                        c = blk.o_proj.c()
+                        check(lib.swq_encode_gemv(ctypes.byref(c), 0, 0, 0, 0, att[r].data_ptr(), 0,
+                                                  rr[r].data_ptr(), 0, cap), "o_proj")
+                        check(lib.swq_rmsnorm(h[r].data_ptr(), rr[r].data_ptr(), w_post.data_ptr(), _lib.SWQ_BF16,
+                                              eps, 1, hidden, x2[r].data_ptr(), _lib.SWQ_F32, cap), "post norm")
+        return gr
+
+    def timed(gr):
+        gr.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / (reps * n)
+
+    step_us = timed(graph_of(True))
+    layer_us = timed(graph_of(False))
+    # k and v rows of every cached position + the new token's projections and the output
+    step_bytes = 2 * (pos + 1) * KVH * hd * 4 + (H * 2 * hd + 2 * KVH * hd + H * hd) * 4
+    proj_bytes = sum(lin.matrix_bytes for lin in layers[0][0].projections) + layers[0][0].o_proj.matrix_bytes
+    gbs = step_bytes / (step_us * 1e-6) / 1e9
+    del layers
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return {"context": pos + 1, "step_us": round(step_us, 3), "step_bytes": int(step_bytes),
+            "step_gbs": round(gbs, 1), "step_frac": round(gbs / HBM_PEAK_GBS, 4), "layer_us": round(layer_us, 3),
+            "layer_bytes": int(proj_bytes + step_bytes + 4 * hidden * 4),
+            "note": "35B attention layer per token with an f32 KV cache of `context` positions, graph over 10 "
+                    "resident layers x 8: norm + q/k/v GEMVs + swq_attention_step + o_proj + residual/post-norm; "
+                    "step_us from a graph of the step alone"}
 
 
 PCIE_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction

@@ -135,14 +135,18 @@ static int launch_gemv(const swq_qlinear *l, int rows, int64_t w_extra, int64_t 
     const bool x_aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0;
     if (allow_vec && x_aligned && vector_path_ok(l, w_extra, s_extra, b_extra)) {
         QMat m = make_qmat(l, w_extra, s_extra, b_extra);
-        if (plan_fits(m)) {
+        // 4-bit rows of 65..128 chunks (in_dim up to 4096) with fp32 x: two
+        // chunks per lane, a plan only the standalone GEMV compiles
+        const bool q4_wide = m.bits == 4 && m.xf == 0 && m.cpl == 2 && m.chunks <= 2 * kWave;
+        if (plan_fits(m) || q4_wide) {
             const int rows_per_block = (kGemvThreads / kWave) * (4 / m.cpl) * (kWave >> m.lpr_log2);
             const dim3 grid(std::min((rows + rows_per_block - 1) / rows_per_block, kGemvMaxBlocks));
 #define SWQ_GEMV_LAUNCH(B, C, E) \
     hipLaunchKernelGGL((gemv_vec_kernel<B, C, E>), grid, dim3(kGemvThreads), 0, stream, m, rows, x, y)
             const bool f32s = m.stype == SWQ_F32;
             if (m.bits == 4) {
-                if (f32s) SWQ_GEMV_LAUNCH(4, 1, 4); else SWQ_GEMV_LAUNCH(4, 1, 2);
+                if (m.cpl == 1) { if (f32s) SWQ_GEMV_LAUNCH(4, 1, 4); else SWQ_GEMV_LAUNCH(4, 1, 2); }
+                else { if (f32s) SWQ_GEMV_LAUNCH(4, 2, 4); else SWQ_GEMV_LAUNCH(4, 2, 2); }
             } else {
                 if (m.cpl == 1) { if (f32s) SWQ_GEMV_LAUNCH(8, 1, 4); else SWQ_GEMV_LAUNCH(8, 1, 2); }
                 else { if (f32s) SWQ_GEMV_LAUNCH(8, 2, 4); else SWQ_GEMV_LAUNCH(8, 2, 2); }

@@ -34,7 +34,8 @@ def test_gemv_affine_matches_cpu(engine, bits, use_fast):
 @pytest.mark.parametrize("rows,cols,bits,group,stype", [
     (512, 2048, 4, 64, SWQ_F16), (2048, 512, 4, 64, SWQ_F16), (256, 2048, 8, 64, SWQ_F16),
     (2048, 512, 8, 64, SWQ_BF16), (96, 256, 4, 32, SWQ_F32), (33, 128, 8, 128, SWQ_F16),
-    (7, 64, 2, 32, SWQ_F32),
+    (7, 64, 2, 32, SWQ_F32), (2048, 4096, 4, 64, SWQ_F16), (65, 3072, 4, 64, SWQ_BF16),
+    (130, 2112, 4, 64, SWQ_F32),
 ])
 def test_encode_gemv_full_shapes(engine, device, rows, cols, bits, group, stype):
     import torch
