@@ -390,6 +390,12 @@ def deltanet_measure(args, torch, lib, hidden, tokens=8):
     rr = torch.empty((DN_LAYERS, hidden), dtype=torch.float32, device=dev)
     x2 = torch.empty((DN_LAYERS, hidden), dtype=torch.float32, device=dev)
     eps = ctypes.c_float(1e-6)
+    multi = []
+    for r, (blk, _, _, _) in enumerate(layers):
+        lins = (_lib.QLinear * 4)(*[lin.c() for lin in blk.projections])
+        ys = (ctypes.c_void_p * 4)(qkvz[r].data_ptr(), qkvz[r].data_ptr() + 4 * convD, ba[r].data_ptr(),
+                                   ba[r].data_ptr() + 4 * nv)
+        multi.append((lins, ys))
 
     def graph_of(step_only):
         gr = torch.cuda.CUDAGraph()
@@ -397,14 +403,10 @@ def deltanet_measure(args, torch, lib, hidden, tokens=8):
             cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
             for t in range(tokens):
                 for r, (blk, st, w_in, w_post) in enumerate(layers):
-                    if not step_only:
-                        check(lib.swq_rmsnorm(h[r].data_ptr(), None, w_in.data_ptr(), _lib.SWQ_BF16, eps, 1, hidden,
-                                              x[r].data_ptr(), _lib.SWQ_F32, cap), "rmsnorm")
-                        for lin, dst, off in ((blk.projections[0], qkvz[r], 0), (blk.projections[1], qkvz[r], convD),
-                                              (blk.projections[2], ba[r], 0), (blk.projections[3], ba[r], nv)):
-                            c = lin.c()
-                            check(lib.swq_encode_gemv(ctypes.byref(c), 0, 0, 0, 0, x[r].data_ptr(), 0,
-                                                      dst.data_ptr(), off, cap), "gemv")
+                    if not step_only:  # input RMSNorm + the four projections: one launch
+                        lins, ys = multi[r]
+                        check(lib.swq_encode_gemv_multi(lins, 4, ys, h[r].data_ptr(), w_in.data_ptr(), _lib.SWQ_BF16,
+                                                        eps, cap), "norm + projections")
                     check(lib.swq_deltanet_step(ctypes.byref(blk._c), qkvz[r].data_ptr(), ba[r].data_ptr(),
                                                 st.data_ptr(), st.numel(), t, y[r].data_ptr(), cap), "deltanet")
                     if not step_only:
@@ -441,7 +443,8 @@ def deltanet_measure(args, torch, lib, hidden, tokens=8):
             "layer_bytes": int(layer_bytes),
             "layer_gbs": round(layer_bytes / (layer_us * 1e-6) / 1e9, 1),
             "note": "35B DeltaNet layer per token (split layout, q4 projections), graph over 30 resident layers "
-                    "x 8 tokens: norm + 4 GEMVs + swq_deltanet_step + out_proj + residual/post-norm; "
+                    "x 8 tokens: input norm + 4 projections (one launch) + swq_deltanet_step + out_proj + "
+                    "residual/post-norm; "
                     "step_us from a graph of the step alone (state 2 MB read + written per layer)"}
 
 
@@ -486,6 +489,10 @@ def attention_measure(args, torch, lib, hidden, reps=8):
     rr = torch.empty((n, hidden), dtype=torch.float32, device=dev)
     x2 = torch.empty((n, hidden), dtype=torch.float32, device=dev)
     eps = ctypes.c_float(1e-6)
+    multi = []
+    for r, (blk, _, _, _, _) in enumerate(layers):
+        multi.append(((_lib.QLinear * 3)(*[lin.c() for lin in blk.projections]),
+                      (ctypes.c_void_p * 3)(q[r].data_ptr(), kk[r].data_ptr(), vv[r].data_ptr())))
 
     def graph_of(step_only):
         gr = torch.cuda.CUDAGraph()
@@ -493,13 +500,10 @@ def attention_measure(args, torch, lib, hidden, reps=8):
             cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
             for _ in range(reps):
                 for r, (blk, cache, ws, w_in, w_post) in enumerate(layers):
-                    if not step_only:
-                        check(lib.swq_rmsnorm(h[r].data_ptr(), None, w_in.data_ptr(), _lib.SWQ_BF16, eps, 1, hidden,
-                                              x[r].data_ptr(), _lib.SWQ_F32, cap), "rmsnorm")
-                        for lin, dst in zip(blk.projections, (q[r], kk[r], vv[r])):
-                            c = lin.c()
-                            check(lib.swq_encode_gemv(ctypes.byref(c), 0, 0, 0, 0, x[r].data_ptr(), 0,
-                                                      dst.data_ptr(), 0, cap), "gemv")
+                    if not step_only:  # input RMSNorm + q/k/v_proj: one launch
+                        lins, ys = multi[r]
+                        check(lib.swq_encode_gemv_multi(lins, 3, ys, h[r].data_ptr(), w_in.data_ptr(), _lib.SWQ_BF16,
+                                                        eps, cap), "norm + projections")
                     check(lib.swq_attention_step(ctypes.byref(blk._c), q[r].data_ptr(), kk[r].data_ptr(),
                                                  vv[r].data_ptr(), cache.data_ptr(), cache.numel(), pos,
                                                  att[r].data_ptr(), ws.data_ptr(), ws.numel(), cap), "attention")
@@ -534,7 +538,8 @@ def attention_measure(args, torch, lib, hidden, reps=8):
             "step_gbs": round(gbs, 1), "step_frac": round(gbs / HBM_PEAK_GBS, 4), "layer_us": round(layer_us, 3),
             "layer_bytes": int(proj_bytes + step_bytes + 4 * hidden * 4),
             "note": "35B attention layer per token with an f32 KV cache of `context` positions, graph over 10 "
-                    "resident layers x 8: norm + q/k/v GEMVs + swq_attention_step + o_proj + residual/post-norm; "
+                    "resident layers x 8: input norm + q/k/v_proj (one launch) + swq_attention_step + o_proj + "
+                    "residual/post-norm; "
                     "step_us from a graph of the step alone"}
 
 

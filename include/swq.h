@@ -142,6 +142,18 @@ int swq_encode_gemv(const swq_qlinear *lin, int rows,
                     const float *x, int64_t x_off, float *y, int64_t y_off,
                     void *stream);
 
+/* y_i = W_i x for n <= 4 linears that share x and one format (in_dim, bits,
+ * group_size, scales_type), in one launch; ys: host array of n device
+ * pointers.  With norm_weight != NULL the input is first replaced by
+ * rmsnorm(x) * norm_weight (norm_dtype SWQ_F32 / SWQ_F16 / SWQ_BF16, eps)
+ * inside the kernel — the input RMSNorm of a decoder layer fused into its
+ * projections.  x 16 B aligned.  Formats the vectorised GEMV does not take:
+ * SWQ_ERR_LIMIT (call swq_encode_gemv per matrix instead).
+ * Replaces encNormCopy + the projections' encodeGemv calls of one layer
+ * (QwenMetalModel.swift:997-1006, :924-931). */
+int swq_encode_gemv_multi(const swq_qlinear *lins, int n, float *const *ys, const float *x,
+                          const void *norm_weight, int norm_dtype, float norm_eps, void *stream);
+
 /* buf[dst_off + i] = silu(buf[g_off + i]) * buf[u_off + i], i < count.
  * Replaces MetalEngine.encodeSiluMul (MetalEngine.swift:172-187). */
 int swq_encode_silu_mul(float *buf, int count, int64_t g_off, int64_t u_off,

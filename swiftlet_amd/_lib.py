@@ -120,6 +120,7 @@ SIGNATURES = {
     "swq_gemv_quantized": (_I, [_P, _P, _SZ, _P, _SZ, _P, _SZ, _I, _I, _I, _I, _I, _I, _P]),
     "swq_encode_gemv": (_I, [_c.POINTER(QLinear), _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
     "swq_encode_silu_mul": (_I, [_P, _I, _I64, _I64, _I64, _P]),
+    "swq_encode_gemv_multi": (_I, [_c.POINTER(QLinear), _I, _c.POINTER(_P), _P, _P, _I, _c.c_float, _P]),
     "swq_dequantize": (_I, [_c.POINTER(QLinear), _I64, _I64, _P, _P]),
     "swq_rmsnorm": (_I, [_P, _P, _P, _I, _c.c_float, _I, _I, _P, _I, _P]),
     "swq_sample_workspace_bytes": (_SZ, [_I]),

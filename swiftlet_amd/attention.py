@@ -71,16 +71,17 @@ class AttentionGPU:
               "attention_step")
         return out
 
-    def forward_token(self, engine: HipEngine, x, cache, ws, position: int, stream=None):
-        """x [H_model] f32 (input-normed) -> the block's output: q/k/v_proj,
-        step, o_proj."""
+    def forward_token(self, engine: HipEngine, x, cache, ws, position: int, norm_weight=None, eps: float = 1e-6,
+                      stream=None):
+        """x [H_model] f32 -> the block's output: q/k/v_proj in one launch
+        (with norm_weight, x is the un-normalised hidden state and the input
+        RMSNorm runs inside that launch), the step, o_proj."""
         torch = _torch()
         pq, pk, pv = self.projections
         q = torch.empty(pq.out_dim, dtype=torch.float32, device=x.device)
         k = torch.empty(pk.out_dim, dtype=torch.float32, device=x.device)
         v = torch.empty(pv.out_dim, dtype=torch.float32, device=x.device)
-        for lin, y in ((pq, q), (pk, k), (pv, v)):
-            engine.encode_gemv(lin, x, y, stream=stream)
+        engine.encode_gemv_multi([pq, pk, pv], x, [q, k, v], norm_weight=norm_weight, eps=eps, stream=stream)
         att = self.step(q, k, v, cache, ws, position, stream=stream)
         r = torch.empty(self.o_proj.out_dim, dtype=torch.float32, device=x.device)
         engine.encode_gemv(self.o_proj, att, r, stream=stream)

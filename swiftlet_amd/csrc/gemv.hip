@@ -52,6 +52,130 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_vec_kernel(QMat m, int rows
     }
 }
 
+// Several matrices with one input and one lane plan (same in_dim, bits,
+// group, scale dtype) in one launch: their row tiles are numbered
+// consecutively (matrix i owns tiles [tile_end[i-1], tile_end[i])) and the
+// waves walk them as gemv_vec_kernel walks one matrix.  With NORM the input
+// is h and each wave turns its slice into rmsnorm(h) * w in registers: the
+// lanes of row slot 0 hold every chunk of h once, so their squares summed
+// over the wave give sum(h^2); then x = h * (scale * w) (the product order
+// of QwenCPUModel.rmsNorm).
+constexpr int kMultiMax = 4;
+
+struct MultiArgs {
+    QMat m;  // the shared plan (pointers of matrix 0)
+    const uint8_t *w[kMultiMax], *s[kMultiMax], *b[kMultiMax];
+    float *y[kMultiMax];
+    int32_t rows[kMultiMax];
+    int32_t tile_end[kMultiMax];
+    int32_t n;
+    int32_t norm_dtype;
+    const float *x;
+    const void *norm_w;
+    float eps;
+};
+
+template <int BITS, int CPL, int ES, bool NORM>
+__global__ __launch_bounds__(kGemvThreads) void gemv_multi_kernel(const MultiArgs a) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
+    constexpr int kCPC = codes_per_chunk<BITS>();
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const LaneMap lm = lane_map(a.m.lpr_log2, lane);
+    const int tile_rows = RI * lm.rpw;
+    const int ntiles = a.tile_end[a.n - 1];
+    const int nw = gridDim.x * (kGemvThreads / kWave);
+    int t = blockIdx.x * (kGemvThreads / kWave) + wave;
+    if (t >= ntiles) return;
+    auto mat_of = [&](int tt) {
+        int i = 0;
+        while (i + 1 < a.n && tt >= a.tile_end[i]) ++i;
+        return i;
+    };
+    auto qmat = [&](int i) {
+        QMat q = a.m;
+        q.w = a.w[i];
+        q.s = a.s[i];
+        q.b = a.b[i];
+        return q;
+    };
+    auto row0_of = [&](int tt, int i) { return (tt - (i ? a.tile_end[i - 1] : 0)) * tile_rows; };
+    // x and the norm weights first: loads complete in issue order, so the
+    // norm arithmetic below waits for these and not for the weight tiles
+    XSlice<BITS, CPL, kXF32> xs;
+    load_xslice<SWQ_F32>(xs, a.m, lm, a.x, 0);
+    constexpr int kWB = NORM ? kCPC * 4 / 16 : 1;  // 16-byte words of a chunk's norm weights (f32 at most)
+    uint4 wraw[CPL][kWB];
+    if constexpr (NORM) {
+        const int wbytes = a.norm_dtype == SWQ_F32 ? 4 : 2;
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) {
+            const int c = min(lm.j + u * lm.lpr, a.m.chunks - 1);
+            const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const uint8_t *>(a.norm_w) +
+                                                               static_cast<int64_t>(c) * kCPC * wbytes);
+            const int kw = kCPC * wbytes / 16;  // words this chunk's weights fill (the rest repeat the last one)
+#pragma unroll
+            for (int k = 0; k < kWB; ++k) wraw[u][k] = src[min(k, kw - 1)];
+        }
+    }
+    RowTile<BITS, CPL, ES> cur, next, next2;
+    int mc = mat_of(t);
+    load_tile(cur, qmat(mc), 0, lm, row0_of(t, mc), a.rows[mc]);
+    int tn1 = min(t + nw, ntiles - 1), mn1 = mat_of(tn1);
+    load_tile(next, qmat(mn1), 0, lm, row0_of(tn1, mn1), a.rows[mn1]);
+    if constexpr (NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) {
+            if (lm.q == 0 && lm.j + u * lm.lpr < a.m.chunks) {
+#pragma unroll
+                for (int i = 0; i < kCPC; ++i) ss += xs.v[u][i] * xs.v[u][i];
+            }
+        }
+        ss = wave_sum(ss);
+        const float sc = 1.0f / __fsqrt_rn(ss / static_cast<float>(a.m.in) + a.eps);
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) {
+            const uint32_t *wr = reinterpret_cast<const uint32_t *>(wraw[u]);
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < kCPC; ++i) {
+                float wv;
+                if (a.norm_dtype == SWQ_F32) {
+                    wv = __uint_as_float(wr[i]);
+                } else {
+                    const uint16_t raw = static_cast<uint16_t>(wr[i / 2] >> (16 * (i & 1)));
+                    wv = a.norm_dtype == SWQ_BF16 ? bf16_to_f32(raw) : f16_to_f32(raw);
+                }
+                xs.v[u][i] *= sc * wv;
+                sum += xs.v[u][i];
+            }
+            xs.sum[u] = sum;
+        }
+    }
+    for (;;) {
+        const int tn = t + nw;
+        const int tn2 = min(tn + nw, ntiles - 1), mn2 = mat_of(tn2);
+        load_tile(next2, qmat(mn2), 0, lm, row0_of(tn2, mn2), a.rows[mn2]);
+        float res[RI];
+        dot_tile(res, cur, xs, a.m, lm);
+        if (lm.j == lm.lpr - 1) {
+            const int r0 = row0_of(t, mc);
+            float *y = a.y[mc];
+#pragma unroll
+            for (int i = 0; i < RI; ++i) {
+                const int row = r0 + i * lm.rpw + lm.q;
+                if (row < a.rows[mc]) y[row] = res[i];
+            }
+        }
+        if (tn >= ntiles) break;
+        cur = next;
+        next = next2;
+        t = tn;
+        mc = mat_of(t);
+    }
+}
+
 // Scalar-form GEMV for any alignment and bits in {2, 4, 8}: one wave per
 // row, lanes striding over groups, the factored per-group sum of
 // Kernels.metal.txt:56-75 with byte-addressed loads (:27-37).
@@ -167,6 +291,65 @@ static int launch_gemv(const swq_qlinear *l, int rows, int64_t w_extra, int64_t 
 }  // namespace swq
 
 using namespace swq;
+
+extern "C" int swq_encode_gemv_multi(const swq_qlinear *lins, int n, float *const *ys, const float *x,
+                                     const void *norm_weight, int norm_dtype, float norm_eps, void *stream) {
+    if (!lins || !ys || !x || n <= 0) return SWQ_ERR_INVALID_ARGUMENT;
+    if (n > kMultiMax) return SWQ_ERR_LIMIT;
+    if (norm_weight && norm_dtype != SWQ_F32 && norm_dtype != SWQ_F16 && norm_dtype != SWQ_BF16)
+        return SWQ_ERR_UNSUPPORTED_DTYPE;
+    if (norm_weight && !(norm_eps >= 0.f)) return SWQ_ERR_INVALID_ARGUMENT;
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return SWQ_ERR_MISALIGNED;
+    const swq_qlinear &l0 = lins[0];
+    MultiArgs a{};
+    for (int i = 0; i < n; ++i) {
+        const swq_qlinear &l = lins[i];
+        int st = check_linear_shape(&l);
+        if (st != SWQ_OK) return st;
+        if (!ys[i]) return SWQ_ERR_INVALID_ARGUMENT;
+        if (l.in_dim != l0.in_dim || l.bits != l0.bits || l.group_size != l0.group_size ||
+            l.scales_type != l0.scales_type)
+            return SWQ_ERR_BAD_SHAPE;
+        if (!vector_path_ok(&l, 0, 0, 0)) return SWQ_ERR_MISALIGNED;
+        const QMat mi = make_qmat(&l);
+        a.w[i] = mi.w;
+        a.s[i] = mi.s;
+        a.b[i] = mi.b;
+        a.y[i] = ys[i];
+        a.rows[i] = l.out_dim;
+    }
+    a.m = make_qmat(&l0);
+    const bool q4_wide = a.m.bits == 4 && a.m.xf == 0 && a.m.cpl == 2 && a.m.chunks <= 2 * kWave;
+    if (!(plan_fits(a.m) || q4_wide) || a.m.xf != 0) return SWQ_ERR_LIMIT;
+    const int tile_rows = (4 / a.m.cpl) * (kWave >> a.m.lpr_log2);
+    int total = 0;
+    for (int i = 0; i < n; ++i) {
+        total += (a.rows[i] + tile_rows - 1) / tile_rows;
+        a.tile_end[i] = total;
+    }
+    a.n = n;
+    a.x = x;
+    a.norm_w = norm_weight;
+    a.norm_dtype = norm_dtype;
+    a.eps = norm_eps;
+    const dim3 grid(std::min((total + kGemvThreads / kWave - 1) / (kGemvThreads / kWave), kGemvMaxBlocks));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool f32s = a.m.stype == SWQ_F32, norm = norm_weight != nullptr;
+#define SWQ_MULTI(B, C, E)                                                                          \
+    do {                                                                                            \
+        if (norm) hipLaunchKernelGGL((gemv_multi_kernel<B, C, E, true>), grid, dim3(kGemvThreads), 0, s, a); \
+        else hipLaunchKernelGGL((gemv_multi_kernel<B, C, E, false>), grid, dim3(kGemvThreads), 0, s, a);     \
+    } while (0)
+    if (a.m.bits == 4) {
+        if (a.m.cpl == 1) { if (f32s) SWQ_MULTI(4, 1, 4); else SWQ_MULTI(4, 1, 2); }
+        else { if (f32s) SWQ_MULTI(4, 2, 4); else SWQ_MULTI(4, 2, 2); }
+    } else {
+        if (a.m.cpl == 1) { if (f32s) SWQ_MULTI(8, 1, 4); else SWQ_MULTI(8, 1, 2); }
+        else { if (f32s) SWQ_MULTI(8, 2, 4); else SWQ_MULTI(8, 2, 2); }
+    }
+#undef SWQ_MULTI
+    return launch_status();
+}
 
 extern "C" int swq_encode_gemv(const swq_qlinear *lin, int rows, int64_t w_extra, int64_t s_extra,
                                int64_t b_extra, const float *x, int64_t x_off, float *y, int64_t y_off,

@@ -75,23 +75,20 @@ class DeltaNetGPU:
               "deltanet_step")
         return out
 
-    def forward_token(self, engine: HipEngine, x, state, position: int, stream=None):
-        """x [H] f32 (the input-normed hidden state) -> the block's output
-        [H]: projections, step, out_proj."""
+    def forward_token(self, engine: HipEngine, x, state, position: int, norm_weight=None, eps: float = 1e-6,
+                      stream=None):
+        """x [H] f32 -> the block's output [H]: the input projections in one
+        launch (with norm_weight, x is the un-normalised hidden state and the
+        input RMSNorm runs inside that launch), the step, out_proj."""
         torch = _torch()
         dev = x.device
         qkvz = torch.empty(self.conv_dim + self.value_dim, dtype=torch.float32, device=dev)
         ba = torch.empty(2 * self.nv, dtype=torch.float32, device=dev)
         if self.layout == SWQ_DELTA_INTERLEAVED:
-            p_qkvz, p_ba = self.projections
-            engine.encode_gemv(p_qkvz, x, qkvz, stream=stream)
-            engine.encode_gemv(p_ba, x, ba, stream=stream)
+            ys = [qkvz, ba]
         else:
-            p_qkv, p_z, p_b, p_a = self.projections
-            engine.encode_gemv(p_qkv, x, qkvz, stream=stream)
-            engine.encode_gemv(p_z, x, qkvz, y_off=self.conv_dim, stream=stream)
-            engine.encode_gemv(p_b, x, ba, stream=stream)
-            engine.encode_gemv(p_a, x, ba, y_off=self.nv, stream=stream)
+            ys = [qkvz.data_ptr(), qkvz.data_ptr() + 4 * self.conv_dim, ba.data_ptr(), ba.data_ptr() + 4 * self.nv]
+        engine.encode_gemv_multi(list(self.projections), x, ys, norm_weight=norm_weight, eps=eps, stream=stream)
         y = self.step(qkvz, ba, state, position, stream=stream)
         r = torch.empty(self.out_proj.out_dim, dtype=torch.float32, device=dev)
         engine.encode_gemv(self.out_proj, y, r, stream=stream)

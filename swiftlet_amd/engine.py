@@ -131,6 +131,22 @@ class HipEngine:
                                        x.data_ptr(), x_off, y.data_ptr(), y_off,
                                        _stream_handle(stream)), "encode_gemv")
 
+    # encNormCopy + the projections' encodeGemv calls of one layer, one launch.
+    def encode_gemv_multi(self, lins, x, ys, norm_weight=None, eps: float = 1e-6, stream=None):
+        """ys[i] = W_i x (x: f32 device vector; ys: f32 device tensors or raw
+        device addresses); with norm_weight, x is replaced by rmsnorm(x) *
+        norm_weight inside the kernel."""
+        torch = _torch()
+        n = len(lins)
+        arr = (QLinear * n)(*[l.c() for l in lins])
+        ptrs = (ctypes.c_void_p * n)(*[y if isinstance(y, int) else y.data_ptr() for y in ys])
+        wdt, wptr = SWQ_F32, None
+        if norm_weight is not None:
+            wdt = {torch.float32: SWQ_F32, torch.float16: SWQ_F16, torch.bfloat16: SWQ_BF16}[norm_weight.dtype]
+            wptr = norm_weight.data_ptr()
+        check(self.lib.swq_encode_gemv_multi(arr, n, ptrs, x.data_ptr(), wptr, wdt, eps, _stream_handle(stream)),
+              "encode_gemv_multi")
+
     # MetalEngine.encodeSiluMul (MetalEngine.swift:172-187).
     def encode_silu_mul(self, buf, count: int, g_off: int, u_off: int, dst_off: int, stream=None):
         check(self.lib.swq_encode_silu_mul(buf.data_ptr(), count, g_off, u_off, dst_off,

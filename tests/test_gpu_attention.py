@@ -12,7 +12,8 @@ shape (hd 16, 4 heads over 2 kv heads, 4 rotary dims) token by token; the
 at positions 1000 and 5000 over a random cache (several splits, chunks
 above the minimum); and the reference's tiny 4-bit qwen3_next model run
 entirely on the device — embedding rows, every norm, DeltaNet and attention
-block, MoE block and the lm_head — against mlx's logits (2e-3,
+block (input norm fused into the projections' launch), MoE block and the
+lm_head — against mlx's logits (2e-3,
 FixtureForwardTests.swift:94-95) and greedy ids."""
 
 import json
@@ -123,15 +124,16 @@ def test_tiny_q4_model_entirely_on_the_device_matches_mlx():
     interval = cfg["full_attention_interval"]
     for i in range(cfg["num_hidden_layers"]):
         p = f"model.layers.{i}."
-        xin = eng.rms_norm(hd, ck.load(p + "input_layernorm.weight"), eps)
+        w_in = ck.load(p + "input_layernorm.weight")  # the input norm runs inside the projections' launch
         if (i + 1) % interval != 0:
             blk = deltanet_from_checkpoint(ck, i, cfg)
             state = blk.new_state()
-            att = torch.stack([blk.forward_token(eng, xin[t], state, t) for t in range(S)])
+            att = torch.stack([blk.forward_token(eng, hd[t], state, t, norm_weight=w_in, eps=eps) for t in range(S)])
         else:
             blk = attention_from_checkpoint(ck, i, cfg, max_positions=64)
             cache, ws = blk.new_cache(), blk.new_workspace()
-            att = torch.stack([blk.forward_token(eng, xin[t], cache, ws, t) for t in range(S)])
+            att = torch.stack([blk.forward_token(eng, hd[t], cache, ws, t, norm_weight=w_in, eps=eps)
+                               for t in range(S)])
         x2 = eng.rms_norm(hd, ck.load(p + "post_attention_layernorm.weight"), eps, residual=att.contiguous())
         moe_layer_from_checkpoint(ck, i, cfg).decode(x2, out=hd, accumulate=True)
         torch.cuda.synchronize()

@@ -127,3 +127,55 @@ def test_synth_device_matches_host(device):
         assert np.array_equal(lin.w.cpu().numpy().view(np.uint32), w.reshape(-1))
         assert np.array_equal(lin.scales.cpu().numpy().view(np.uint16), s.reshape(-1))
         assert np.array_equal(lin.biases.cpu().numpy().view(np.uint16), b.reshape(-1))
+
+
+def _random_linear(rng, rows, cols, bits, group, stype, device):
+    words = rng.integers(0, 2**32, size=(rows, cols * bits // 32), dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(0.001, 0.02, size=(rows, cols // group)).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, size=(rows, cols // group)).astype(np.float32)
+    if stype == SWQ_F16:
+        s_raw, b_raw = s.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+    elif stype == SWQ_BF16:
+        s_raw, b_raw = R.f32_to_bf16_bits_rne(s), R.f32_to_bf16_bits_rne(b)
+    else:
+        s_raw, b_raw = s, b
+    return GPULinear.from_host(words, s_raw, b_raw, group, bits, stype, device), (words, s_raw, b_raw)
+
+
+@pytest.mark.parametrize("cols,bits,stype,norm", [
+    (2048, 4, SWQ_F16, None), (2048, 4, SWQ_F16, "bf16"), (4096, 4, SWQ_BF16, "f32"), (1024, 8, SWQ_F32, "f16"),
+])
+def test_gemv_multi_matches_separate_calls(engine, device, cols, bits, stype, norm):
+    """swq_encode_gemv_multi: several matrices sharing x in one launch (the
+    projections of a layer), optionally behind the fused input RMSNorm.
+    Without the norm every output equals the separate swq_encode_gemv call
+    bit for bit (the same tiles and sums); with it, within 1e-5 of
+    swq_rmsnorm followed by the separate calls (the sum of squares is taken
+    in another order) and of the oracle's rms_norm + gemv_affine."""
+    import torch
+    from oracle.qwen_tiny import rms_norm
+    rng = np.random.default_rng(cols + bits)
+    rows = [700, 320, 32, 5]
+    lins, host = zip(*[_random_linear(rng, r, cols, bits, 64, stype, device) for r in rows])
+    h = (rng.standard_normal(cols) * 2).astype(np.float32)
+    ht = torch.from_numpy(h).to(device)
+    w = None
+    if norm is not None:
+        wt = (1 + 0.2 * rng.standard_normal(cols)).astype(np.float32)
+        w = torch.from_numpy(wt).to(device).to({"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[norm])
+    ys = [torch.full((r,), -3.0, dtype=torch.float32, device=device) for r in rows]
+    engine.encode_gemv_multi(list(lins), ht, ys, norm_weight=w, eps=1e-6)
+    x_sep = ht if w is None else engine.rms_norm(ht.clone().unsqueeze(0), w, 1e-6)[0]
+    sep = [torch.empty((r,), dtype=torch.float32, device=device) for r in rows]
+    for lin, y in zip(lins, sep):
+        engine.encode_gemv(lin, x_sep, y)
+    torch.cuda.synchronize()
+    x_ref = h if w is None else rms_norm(h, w.float().cpu().numpy(), 1e-6)
+    for i, (y, ys_, (words, s_raw, b_raw)) in enumerate(zip(ys, sep, host)):
+        got, want = y.cpu().numpy(), ys_.cpu().numpy()
+        if w is None:
+            assert np.array_equal(got, want), i
+        else:
+            assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max()), i
+        ref = R.gemv_affine(x_ref, words, s_raw, b_raw, bits, 64, stype)
+        assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max()) + 1e-5, i
