@@ -261,8 +261,34 @@ def main():
     gt.replay()
     b1.record()
     torch.cuda.synchronize()
-    tail_us = b0.elapsed_time(b1) * 1000.0 / K
+    tail_sep_us = b0.elapsed_time(b1) * 1000.0 / K
     del gt
+    # the same tail with the residual add and the norm folded into the MoE
+    # step's launch (swq_moe_decode_norm; batch 1, the single-launch path)
+    tail_us = tail_sep_us
+    tail_folded = False
+    if batch == 1:
+        hs_out = torch.empty_like(hs)
+        fold_calls = [(ctypes.byref(l._c), ctypes.c_void_p(hs[r].data_ptr()), ctypes.c_void_p(rs[r].data_ptr()),
+                       ctypes.c_void_p(wnorm.data_ptr()), _lib.SWQ_BF16, ctypes.c_float(1e-6),
+                       ctypes.c_void_p(hs_out[r].data_ptr()), ctypes.c_void_p(ids[r].data_ptr()),
+                       ctypes.c_void_p(wts[r].data_ptr()), ctypes.c_void_p(wss[r].data_ptr()), wss[r].numel())
+                      for r, l in enumerate(layers)]
+        if lib.swq_moe_decode_norm(*fold_calls[0], sh) == _lib.SWQ_OK:
+            gf = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gf):
+                cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+                for i in range(K):
+                    check(lib.swq_moe_decode_norm(*fold_calls[i % R], cap), "moe_decode_norm (capture)")
+            gf.replay()
+            torch.cuda.synchronize()
+            b0.record()
+            gf.replay()
+            b1.record()
+            torch.cuda.synchronize()
+            tail_us = b0.elapsed_time(b1) * 1000.0 / K
+            tail_folded = True
+            del gf
 
     # unique experts per step (batch > 1 reads each distinct expert once)
     ids_h = ids.cpu().numpy()
@@ -319,6 +345,10 @@ def main():
         "step_gbs_kernels": round(step_bytes / (sum(stage_us) * 1e-6) / 1e9, 1),
         "eager_us_per_step": round(eager_us_per_step, 3),
         "layer_tail_us": round(tail_us, 3),
+        "layer_tail_separate_us": round(tail_sep_us, 3),
+        "layer_tail_note": ("residual add + post-attention RMSNorm + MoE step: one launch (swq_moe_decode_norm); "
+                            "layer_tail_separate_us: swq_rmsnorm then the MoE step" if tail_folded else
+                            "swq_rmsnorm then the MoE step"),
         "unique_experts_per_step": mean_uniq,
     }
 

@@ -432,6 +432,22 @@ int swq_moe_decode(const swq_moe_layer *layer,
                    int32_t *topk_ids, float *topk_weights,
                    void *ws, size_t ws_bytes, int flags, void *stream);
 
+/* The MoE step of one token with the layer's residual add and post-attention
+ * RMSNorm folded into the same launch:
+ *     h1  = h + residual                      (residual may be NULL)
+ *     out = h1 + moe(rmsnorm(h1) * norm_weight)
+ * h, residual, out: [hidden] f32 device vectors; out must not overlap h or
+ * residual (the hidden state alternates between two buffers).  norm_weight:
+ * [hidden] of norm_dtype (SWQ_F32 / SWQ_F16 / SWQ_BF16).  The workspace is
+ * swq_moe_decode's for batch 1.  SWQ_ERR_LIMIT when the layer does not take
+ * the single-launch path (or hidden > 4096): call swq_rmsnorm and
+ * swq_moe_decode instead.  Replaces add_inplace + norm_copy + the MoE
+ * dispatches of one layer (QwenMetalModel.swift:938-951, :798-873), numerics
+ * of QwenCPUModel.layerForward's second half (QwenCPUModel.swift:276-279). */
+int swq_moe_decode_norm(const swq_moe_layer *layer, const float *h, const float *residual,
+                        const void *norm_weight, int norm_dtype, float norm_eps, float *out,
+                        int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes, void *stream);
+
 /* ---- MoE layer prefill ------------------------------------------------ */
 
 /* Workspace bytes swq_moe_prefill needs for `tokens` tokens; 0 on bad input

@@ -152,6 +152,7 @@ SIGNATURES = {
     "swq_moe_decode_workspace_bytes": (_SZ, [_c.POINTER(MoELayer), _I]),
     "swq_moe_workspace_init": (_I, [_P, _SZ, _P]),
     "swq_moe_decode": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _I, _P]),
+    "swq_moe_decode_norm": (_I, [_c.POINTER(MoELayer), _P, _P, _P, _I, _c.c_float, _P, _P, _P, _P, _SZ, _P]),
     "swq_synth_u32": (_I, [_P, _I64, _U64, _U64, _I64, _P]),
     "swq_synth_scales": (_I, [_P, _P, _I64, _I, _U64, _U64, _I64, _P]),
     "swq_moe_decode_stages": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _I, _I, _P]),

@@ -657,6 +657,32 @@ static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtyp
     return SWQ_OK;
 }
 
+extern "C" int swq_moe_decode_norm(const swq_moe_layer *layer, const float *h, const float *residual,
+                                   const void *norm_weight, int norm_dtype, float norm_eps, float *out,
+                                   int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes, void *stream) {
+    int st = check_layer(layer, 1, SWQ_F32);
+    if (st != SWQ_OK) return st;
+    if (!h || !out || !norm_weight) return SWQ_ERR_INVALID_ARGUMENT;
+    if (norm_dtype != SWQ_F32 && norm_dtype != SWQ_F16 && norm_dtype != SWQ_BF16) return SWQ_ERR_UNSUPPORTED_DTYPE;
+    if (!(norm_eps >= 0.f)) return SWQ_ERR_INVALID_ARGUMENT;
+    const int64_t H = layer->hidden;
+    auto overlaps = [H](const float *p, const float *q) { return p && q && p < q + H && q < p + H; };
+    if (overlaps(out, h) || overlaps(out, residual)) return SWQ_ERR_INVALID_ARGUMENT;
+    if (reinterpret_cast<uintptr_t>(h) % 4 != 0 || reinterpret_cast<uintptr_t>(residual) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(out) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(norm_weight) % (norm_dtype == SWQ_F32 ? 4 : 2) != 0)
+        return SWQ_ERR_MISALIGNED;
+    const WsLayout wl = ws_layout(layer, 1);
+    if (!ws || ws_bytes < fused_ws_bytes(layer, wl.total)) return SWQ_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(ws) % 256 != 0) return SWQ_ERR_MISALIGNED;
+    const FusedPrenorm pn{h, residual, norm_weight, norm_dtype, norm_eps};
+    bool taken = false;
+    st = fused_decode(layer, nullptr, SWQ_F32, 1, out, SWQ_F32, topk_ids, topk_weights, ws, ws_bytes, wl.total, false,
+                      static_cast<hipStream_t>(stream), &taken, &pn);
+    if (st != SWQ_OK) return st;
+    return taken ? SWQ_OK : SWQ_ERR_LIMIT;
+}
+
 extern "C" int swq_moe_decode_stages(const swq_moe_layer *layer, const void *x, int x_dtype, int batch,
                                      void *out, int out_dtype, int32_t *topk_ids, float *topk_weights, void *ws,
                                      size_t ws_bytes, int flags, int stage_mask, void *stream) {

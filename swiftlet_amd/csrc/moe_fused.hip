@@ -47,6 +47,7 @@ constexpr int kFusedMaxBlocks = 1024;        // gen[] entries kept in step
 constexpr int kReplicas = 8;                 // logit replicas (one per XCD)
 constexpr int kMaxInterFused = 2048;         // activations a down tile reads
 constexpr int kMaxCombineRows = 64;
+constexpr int kPrenormMaxHidden = 4096;  // hidden size the folded-in norm holds in LDS
 constexpr uint32_t kSpinLimit = 1u << 20;  // polls of ~1 us: about a second
 
 struct FusedArgs {
@@ -70,6 +71,12 @@ struct FusedArgs {
     int32_t dn_tpe, dn_tpe_sh;       // down tiles per routed slot, of the shared expert
     int32_t local;                   // a group's workgroups share an XCD (verified on the host)
     int32_t rows_cmb;                // output rows combined per workgroup
+    // the layer's post-attention norm folded in (the PRENORM kernels):
+    // x = rmsnorm(h_in + res_in) * norm_w, out = (h_in + res_in) + moe(x)
+    const float *h_in, *res_in;
+    const void *norm_w;
+    int32_t norm_dtype;
+    float norm_eps;
 };
 
 // ---------------------------------------------------------------------------
@@ -172,7 +179,7 @@ __device__ __forceinline__ void poll_pairs(uint64_t *src, int n, int seg, int st
 
 // Router rows of tile `tile` -> logits, one copy per replica.
 template <int XDT, int BITS, int CPL, int ES, int XF>
-__device__ __forceinline__ void router_job(const FusedArgs &a, int tile, uint32_t g, int lane) {
+__device__ __forceinline__ void router_job(const FusedArgs &a, const void *x, int tile, uint32_t g, int lane) {
     constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
     const QMat &m = a.router;
     const LaneMap lm = lane_map(m.lpr_log2, lane);
@@ -180,7 +187,7 @@ __device__ __forceinline__ void router_job(const FusedArgs &a, int tile, uint32_
     RowTile<BITS, CPL, ES> rt;
     load_tile(rt, m, 0, lm, row0, a.E);
     XSlice<BITS, CPL, XF> xs;
-    load_xslice<XDT>(xs, m, lm, a.x, 0);
+    load_xslice<XDT>(xs, m, lm, x, 0);
     float res[RI];
     dot_tile(res, rt, xs, m, lm);
     if (lm.j == lm.lpr - 1) {
@@ -197,7 +204,7 @@ __device__ __forceinline__ void router_job(const FusedArgs &a, int tile, uint32_
 
 // Shared-expert gate/up rows of tile `tile` -> silu(g) * u.
 template <int XDT, int BITS, int CPL, int ES, int XF>
-__device__ __forceinline__ void shared_gateup_job(const FusedArgs &a, int tile, uint32_t g, int lane) {
+__device__ __forceinline__ void shared_gateup_job(const FusedArgs &a, const void *x, int tile, uint32_t g, int lane) {
     constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
     const LaneMap lm = lane_map(a.sh_gate.lpr_log2, lane);
     const int row0 = tile * RI * lm.rpw;
@@ -205,7 +212,7 @@ __device__ __forceinline__ void shared_gateup_job(const FusedArgs &a, int tile, 
     load_tile(tg, a.sh_gate, 0, lm, row0, a.Is);
     load_tile(tu, a.sh_up, 0, lm, row0, a.Is);
     XSlice<BITS, CPL, XF> xs;
-    load_xslice<XDT>(xs, a.sh_gate, lm, a.x, 0);
+    load_xslice<XDT>(xs, a.sh_gate, lm, x, 0);
     float rg[RI], ru[RI];
     dot_tile(rg, tg, xs, a.sh_gate, lm);
     dot_tile(ru, tu, xs, a.sh_up, lm);
@@ -220,13 +227,13 @@ __device__ __forceinline__ void shared_gateup_job(const FusedArgs &a, int tile, 
 
 // The shared-expert gate logit <w_sg, x>, returned to every lane.
 template <int XDT, int BITS, int CPL, int ES, int XF>
-__device__ __forceinline__ void seg_job(const FusedArgs &a, int lane, float &sg) {
+__device__ __forceinline__ void seg_job(const FusedArgs &a, const void *x, int lane, float &sg) {
     constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
     const LaneMap lm = lane_map(a.seg.lpr_log2, lane);
     RowTile<BITS, CPL, ES> rt;
     load_tile(rt, a.seg, 0, lm, 0, 1);
     XSlice<BITS, CPL, XF> xs;
-    load_xslice<XDT>(xs, a.seg, lm, a.x, 0);
+    load_xslice<XDT>(xs, a.seg, lm, x, 0);
     float res[RI];
     dot_tile(res, rt, xs, a.seg, lm);
     // row 0 is pass 0, row slot 0: the last lane of the first segment
@@ -413,7 +420,7 @@ constexpr int kShWave = 1, kAuxWave = 7;
 constexpr int kGroupSlots = (SWQ_MAX_TOPK + kGroups - 1) / kGroups;  // routed slots per group
 constexpr int kShBuf = kGroupSlots;                                    // LDS buffer of the shared slot
 
-template <int XDT, int GB, int GC, int GX, int DB>
+template <int XDT, int GB, int GC, int GX, int DB, bool PN>
 __global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
     __shared__ float s_logits[kMaxExperts];
     __shared__ int32_t s_ids[SWQ_MAX_TOPK];
@@ -426,6 +433,8 @@ __global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
     // issued earlier would only compete with the weight stream.
     __shared__ int32_t s_cnt[3];
     __shared__ float s_cmb[(SWQ_MAX_TOPK + 1) * kMaxCombineRows];
+    __shared__ __attribute__((aligned(16))) float s_x[PN ? kPrenormMaxHidden : 4];  // the normalised input
+    __shared__ float s_red[kFusedWaves];
 
     static_assert(sizeof(FusedArgs) > 896 && sizeof(FusedArgs) <= 960, "prefetch_kernargs covers 15 lines");
     prefetch_kernargs();
@@ -442,6 +451,50 @@ __global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
     const bool has_sh_tiles = a.has_shared && b < a.dn_tpe_sh;
     if (threadIdx.x <= kGroupSlots) s_ready[threadIdx.x] = 0;
     if (threadIdx.x < 3) s_cnt[threadIdx.x] = 0;
+    const void *x = a.x;
+    if constexpr (PN) {
+        // the post-attention RMSNorm of the layer, per workgroup into LDS:
+        // s_x = h_in + res_in, then x = s_x * (scale * w) (QwenCPUModel.rmsNorm
+        // and the residual add before it, QwenCPUModel.swift:47-59, :276-277)
+        // one round trip: h, r and the weights of this thread's elements,
+        // loaded unconditionally (indices clamped, values past H masked)
+        constexpr int kPer = kPrenormMaxHidden / kFusedThreads;
+        const bool has_r = a.res_in != nullptr, wf32 = a.norm_dtype == SWQ_F32;
+        const float *rp = has_r ? a.res_in : a.h_in;
+        float hr[kPer], rr[kPer];
+        uint32_t wr[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int ic = min(static_cast<int>(threadIdx.x) + k * kFusedThreads, a.H - 1);
+            hr[k] = a.h_in[ic];
+            rr[k] = rp[ic];
+            wr[k] = wf32 ? static_cast<const uint32_t *>(a.norm_w)[ic] : static_cast<const uint16_t *>(a.norm_w)[ic];
+        }
+        float v[kPer], wv[kPer];
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const bool valid = static_cast<int>(threadIdx.x) + k * kFusedThreads < a.H;
+            v[k] = valid ? (has_r ? hr[k] + rr[k] : hr[k]) : 0.f;
+            wv[k] = wf32 ? __uint_as_float(wr[k])
+                         : (a.norm_dtype == SWQ_BF16 ? bf16_to_f32(static_cast<uint16_t>(wr[k]))
+                                                     : f16_to_f32(static_cast<uint16_t>(wr[k])));
+            ss += v[k] * v[k];
+        }
+        ss = wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int i = 0; i < kFusedWaves; ++i) tot += s_red[i];
+        const float sc = 1.0f / __fsqrt_rn(tot / static_cast<float>(a.H) + a.norm_eps);
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int i = threadIdx.x + k * kFusedThreads;
+            if (i < a.H) s_x[i] = v[k] * (sc * wv[k]);
+        }
+        x = s_x;
+    }
     __syncthreads();
     constexpr int DRI = RowTile<DB, 1, 2>::kRI;
     RowTile<DB, 1, 2> dt0;
@@ -452,12 +505,12 @@ __global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
     if (wave < kAuxWave) {
 #pragma unroll 1
         for (int p = (kAuxWave - 1 - wave) * NB + b; p < a.p1_tiles; p += kAuxWave * NB) {
-            if (p < a.router_tiles) SWQ_DISPATCH2(XDT, a.router, router_job, a, p, g, lane);
-            else SWQ_DISPATCH2(XDT, a.sh_gate, shared_gateup_job, a, p - a.router_tiles, g, lane);
+            if (p < a.router_tiles) SWQ_DISPATCH2(XDT, a.router, router_job, a, x, p, g, lane);
+            else SWQ_DISPATCH2(XDT, a.sh_gate, shared_gateup_job, a, x, p - a.router_tiles, g, lane);
         }
         count_done(&s_cnt[0], lane);
     } else if (a.has_shared) {
-        SWQ_DISPATCH2(XDT, a.seg, seg_job, a, lane, sg);
+        SWQ_DISPATCH2(XDT, a.seg, seg_job, a, x, lane, sg);
     }
 
     // ---- routing ------------------------------------------------------------
@@ -514,7 +567,7 @@ __global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
                 load_tile(tg, a.gate, e, lm, row0, a.I);
                 load_tile(tu, a.up, e, lm, row0, a.I);
                 XSlice<GB, GC, GX> xs;
-                load_xslice<XDT>(xs, a.gate, lm, a.x, 0);
+                load_xslice<XDT>(xs, a.gate, lm, x, 0);
                 float rg[GRI], ru[GRI];
                 dot_tile(rg, tg, xs, a.gate, lm);
                 dot_tile(ru, tu, xs, a.up, lm);
@@ -592,7 +645,14 @@ __global__ __launch_bounds__(kFusedThreads) void moe_fused(FusedArgs a) {
                     static_cast<uint16_t *>(a.out)[row] = f32_to_bf16_rne(acc);
                 } else {
                     float *out = static_cast<float *>(a.out);
-                    out[row] = a.accumulate ? out[row] + acc : acc;
+                    if constexpr (PN) {
+                        // the layer's residual stream: (h + r) + moe (QwenCPUModel.swift:276-279)
+                        float hv = a.h_in[row];
+                        if (a.res_in) hv += a.res_in[row];
+                        out[row] = hv + acc;
+                    } else {
+                        out[row] = a.accumulate ? out[row] + acc : acc;
+                    }
                 }
             }
         }
@@ -638,15 +698,22 @@ inline FusedLayout fused_layout(const swq_moe_layer *l, size_t base) {
 using FusedKernel = void (*)(FusedArgs);
 
 // The instantiation for this layer's formats, or nullptr.
-static FusedKernel fused_kernel_for(const QMat &gate, const QMat &down, int x_dtype) {
+static FusedKernel fused_kernel_for(const QMat &gate, const QMat &down, int x_dtype, bool prenorm) {
+    if (prenorm) {  // x is the f32 normalised input in LDS
+        if (x_dtype != SWQ_F32) return nullptr;
+        if (gate.bits == 4 && gate.xf == 0 && gate.cpl == 1 && down.bits == 4) return moe_fused<SWQ_F32, 4, 1, kXF32, 4, true>;
+        if (gate.bits == 8 && gate.cpl == 2 && down.bits == 8) return moe_fused<SWQ_F32, 8, 2, kXF32, 8, true>;
+        if (gate.bits == 8 && gate.cpl == 1 && down.bits == 8) return moe_fused<SWQ_F32, 8, 1, kXF32, 8, true>;
+        return nullptr;
+    }
     if (x_dtype == SWQ_BF16) {
-        if (gate.bits == 4 && gate.xf == 1 && gate.cpl == 2 && down.bits == 4) return moe_fused<SWQ_BF16, 4, 2, kXBF16, 4>;
-        if (gate.bits == 8 && gate.cpl == 2 && down.bits == 8) return moe_fused<SWQ_BF16, 8, 2, kXF32, 8>;
-        if (gate.bits == 8 && gate.cpl == 1 && down.bits == 8) return moe_fused<SWQ_BF16, 8, 1, kXF32, 8>;
+        if (gate.bits == 4 && gate.xf == 1 && gate.cpl == 2 && down.bits == 4) return moe_fused<SWQ_BF16, 4, 2, kXBF16, 4, false>;
+        if (gate.bits == 8 && gate.cpl == 2 && down.bits == 8) return moe_fused<SWQ_BF16, 8, 2, kXF32, 8, false>;
+        if (gate.bits == 8 && gate.cpl == 1 && down.bits == 8) return moe_fused<SWQ_BF16, 8, 1, kXF32, 8, false>;
     } else {
-        if (gate.bits == 4 && gate.xf == 0 && gate.cpl == 1 && down.bits == 4) return moe_fused<SWQ_F32, 4, 1, kXF32, 4>;
-        if (gate.bits == 8 && gate.cpl == 2 && down.bits == 8) return moe_fused<SWQ_F32, 8, 2, kXF32, 8>;
-        if (gate.bits == 8 && gate.cpl == 1 && down.bits == 8) return moe_fused<SWQ_F32, 8, 1, kXF32, 8>;
+        if (gate.bits == 4 && gate.xf == 0 && gate.cpl == 1 && down.bits == 4) return moe_fused<SWQ_F32, 4, 1, kXF32, 4, false>;
+        if (gate.bits == 8 && gate.cpl == 2 && down.bits == 8) return moe_fused<SWQ_F32, 8, 2, kXF32, 8, false>;
+        if (gate.bits == 8 && gate.cpl == 1 && down.bits == 8) return moe_fused<SWQ_F32, 8, 1, kXF32, 8, false>;
     }
     return nullptr;
 }
@@ -689,7 +756,8 @@ static int fused_blocks(FusedKernel k) {
 
 // The fused launch's arguments for this layer, or no kernel when the layer,
 // the batch or the device does not take the fused path.
-static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch, FusedArgs *fa, int *nb) {
+static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch, bool prenorm, FusedArgs *fa,
+                              int *nb) {
     if (batch != 1) return nullptr;
     const swq_qlinear *mats[8] = {&layer->router, &layer->gate, &layer->up, &layer->down,
                                   &layer->shared_gate, &layer->shared_up, &layer->shared_down,
@@ -719,7 +787,8 @@ static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch
     }
     if (layer->moe_intermediate > kMaxInterFused) return nullptr;
     if (layer->has_shared && layer->shared_intermediate > kMaxInterFused) return nullptr;
-    FusedKernel kern = fused_kernel_for(a.gate, a.down, x_dtype);
+    if (prenorm && layer->hidden > kPrenormMaxHidden) return nullptr;
+    FusedKernel kern = fused_kernel_for(a.gate, a.down, x_dtype, prenorm);
     if (!kern) return nullptr;
     const int blocks = fused_blocks(kern);
     if (blocks <= 0) return nullptr;
@@ -751,11 +820,11 @@ size_t fused_ws_bytes(const swq_moe_layer *l, size_t base) { return fused_layout
 
 int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int batch, void *out, int out_dtype,
                  int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes, size_t staged_bytes,
-                 bool accumulate, hipStream_t stream, bool *taken) {
+                 bool accumulate, hipStream_t stream, bool *taken, const FusedPrenorm *pn) {
     *taken = false;
     FusedArgs a;
     int nb = 0;
-    FusedKernel k = fused_plan(layer, x_dtype, batch, &a, &nb);
+    FusedKernel k = fused_plan(layer, x_dtype, batch, pn != nullptr, &a, &nb);
     if (!k) return SWQ_OK;
     const FusedLayout fl = fused_layout(layer, staged_bytes);
     if (ws_bytes < fl.total) return SWQ_OK;
@@ -773,6 +842,13 @@ int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int bat
     a.rep_stride = fl.rep_stride;
     a.odt = out_dtype;
     a.accumulate = accumulate ? 1 : 0;
+    if (pn) {
+        a.h_in = pn->h;
+        a.res_in = pn->residual;
+        a.norm_w = pn->weight;
+        a.norm_dtype = pn->dtype;
+        a.norm_eps = pn->eps;
+    }
     hipLaunchKernelGGL(k, dim3(nb), dim3(kFusedThreads), 0, stream, a);
     const int st = launch_status();
     if (st != SWQ_OK) return st;

@@ -89,8 +89,16 @@ inline int check_layer(const swq_moe_layer *l, int B, int x_dtype) {
 size_t fused_ws_bytes(const swq_moe_layer *l, size_t base);
 size_t fused_err_offset(const swq_moe_layer *l, size_t base);
 int fused_probe_device(hipStream_t stream);
+// The layer's post-attention norm folded into the single launch:
+// x = rmsnorm(h + residual) * weight, out = (h + residual) + moe(x).
+struct FusedPrenorm {
+    const float *h, *residual;  // residual may be null
+    const void *weight;
+    int dtype;
+    float eps;
+};
 int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int batch, void *out, int out_dtype,
                  int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes, size_t staged_bytes,
-                 bool accumulate, hipStream_t stream, bool *taken);
+                 bool accumulate, hipStream_t stream, bool *taken, const FusedPrenorm *prenorm = nullptr);
 
 }  // namespace swq

@@ -107,6 +107,31 @@ class MoELayerGPU:
             check(self.lib.swq_moe_decode_stages(*args, mask, _stream_handle(stream)), f"moe_decode ({path})")
         return out, topk_ids, topk_weights
 
+    def decode_norm(self, h, norm_weight, eps: float, residual=None, out=None, ws=None, topk_ids=None,
+                    topk_weights=None, stream=None):
+        """One token's MoE step with the residual add and the post-attention
+        RMSNorm in the same launch (swq_moe_decode_norm): h1 = h + residual,
+        out = h1 + moe(rmsnorm(h1) * norm_weight).  h, residual, out: f32
+        [H] device tensors; out must be a different buffer from h and
+        residual.  Returns (out, topk_ids [1, K], topk_weights [1, K])."""
+        torch = _torch()
+        h = h.reshape(-1)
+        if out is None:
+            out = torch.empty(self.hidden, dtype=torch.float32, device=h.device)
+        if ws is None:
+            ws = self.new_workspace(1, stream)
+        if topk_ids is None:
+            topk_ids = torch.empty((1, self.top_k), dtype=torch.int32, device=h.device)
+        if topk_weights is None:
+            topk_weights = torch.empty((1, self.top_k), dtype=torch.float32, device=h.device)
+        wdt = {torch.float32: SWQ_F32, torch.float16: _lib.SWQ_F16, torch.bfloat16: SWQ_BF16}[norm_weight.dtype]
+        check(self.lib.swq_moe_decode_norm(ctypes.byref(self._c), h.data_ptr(),
+                                           residual.data_ptr() if residual is not None else None,
+                                           norm_weight.data_ptr(), wdt, eps, out.data_ptr(), topk_ids.data_ptr(),
+                                           topk_weights.data_ptr(), ws.data_ptr(), ws.numel(),
+                                           _stream_handle(stream)), "moe_decode_norm")
+        return out, topk_ids, topk_weights
+
     # -- prefill -------------------------------------------------------
     def prefill_workspace_bytes(self, tokens: int) -> int:
         n = self.lib.swq_moe_prefill_workspace_bytes(ctypes.byref(self._c), tokens)

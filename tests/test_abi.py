@@ -249,3 +249,22 @@ def test_attention_validation(lib):
     assert step(L, cache_bytes=n - 1) == _lib.SWQ_ERR_WORKSPACE
     assert step(L, ws_bytes=w - 1) == _lib.SWQ_ERR_WORKSPACE
     assert step(L, cache=FAKE + 64) == _lib.SWQ_ERR_MISALIGNED
+
+
+def test_moe_decode_norm_validation(lib):
+    """swq_moe_decode_norm's argument checks (before any launch)."""
+    L = layer()
+    ws_bytes = lib.swq_moe_decode_workspace_bytes(ctypes.byref(L), 1)
+    H = L.hidden
+
+    def call(h=FAKE, res=None, w=FAKE, wdt=_lib.SWQ_BF16, eps=1e-6, out=FAKE + (1 << 20), ws=FAKE, wsb=ws_bytes):
+        return lib.swq_moe_decode_norm(ctypes.byref(L), h, res, w, wdt, eps, out, None, None, ws, wsb, None)
+
+    assert call(h=None) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert call(w=None) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert call(wdt=7) == _lib.SWQ_ERR_UNSUPPORTED_DTYPE
+    assert call(eps=-1.0) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert call(out=FAKE + 4 * (H - 1)) == _lib.SWQ_ERR_INVALID_ARGUMENT  # out overlaps h
+    assert call(res=FAKE + (2 << 20), out=FAKE + (2 << 20) + 8) == _lib.SWQ_ERR_INVALID_ARGUMENT  # out overlaps r
+    assert call(wsb=ws_bytes - 1) == _lib.SWQ_ERR_WORKSPACE
+    assert call(h=FAKE + 2) == _lib.SWQ_ERR_MISALIGNED

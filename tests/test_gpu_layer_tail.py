@@ -116,3 +116,63 @@ def test_tiny_q4_model_with_device_layer_tails_matches_mlx(eng):
     assert diff < 2e-3, diff
     want = json.loads((G / "tiny_forward_q4.json").read_text())["greedy_next_tokens"]
     assert np.argmax(got, axis=-1).tolist() == want
+
+
+@pytest.mark.parametrize("with_residual", [True, False])
+def test_moe_decode_with_folded_norm(eng, with_residual):
+    """swq_moe_decode_norm: the residual add and the post-attention RMSNorm in
+    the MoE step's launch.  out - (h + r) is the MoE output of the
+    normalised input: the oracle's expert ids exactly (the input's top-k
+    margin checked first), the MoE output within the decode bar (1e-3
+    relative L2, fp32 sums in another order), and within 1e-4 of swq_rmsnorm
+    followed by swq_moe_decode (the sum of squares is taken in another
+    order, so x differs in the last bits).  h and r are left as they were."""
+    import torch
+    from swiftlet_amd import moe, synth
+    from tests import helpers
+    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    layer = moe.synth_layer(shape, helpers.SEED, 0, "cuda")
+    ref_layer = helpers.ref_layer(shape, helpers.SEED, 0)
+    rng = np.random.default_rng(31)
+    w16 = (1 + 0.1 * rng.standard_normal(shape.hidden)).astype(np.float32)
+    wt = torch.from_numpy(w16).to(torch.bfloat16).cuda()
+    w_dev = wt.float().cpu().numpy()
+    for trial in range(8):
+        h = (rng.standard_normal(shape.hidden) * 2).astype(np.float32)
+        r = rng.standard_normal(shape.hidden).astype(np.float32) if with_residual else None
+        h1 = (h + r).astype(np.float32) if with_residual else h
+        x = rms_norm(h1[None], w_dev, EPS)
+        if R.router_margin(x, ref_layer)[0] <= 1e-3:
+            continue
+        ref_m, picks, ref_w = R.moe_forward(x, ref_layer)
+        hd = torch.from_numpy(h).cuda()
+        rd = torch.from_numpy(r).cuda() if with_residual else None
+        out, ids, wts = layer.decode_norm(hd, wt, EPS, residual=rd)
+        # the separate launches
+        hs = hd.clone()
+        x_sep = eng.rms_norm(hs, wt, EPS, residual=rd)
+        sep, sep_ids, _ = layer.decode(x_sep, out=hs, accumulate=True)
+        torch.cuda.synchronize()
+        print(f"trial {trial}", flush=True)
+        assert np.array_equal(hd.cpu().numpy(), h)  # inputs untouched
+        assert ids.cpu().numpy()[0].tolist() == [e for e, _ in picks[0]]
+        assert np.allclose(wts.cpu().numpy()[0], ref_w[0], rtol=1e-5, atol=1e-7)
+        got_m = out.cpu().numpy() - h1
+        assert R.rel_l2(got_m[None], ref_m) < 1e-3
+        assert torch.equal(ids, sep_ids)
+        sep_h = sep.cpu().numpy().reshape(-1)
+        assert np.abs(out.cpu().numpy() - sep_h).max() <= 1e-4 * np.abs(sep_h).max()
+
+
+def test_moe_decode_norm_limits(eng):
+    """A layer outside the single launch (f32 scales, the tiny fixture
+    model) returns SWQ_ERR_LIMIT: the caller falls back to the separate
+    launches."""
+    import torch
+    m = TinyQwen(G / "tiny-model-q4")
+    layer = _moe_gpu(m, 0)
+    h = torch.zeros(m.c["hidden_size"], dtype=torch.float32, device="cuda")
+    w = torch.ones(m.c["hidden_size"], dtype=torch.float32, device="cuda")
+    with pytest.raises(_lib.SwqError) as e:
+        layer.decode_norm(h, w, EPS)
+    assert e.value.code == _lib.SWQ_ERR_LIMIT
