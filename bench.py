@@ -79,6 +79,7 @@ def parse():
     ap.add_argument("--no-load", action="store_true", help="decode line without the qpack layer-load rate")
     ap.add_argument("--no-deltanet", action="store_true", help="decode line without the DeltaNet layer summary")
     ap.add_argument("--no-attention", action="store_true", help="decode line without the attention layer summary")
+    ap.add_argument("--no-model", action="store_true", help="decode line without the whole-model token summary")
     ap.add_argument("--attention-context", type=int, default=4096, help="cached positions of the attention summary")
     ap.add_argument("--prefill-steps", type=int, default=40, help="prefill chunks timed")
     ap.add_argument("--prefill-replicas", type=int, default=3, help="distinct layers the prefill chunks cycle")
@@ -360,6 +361,10 @@ def main():
     if not args.no_lmhead and shape_key.startswith("qwen3.6-35b"):
         result["lm_head"] = lmhead_measure(args, torch, lib, shape.hidden)
 
+    # ---- one token through the whole model ---------------------------------
+    if not args.no_model and shape_key == "qwen3.6-35b-a3b-q4" and batch == 1:
+        result["model_decode"] = model_measure(args, torch, lib, shape, layers, wss)
+
     # ---- the DeltaNet layer (the layer type of 30 of the 40 layers) ---------
     if not args.no_deltanet and shape_key.startswith("qwen3.6-35b"):
         result["deltanet"] = deltanet_measure(args, torch, lib, shape.hidden)
@@ -382,6 +387,149 @@ def main():
         result["prefill"] = {k: line[k] for k in ("config", "value", "unit", "roofline", "kernel_us", "mfma")}
 
     print(json.dumps(result), flush=True)
+
+
+MODEL_LAYERS = 40  # qwen3.6-35b: 30 DeltaNet layers, every 4th one full attention
+
+
+def model_measure(args, torch, lib, shape, moe_layers, moe_ws, tokens=4):
+    """One decode token through the whole 35B-shape model, every kernel on
+    the device, as one graph: per layer the input RMSNorm + projections (one
+    launch), the DeltaNet step or the attention step (cache of
+    --attention-context positions), out_proj / o_proj, then the residual add,
+    post-attention RMSNorm and MoE step in one launch (the 40 resident MoE
+    layers of the decode measurement); then the final RMSNorm, the q4
+    lm_head (248,320 rows) and Qwen's default sampling.  Synthetic weights
+    of the real shapes; the hidden state alternates between two buffers."""
+    from swiftlet_amd import _lib, moe
+    from swiftlet_amd._lib import check
+    from swiftlet_amd.attention import AttentionGPU
+    from swiftlet_amd.deltanet import DeltaNetGPU
+    dev = "cuda"
+    H = shape.hidden
+    nk, nv, dk, dv, K = 16, 32, 128, 128, 4
+    convD, valD = 2 * nk * dk + nv * dv, nv * dv
+    AH, AKV, ahd = 16, 2, 256
+    pos = args.attention_context - 1
+    g = torch.Generator(device="cpu").manual_seed(args.seed + 2)
+
+    def bf16_ones():
+        return (1.0 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev)
+
+    blocks = []
+    for i in range(MODEL_LAYERS):
+        seed_base = 5000 + 16 * i
+        if (i + 1) % 4 != 0:
+            projs = [moe.synth_linear(args.seed, seed_base + j, "router", None, rows, H, 4, 64, dev)
+                     for j, rows in enumerate((convD, valD, nv, nv))]
+            out = moe.synth_linear(args.seed, seed_base + 4, "router", None, H, valD, 4, 64, dev)
+            blk = DeltaNetGPU(nk, nv, dk, dv, K, _lib.SWQ_DELTA_SPLIT, 1e-6,
+                              torch.randn(convD * K, generator=g) * 0.3, torch.randn(nv, generator=g) * 0.5,
+                              torch.randn(nv, generator=g) * 0.5, 1.0 + 0.1 * torch.randn(dv, generator=g),
+                              projections=projs, out_proj=out, device=dev)
+            blocks.append(("delta", blk, blk.new_state()))
+        else:
+            projs = [moe.synth_linear(args.seed, seed_base + j, "router", None, rows, H, 4, 64, dev)
+                     for j, rows in enumerate((AH * 2 * ahd, AKV * ahd, AKV * ahd))]
+            o = moe.synth_linear(args.seed, seed_base + 3, "router", None, H, AH * ahd, 4, 64, dev)
+            blk = AttentionGPU(AH, AKV, ahd, 64, 1e7, 1e-6, pos + 1, 1.0 + 0.1 * torch.randn(ahd, generator=g),
+                               1.0 + 0.1 * torch.randn(ahd, generator=g), projections=projs, o_proj=o, device=dev)
+            cache = blk.new_cache()
+            ck, cv = blk.cache_views(cache)
+            ck[:pos].normal_(0.0, 0.5)
+            cv[:pos].normal_()
+            blocks.append(("attn", blk, (cache, blk.new_workspace())))
+    w_in = [bf16_ones() for _ in range(MODEL_LAYERS)]
+    w_post = [bf16_ones() for _ in range(MODEL_LAYERS)]
+    w_final = bf16_ones()
+    head = moe.synth_linear(args.seed, 990, "router", None, LMHEAD_VOCAB, H, 4, 64, dev)
+    hbuf = [torch.randn(H, generator=g).to(dev), torch.empty(H, dtype=torch.float32, device=dev)]
+    proj_out = torch.empty(convD + valD, dtype=torch.float32, device=dev)
+    ba = torch.empty(2 * nv, dtype=torch.float32, device=dev)
+    q = torch.empty(AH * 2 * ahd, dtype=torch.float32, device=dev)
+    kk = torch.empty(AKV * ahd, dtype=torch.float32, device=dev)
+    vv = torch.empty(AKV * ahd, dtype=torch.float32, device=dev)
+    y = torch.empty(max(valD, AH * ahd), dtype=torch.float32, device=dev)
+    r = torch.empty(H, dtype=torch.float32, device=dev)
+    xf = torch.empty(H, dtype=torch.float32, device=dev)
+    logits = torch.empty(LMHEAD_VOCAB, dtype=torch.float32, device=dev)
+    n_ws = lib.swq_sample_workspace_bytes(LMHEAD_VOCAB)
+    sws = torch.zeros(n_ws, dtype=torch.uint8, device=dev)
+    seen = torch.arange(0, 64 * 997, 997, dtype=torch.int32, device=dev) % LMHEAD_VOCAB
+    counts = torch.ones(64, dtype=torch.int32, device=dev)
+    banned = torch.tensor([LMHEAD_VOCAB - 1], dtype=torch.int32, device=dev)
+    tok = torch.empty(1, dtype=torch.int32, device=dev)
+    ids = torch.empty((1, shape.top_k), dtype=torch.int32, device=dev)
+    wts = torch.empty((1, shape.top_k), dtype=torch.float32, device=dev)
+    opt = _lib.SampleOptions(0.7, 20, 0.8, 1.5, 0.5)
+    eps = ctypes.c_float(1e-6)
+    multi = []
+    for kind, blk, _ in blocks:
+        if kind == "delta":
+            ptrs = (proj_out.data_ptr(), proj_out.data_ptr() + 4 * convD, ba.data_ptr(), ba.data_ptr() + 4 * nv)
+        else:
+            ptrs = (q.data_ptr(), kk.data_ptr(), vv.data_ptr())
+        multi.append(((_lib.QLinear * len(ptrs))(*[l.c() for l in blk.projections]), (ctypes.c_void_p * len(ptrs))(*ptrs)))
+    outs_c = [blk.out_proj.c() if kind == "delta" else blk.o_proj.c() for kind, blk, _ in blocks]
+    head_c = head.c()
+    launches = 0
+
+    def token(cap, t):
+        nonlocal launches
+        for i, (kind, blk, st) in enumerate(blocks):
+            hc, hn = hbuf[i % 2], hbuf[(i + 1) % 2]
+            lins, ys = multi[i]
+            check(lib.swq_encode_gemv_multi(lins, len(ys), ys, hc.data_ptr(), w_in[i].data_ptr(), _lib.SWQ_BF16, eps,
+                                            cap), "norm + projections")
+            if kind == "delta":
+                check(lib.swq_deltanet_step(ctypes.byref(blk._c), proj_out.data_ptr(), ba.data_ptr(), st.data_ptr(),
+                                            st.numel(), pos + t, y.data_ptr(), cap), "deltanet")
+                launches += 1
+            else:
+                cache, ws = st
+                check(lib.swq_attention_step(ctypes.byref(blk._c), q.data_ptr(), kk.data_ptr(), vv.data_ptr(),
+                                             cache.data_ptr(), cache.numel(), pos, y.data_ptr(), ws.data_ptr(),
+                                             ws.numel(), cap), "attention")
+                launches += 2
+            check(lib.swq_encode_gemv(ctypes.byref(outs_c[i]), 0, 0, 0, 0, y.data_ptr(), 0, r.data_ptr(), 0, cap),
+                  "out_proj")
+            ml = moe_layers[i]
+            check(lib.swq_moe_decode_norm(ctypes.byref(ml._c), hc.data_ptr(), r.data_ptr(), w_post[i].data_ptr(),
+                                          _lib.SWQ_BF16, eps, hn.data_ptr(), ids.data_ptr(), wts.data_ptr(),
+                                          moe_ws[i].data_ptr(), moe_ws[i].numel(), cap), "moe")
+            launches += 3
+        hc = hbuf[MODEL_LAYERS % 2]
+        check(lib.swq_rmsnorm(hc.data_ptr(), None, w_final.data_ptr(), _lib.SWQ_BF16, eps, 1, H, xf.data_ptr(),
+                              _lib.SWQ_F32, cap), "final norm")
+        check(lib.swq_encode_gemv(ctypes.byref(head_c), 0, 0, 0, 0, xf.data_ptr(), 0, logits.data_ptr(), 0, cap),
+              "lm_head")
+        check(lib.swq_sample(logits.data_ptr(), LMHEAD_VOCAB, ctypes.byref(opt), seen.data_ptr(), counts.data_ptr(),
+                             64, banned.data_ptr(), 1, ctypes.c_float(0.5), tok.data_ptr(), sws.data_ptr(), n_ws, cap),
+              "sample")
+        launches += 4
+
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for t in range(tokens):
+            token(cap, t)
+    gr.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / tokens
+    del gr, blocks, head
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1), "layers": MODEL_LAYERS,
+            "attention_context": pos + 1, "launches_per_token": launches // tokens,
+            "note": "one decode token of the 35B-A3B-shape 4-bit model (30 DeltaNet + 10 attention layers, 40 MoE "
+                    "steps, final norm, 248,320-row lm_head, sampling), all on the device, graph of 4 tokens; "
+                    "synthetic weights; context only: the reference publishes 7-11 tok/s for this model on an "
+                    "M5 Mac (README.md:21), whole decode including its SSD expert streaming"}
 
 
 DN_LAYERS = 30  # qwen3.6-35b: 40 layers, every 4th one full attention
