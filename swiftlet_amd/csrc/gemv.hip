@@ -14,8 +14,8 @@ constexpr int kGemvThreads = 256;
 // Vectorised GEMV over fp32 activations: each wave loads its slice of x once
 // and walks tiles of rows (4/CPL passes of 64/LPR rows) t, t + W, t + 2W, ...
 // (W: the grid's waves), the loads of the next two tiles in flight while the
-// current tile's dot products run.  Prefetches past the end repeat the last
-// tile (clamped, never used), so no load depends on a branch.
+// current tile's dot products run (a wave-uniform branch skips prefetches
+// past the last tile).
 constexpr int kGemvMaxBlocks = 1024;  // 4096 waves: 16 per CU
 
 template <int BITS, int CPL, int ES>
@@ -32,10 +32,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_vec_kernel(QMat m, int rows
     load_xslice<SWQ_F32>(xs, m, lm, x, 0);
     RowTile<BITS, CPL, ES> cur, next, next2;
     load_tile(cur, m, 0, lm, t * tile_rows, rows);
-    load_tile(next, m, 0, lm, min(t + nw, ntiles - 1) * tile_rows, rows);
+    if (t + nw < ntiles) load_tile(next, m, 0, lm, (t + nw) * tile_rows, rows);
     for (;;) {
         const int tn = t + nw;
-        load_tile(next2, m, 0, lm, min(tn + nw, ntiles - 1) * tile_rows, rows);
+        if (tn + nw < ntiles) load_tile(next2, m, 0, lm, (tn + nw) * tile_rows, rows);
         float res[RI];
         dot_tile(res, cur, xs, m, lm);
         if (lm.j == lm.lpr - 1) {
@@ -121,8 +121,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_multi_kernel(const MultiArg
     RowTile<BITS, CPL, ES> cur, next, next2;
     int mc = mat_of(t);
     load_tile(cur, qmat(mc), 0, lm, row0_of(t, mc), a.rows[mc]);
-    int tn1 = min(t + nw, ntiles - 1), mn1 = mat_of(tn1);
-    load_tile(next, qmat(mn1), 0, lm, row0_of(tn1, mn1), a.rows[mn1]);
+    if (t + nw < ntiles) {
+        const int tn1 = t + nw, mn1 = mat_of(tn1);
+        load_tile(next, qmat(mn1), 0, lm, row0_of(tn1, mn1), a.rows[mn1]);
+    }
     if constexpr (NORM) {
         float ss = 0.f;
 #pragma unroll
@@ -155,8 +157,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_multi_kernel(const MultiArg
     }
     for (;;) {
         const int tn = t + nw;
-        const int tn2 = min(tn + nw, ntiles - 1), mn2 = mat_of(tn2);
-        load_tile(next2, qmat(mn2), 0, lm, row0_of(tn2, mn2), a.rows[mn2]);
+        if (tn + nw < ntiles) {
+            const int tn2 = tn + nw, mn2 = mat_of(tn2);
+            load_tile(next2, qmat(mn2), 0, lm, row0_of(tn2, mn2), a.rows[mn2]);
+        }
         float res[RI];
         dot_tile(res, cur, xs, a.m, lm);
         if (lm.j == lm.lpr - 1) {
