@@ -192,7 +192,10 @@ typedef struct {
     float frequency_penalty;  /* >= 0, times the token's count */
 } swq_sample_options;
 
-/* Workspace bytes of swq_sample for `vocab` logits (0: vocab above 524288). */
+/* Workspace bytes of swq_sample for `vocab` logits (0: vocab above 524288).
+ * The workspace must be zero-filled before its first call (it holds the
+ * arrival counter of the call's workgroups); every call leaves it so.  Calls
+ * that run at the same time need workspaces of their own. */
 size_t swq_sample_workspace_bytes(int vocab);
 
 /* One next token from `vocab` f32 logits (device), entirely on the device:

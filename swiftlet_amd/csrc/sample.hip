@@ -1,20 +1,26 @@
 // Next-token sampling on the device: SwiftletSession.sample
-// (SwiftletSession.swift:226-273) over the lm_head logits.
+// (SwiftletSession.swift:226-273) over the lm_head logits, one launch.
 //
-//   1. each workgroup takes a slice of the vocabulary into LDS, applies the
-//      penalties that fall in it (banned tokens -- the suppressed ids, and EOS
-//      while it is banned -- become -inf; every seen token t loses
-//      presence + frequency * count(t); :227-236) and keeps its top-K,
-//      sorted by (logit desc, id asc);
-//   2. one workgroup merges the slices' lists into the global top-K, then:
-//      temperature <= 0: the first maximum (:238-242); else the top-k
-//      candidates (:244-253), p_i = exp((l_i - l_0) / T) (:254), the top-p
-//      cut (:256-265) and the draw r = u * sum, first i with r - sum_{<=i} p
-//      <= 0 (:266-271), u in [0, 1) from the caller (the reference's
-//      Float.random).
+//   1. each workgroup takes a 2048-logit slice of the vocabulary into LDS,
+//      applies the penalties that fall in it (banned tokens -- the suppressed
+//      ids, and EOS while it is banned -- become -inf; every seen token t
+//      loses presence + frequency * count(t); :227-236) and writes its top-K,
+//      sorted by (logit desc, id asc), to the workspace;
+//   2. the last workgroup to finish step 1 (an arrival counter in the
+//      workspace, reset by that workgroup) selects the global top-K from the
+//      slices' lists, then: temperature <= 0: the first maximum (:238-242);
+//      else the top-k candidates (:244-253), p_i = exp((l_i - l_0) / T)
+//      (:254), the top-p cut (:256-265) and the draw r = u * sum, first i
+//      with r - sum_{<=i} p <= 0 (:266-271), u in [0, 1) from the caller (the
+//      reference's Float.random).
 // Selection ties go to the lower token id: the reference's greedy loop keeps
 // the first maximum and its candidate scan replaces only on a strictly
 // larger logit.
+//
+// Selection without sequential rounds: a lower bound t of the K-th largest
+// value (each wave's K-th largest lane value by rank, the largest of those),
+// every value >= t compacted into LDS (at least K of them), each one's rank
+// among those counted in parallel, rank < K placed at its position.
 #include "internal.hpp"
 #include "route.hpp"
 
@@ -22,185 +28,252 @@ namespace swq {
 namespace {
 
 constexpr int kSampleThreads = 256;
+constexpr int kSampleWaves = kSampleThreads / kWave;
 constexpr int kSampleMaxK = 64;
-constexpr int kSampleSlices = 256;  // workgroups of step 2
-constexpr int kPerThread = 8;       // logits per thread of step 2 (slice = 2048)
+constexpr int kSampleSlices = 256;  // workgroups (vocabulary slices) at most
+constexpr int kPerThread = 8;       // logits per thread (slice = 2048)
+constexpr int kSlice = kSampleThreads * kPerThread;
+// candidates held in LDS: a slice has at most 8 keys from each of a wave's K
+// best lanes (4 * 8 * 64 = 2048); the last step at most K entries from each
+// of the K lists whose heads are the K largest (64 * 64)
+constexpr int kCandCap = kSampleMaxK * kSampleMaxK;
 
-// (logit, id) as one key: larger logit first, then lower id.
+// (logit, id) as one key: larger logit first, then lower id.  Never 0 for a
+// token (the id part is nonzero), so 0 marks "none".
 __device__ __forceinline__ uint64_t cand_key(float l, int id) {
     return (static_cast<uint64_t>(orderable(l)) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(id));
 }
 __device__ __forceinline__ int key_id(uint64_t k) { return static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(k)); }
 __device__ __forceinline__ float key_logit(uint64_t k) { return from_orderable(static_cast<uint32_t>(k >> 32)); }
 
-// The largest key of the wave (every lane receives it): the largest logit
-// bits, then the largest id bits among the lanes holding them; DPP and
-// scalar maxima only.
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
-    const uint32_t hi = static_cast<uint32_t>(k >> 32), lo = static_cast<uint32_t>(k);
-    const uint32_t mh = wave_max_u32(hi);
-    const uint32_t ml = wave_max_u32(hi == mh ? lo : 0u);
-    return (static_cast<uint64_t>(mh) << 32) | ml;
-}
-
 struct SampleArgs {
     const float *logits;
-    uint64_t *cand;            // [kSampleSlices][kSampleMaxK]
+    uint64_t *cand;            // [kSampleSlices][kSampleMaxK] each slice's sorted top-k (0: none)
+    uint32_t *arrived;         // slices done with this call (the last one resets it)
     const int32_t *seen_ids, *seen_counts, *banned_ids;
     int32_t *out;
     int32_t vocab, n_seen, n_banned, k, slices, slice;
     float temperature, top_p, presence, frequency, u;
 };
 
+struct SampleLds {
+    uint64_t big[kCandCap];      // the slice's logits (as floats), then candidates
+    uint64_t vals[kSampleThreads];
+    uint64_t tau[kSampleWaves];
+    uint64_t top[kSampleMaxK];
+    uint64_t kth;
+    uint32_t count[3];
+    uint32_t last;
+};
+
+// A lower bound of the k-th largest of the workgroup's values v (one per
+// thread, 0 = none, nonzero values distinct): each wave's k-th largest by
+// rank (0 if the wave holds fewer than k nonzero values), the largest of
+// those.  At least min(k, nonzero count) values are >= it, and every value
+// among the k largest is.
+__device__ uint64_t kth_lower_bound(uint64_t v, int k, SampleLds &L) {
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    L.vals[tid] = v;
+    if (lane == 0) L.tau[wave] = 0ull;
+    __syncthreads();
+    const uint64_t *w = L.vals + wave * kWave;
+    int rank = 0;
+#pragma unroll 16
+    for (int j = 0; j < kWave; ++j) rank += w[j] > v;
+    if (rank == k - 1 && v != 0ull) L.tau[wave] = v;
+    __syncthreads();
+    uint64_t t = L.tau[0];
+#pragma unroll
+    for (int i = 1; i < kSampleWaves; ++i) t = L.tau[i] > t ? L.tau[i] : t;
+    return t;
+}
+
+// Rank of x among the n distinct candidates in LDS: the number larger.
+__device__ __forceinline__ int rank_of(uint64_t x, const uint64_t *c, int n) {
+    int r = 0;
+#pragma unroll 8
+    for (int j = 0; j < n; ++j) r += c[j] > x;
+    return r;
+}
+
+// The draw on wave 0 (lane i holds candidate i), in the reference's order of
+// float32 operations: sums left to right, no fused multiply-adds.
+__device__ void sample_draw(const SampleArgs &a, const uint64_t *top) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x;
+    const uint64_t key = lane < a.k ? top[lane] : 0ull;
+    int pick = key_id(top[0]);
+    if (a.temperature > 0.f) {
+        // candidates with a logit (fewer than k only if the vocabulary is): a prefix
+        int n = __popcll(__ballot(key != 0ull));
+        const float l0 = key_logit(top[0]);
+        const float p = lane < n ? expf((key_logit(key) - l0) / a.temperature) : 0.f;
+        auto at = [](float v, int i) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i)); };
+        float sum = 0.f;
+        for (int i = 0; i < n; ++i) sum += at(p, i);
+        if (a.top_p < 1.f) {
+            const float q = p / sum;
+            float cum = 0.f;
+            int cut = n;
+            for (int i = 0; i < n; ++i) {
+                cum += at(q, i);
+                if (cum >= a.top_p) {
+                    cut = i + 1;
+                    break;
+                }
+            }
+            n = cut;
+            sum = 0.f;
+            for (int i = 0; i < n; ++i) sum += at(p, i);
+        }
+        float r = a.u * sum;
+        for (int i = 0; i < n; ++i) {
+            r -= at(p, i);
+            if (r <= 0.f) {
+                pick = key_id(top[i]);
+                break;
+            }
+        }
+    }
+    if (lane == 0) *a.out = pick;
+}
+
+// step 2 (the last slice's workgroup): the global top-k from the slices'
+// sorted lists, then the draw.
+__device__ void sample_final(const SampleArgs &a, SampleLds &L) {
+    const int tid = threadIdx.x;
+    // list tid's first 8 entries (its head first) in one round of loads
+    const uint64_t *list = a.cand + min(tid, a.slices - 1) * kSampleMaxK;
+    uint64_t e[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) e[q] = list[min(q, a.k - 1)];
+    const uint64_t h = tid < a.slices ? e[0] : 0ull;
+    const uint64_t lb = kth_lower_bound(h, a.k, L);
+    // the exact k-th largest head: heads >= lb (the k largest among them) ranked
+    const bool near = h != 0ull && h >= lb;
+    if (near) L.vals[atomicAdd(&L.count[1], 1u)] = h;  // vals is free again
+    __syncthreads();
+    if (near && rank_of(h, L.vals, static_cast<int>(L.count[1])) == a.k - 1) L.kth = h;
+    __syncthreads();
+    const uint64_t kth = L.kth;  // 0 if fewer than k lists hold a token
+    // candidates: the entries >= kth of the (at most k) lists whose head is
+    // >= kth -- sorted lists, so a prefix, 8 entries at a time
+    if (h != 0ull && h >= kth) {
+        for (int r0 = 0; r0 < a.k; r0 += 8) {
+            if (r0 > 0) {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) e[q] = list[min(r0 + q, a.k - 1)];
+            }
+            int c = 0;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) c += r0 + q < a.k && e[q] != 0ull && e[q] >= kth;
+            const uint32_t off = atomicAdd(&L.count[2], static_cast<uint32_t>(c));
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (q < c && off + q < static_cast<uint32_t>(kCandCap)) L.big[off + q] = e[q];
+            if (c < 8) break;
+        }
+    }
+    __syncthreads();
+    const int n = min(static_cast<int>(L.count[2]), kCandCap);  // <= k * k by the bound above
+    for (int i = tid; i < n; i += kSampleThreads) {
+        const uint64_t x = L.big[i];
+        const int r = rank_of(x, L.big, n);
+        if (r < a.k) L.top[r] = x;
+    }
+    for (int i = n + tid; i < a.k; i += kSampleThreads) L.top[i] = 0ull;
+    __syncthreads();
+    if (tid < kWave) sample_draw(a, L.top);
+}
+
 // step 1: the slice's penalised logits in LDS, its top-k, sorted, into
-// cand[slice][0..k) (missing: 0).  Each wave takes the top-k of its 512
-// logits by k rounds of wave maxima (each lane's 8 keys sorted, the winner
-// pops its head), then wave 0 merges the four sorted lists the same way.
+// cand[slice][0..k) (missing: 0); the last slice to finish runs step 2.
 __global__ __launch_bounds__(kSampleThreads) void sample_slices(const SampleArgs a) {
-    __shared__ float s_l[kSampleThreads * kPerThread];
-    __shared__ uint64_t s_top[kSampleThreads / kWave][kSampleMaxK];
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int v0 = blockIdx.x * a.slice;
-    for (int i = threadIdx.x; i < a.slice; i += kSampleThreads) s_l[i] = a.logits[min(v0 + i, a.vocab - 1)];
+#pragma clang fp contract(off)
+    __shared__ SampleLds L;
+    static_assert(kCandCap * 8 >= kSlice * 4, "the slice's logits fit the candidate buffer");
+    float *s_l = reinterpret_cast<float *>(L.big);
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int v0 = blockIdx.x * kSlice;
+    if (tid == 0) {
+        L.count[0] = L.count[1] = L.count[2] = 0u;
+        L.kth = 0ull;
+    }
+    // the slice's logits and the first entries of the penalty lists, all
+    // loads in flight together (clamped indices, no guarded loads)
+    float lv[kPerThread];
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) lv[j] = a.logits[min(v0 + j * kSampleThreads + tid, a.vocab - 1)];
+    int seen0 = 0, count0 = 0, banned0 = 0;
+    if (a.n_seen > 0) {
+        seen0 = a.seen_ids[min(tid, a.n_seen - 1)];
+        count0 = a.seen_counts[min(tid, a.n_seen - 1)];
+    }
+    if (a.n_banned > 0) banned0 = a.banned_ids[min(tid, a.n_banned - 1)];
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) s_l[j * kSampleThreads + tid] = lv[j];
     __syncthreads();
     // penalties inside the slice: the seen tokens, then the banned ones
-    const float pen = a.presence;
-    for (int i = threadIdx.x; i < a.n_seen; i += kSampleThreads) {
-        const int t = a.seen_ids[i] - v0;
-        if (t >= 0 && t < a.slice) atomicAdd(&s_l[t], -(pen + a.frequency * static_cast<float>(a.seen_counts[i])));
+    for (int i = tid; i < a.n_seen; i += kSampleThreads) {
+        const int t = (i == tid ? seen0 : a.seen_ids[i]) - v0;
+        const int c = i == tid ? count0 : a.seen_counts[i];
+        if (t >= 0 && t < kSlice) atomicAdd(&s_l[t], -(a.presence + a.frequency * static_cast<float>(c)));
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < a.n_banned; i += kSampleThreads) {
-        const int t = a.banned_ids[i] - v0;
-        if (t >= 0 && t < a.slice) s_l[t] = -INFINITY;
+    for (int i = tid; i < a.n_banned; i += kSampleThreads) {
+        const int t = (i == tid ? banned0 : a.banned_ids[i]) - v0;
+        if (t >= 0 && t < kSlice) s_l[t] = -INFINITY;
     }
     __syncthreads();
+    // each thread's 8 keys and their maximum
     uint64_t key[kPerThread];
+    uint64_t head = 0ull;
 #pragma unroll
     for (int j = 0; j < kPerThread; ++j) {
         const int i = wave * (kPerThread * kWave) + j * kWave + lane;
         key[j] = v0 + i < a.vocab ? cand_key(s_l[i], v0 + i) : 0ull;
+        head = key[j] > head ? key[j] : head;
     }
+    // the slice's top-k: every key >= a lower bound of the k-th largest
+    // head, ranked (logits in LDS are dead: the bound's barriers follow
+    // their last read)
+    const uint64_t lb = kth_lower_bound(head, a.k, L);
+    int c = 0;
 #pragma unroll
-    for (int i = 0; i < kPerThread; ++i)
+    for (int j = 0; j < kPerThread; ++j) c += key[j] != 0ull && key[j] >= lb;
+    if (c > 0) {
+        uint32_t off = atomicAdd(&L.count[0], static_cast<uint32_t>(c));
 #pragma unroll
-        for (int j = 0; j + 1 < kPerThread - i; ++j) {
-            const uint64_t x = key[j], y = key[j + 1];
-            key[j] = x > y ? x : y;
-            key[j + 1] = x > y ? y : x;
-        }
-    for (int r = 0; r < a.k; ++r) {
-        const uint64_t m = wave_max_key(key[0]);
-        if (lane == 0) s_top[wave][r] = m;
-        if (m != 0ull && key[0] == m) {  // keys are unique (ids differ): one winner pops
-#pragma unroll
-            for (int j = 0; j + 1 < kPerThread; ++j) key[j] = key[j + 1];
-            key[kPerThread - 1] = 0ull;
-        }
+        for (int j = 0; j < kPerThread; ++j)
+            if (key[j] != 0ull && key[j] >= lb) L.big[off++] = key[j];
     }
     __syncthreads();
-    if (wave != 0) return;
-    // lanes 0..3 walk the four waves' lists
-    int pos = 0;
-    const bool has = lane < kSampleThreads / kWave;
-    uint64_t head = has ? s_top[lane][0] : 0ull;
-    for (int r = 0; r < a.k; ++r) {
-        const uint64_t m = wave_max_key(head);
-        if (lane == 0) a.cand[blockIdx.x * kSampleMaxK + r] = m;
-        if (has && m != 0ull && head == m) {
-            ++pos;
-            head = pos < a.k ? s_top[lane][pos] : 0ull;
-        }
+    const int n = static_cast<int>(L.count[0]);
+    for (int i = tid; i < n; i += kSampleThreads) {
+        const uint64_t x = L.big[i];
+        const int r = rank_of(x, L.big, n);
+        if (r < a.k) L.top[r] = x;
     }
-}
-
-// step 2 (one workgroup): merge and draw.  The slices' lists come into LDS
-// first; wave 0 merges them: lane l walks the lists of slices l, l + 64,
-// l + 128, l + 192 (slices <= 256), its best head competes in each round.
-constexpr int kMergeK = 24;  // list entries held in LDS per slice (k <= 24)
-
-__global__ __launch_bounds__(kSampleThreads) void sample_final(const SampleArgs a) {
-    __shared__ uint64_t s_lists[kSampleSlices * kMergeK];
-    __shared__ uint64_t s_top[kSampleMaxK];
-    __shared__ float probs[kSampleMaxK];  // the draw's weights (LDS: no private memory)
-    constexpr int LPL = kSampleSlices / kWave;  // lists per lane
-    const int lane = threadIdx.x & (kWave - 1);
-    const bool in_lds = a.k <= kMergeK;
-    if (in_lds) {
-        for (int i = threadIdx.x; i < a.slices * a.k; i += kSampleThreads) {
-            const int sl = i / a.k, r = i - sl * a.k;
-            s_lists[sl * kMergeK + r] = a.cand[sl * kSampleMaxK + r];
-        }
-        __syncthreads();
-    }
-    auto entry = [&](int sl, int r) {
-        return in_lds ? s_lists[sl * kMergeK + r] : a.cand[sl * kSampleMaxK + r];
-    };
-    if (threadIdx.x < kWave) {
-        int pos[LPL];
-        uint64_t head[LPL];
-#pragma unroll
-        for (int q = 0; q < LPL; ++q) {
-            const int sl = lane + q * kWave;
-            pos[q] = 0;
-            head[q] = sl < a.slices ? entry(sl, 0) : 0ull;
-        }
-        for (int r = 0; r < a.k; ++r) {
-            uint64_t best = head[0];
-#pragma unroll
-            for (int q = 1; q < LPL; ++q) best = head[q] > best ? head[q] : best;
-            const uint64_t m = wave_max_key(best);
-            if (lane == 0) s_top[r] = m;
-#pragma unroll
-            for (int q = 0; q < LPL; ++q) {
-                if (m != 0ull && head[q] == m) {
-                    ++pos[q];
-                    head[q] = pos[q] < a.k ? entry(lane + q * kWave, pos[q]) : 0ull;
-                }
-            }
-        }
+    for (int i = n + tid; i < a.k; i += kSampleThreads) L.top[i] = 0ull;
+    __syncthreads();
+    // The list goes out from wave 0, the wave whose thread 0 then counts the
+    // arrival: that agent-scope release waits for the wave's stores and
+    // writes them back past this XCD's L2; the last arrival's acquire (and
+    // the acquire fence every thread of that workgroup passes) makes every
+    // slice's list visible on whichever XCD that slice ran.
+    if (tid < a.k) a.cand[blockIdx.x * kSampleMaxK + tid] = L.top[tid];
+    if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(a.arrived, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        L.last = prev == static_cast<uint32_t>(a.slices - 1);
+        if (L.last) __hip_atomic_store(a.arrived, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int pick = key_id(s_top[0]);
-        if (a.temperature > 0.f) {
-            // candidates with a logit (fewer than k only if the vocabulary is)
-            int n = 0;
-            while (n < a.k && s_top[n] != 0ull) ++n;
-            const float l0 = key_logit(s_top[0]);
-            float sum = 0.f;
-            for (int i = 0; i < n; ++i) {
-                probs[i] = expf((key_logit(s_top[i]) - l0) / a.temperature);
-                sum += probs[i];
-            }
-            if (a.top_p < 1.f) {
-                float cum = 0.f;
-                int cut = n;
-                for (int i = 0; i < n; ++i) {
-                    cum += probs[i] / sum;
-                    if (cum >= a.top_p) {
-                        cut = i + 1;
-                        break;
-                    }
-                }
-                n = cut;
-                sum = 0.f;
-                for (int i = 0; i < n; ++i) sum += probs[i];
-            }
-            float r = a.u * sum;
-            for (int i = 0; i < n; ++i) {
-                r -= probs[i];
-                if (r <= 0.f) {
-                    pick = key_id(s_top[i]);
-                    break;
-                }
-            }
-        }
-        *a.out = pick;
-    }
+    if (!L.last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    sample_final(a, L);
 }
 
-size_t sample_ws_bytes() { return static_cast<size_t>(kSampleSlices) * kSampleMaxK * 8; }
+size_t sample_ws_bytes() { return static_cast<size_t>(kSampleSlices) * kSampleMaxK * 8 + 256; }
 
 }  // namespace
 }  // namespace swq
@@ -231,6 +304,7 @@ extern "C" int swq_sample(const float *logits, int vocab, const swq_sample_optio
     uint8_t *w = static_cast<uint8_t *>(ws);
     a.logits = logits;
     a.cand = reinterpret_cast<uint64_t *>(w);
+    a.arrived = reinterpret_cast<uint32_t *>(w + static_cast<size_t>(kSampleSlices) * kSampleMaxK * 8);
     a.seen_ids = seen_ids;
     a.seen_counts = seen_counts;
     a.banned_ids = banned_ids;
@@ -248,6 +322,5 @@ extern "C" int swq_sample(const float *logits, int vocab, const swq_sample_optio
     a.u = u;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(sample_slices, dim3(a.slices), dim3(kSampleThreads), 0, s, a);
-    hipLaunchKernelGGL(sample_final, dim3(1), dim3(kSampleThreads), 0, s, a);
     return launch_status();
 }
