@@ -147,8 +147,9 @@ int swq_encode_gemv(const swq_qlinear *lin, int rows,
  * pointers.  With norm_weight != NULL the input is first replaced by
  * rmsnorm(x) * norm_weight (norm_dtype SWQ_F32 / SWQ_F16 / SWQ_BF16, eps)
  * inside the kernel — the input RMSNorm of a decoder layer fused into its
- * projections.  x 16 B aligned.  Formats the vectorised GEMV does not take:
- * SWQ_ERR_LIMIT (call swq_encode_gemv per matrix instead).
+ * projections.  x and norm_weight 16 B aligned.  Formats the vectorised
+ * GEMV does not take, or in_dim above 4096: SWQ_ERR_LIMIT (call
+ * swq_encode_gemv per matrix instead).
  * Replaces encNormCopy + the projections' encodeGemv calls of one layer
  * (QwenMetalModel.swift:997-1006, :924-931). */
 int swq_encode_gemv_multi(const swq_qlinear *lins, int n, float *const *ys, const float *x,

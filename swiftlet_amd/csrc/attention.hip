@@ -44,10 +44,6 @@ struct AttnArgs {
 
 __device__ __forceinline__ float sigmoid_acc(float v) { return 1.0f / (1.0f + expf(-v)); }
 
-// Workgroup barrier for LDS traffic only: each wave's LDS operations
-// complete, then s_barrier.  Global loads stay in flight across it (a full
-// __syncthreads would wait for them too).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Element e of a head vector held EPL per lane (lanes >= HD / EPL hold none).
 template <int HD>

@@ -136,6 +136,11 @@ __device__ __forceinline__ float segment_sum(float v, int width) {
 
 __device__ __forceinline__ float wave_sum(float v) { return segment_sum(v, kWave); }
 
+// Workgroup barrier for LDS traffic only: each wave's LDS operations
+// complete, then s_barrier.  Global loads stay in flight across it (a full
+// __syncthreads would wait for them too).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
     return v;

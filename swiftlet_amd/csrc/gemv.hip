@@ -18,6 +18,131 @@ constexpr int kGemvThreads = 256;
 // past the last tile).
 constexpr int kGemvMaxBlocks = 1024;  // 4096 waves: 16 per CU
 
+// x (at most kStageMaxIn floats) goes through LDS once per workgroup: each
+// thread loads a few 16-byte words of it (and, with NORM, the matching norm
+// weights), the RMSNorm's sum of squares is one workgroup reduction, each
+// thread normalises its own words (x * (scale * w), the product order of
+// QwenCPUModel.rmsNorm), and the waves read their slices from LDS instead
+// of each reading all of x (and the weights) from L2: with a wave per 4-row
+// tile they would otherwise read them ~4 times as often as the workgroup.
+// In LDS, chunk c's 16-byte pieces are rotated by c (piece p at slot
+// (p + c) mod P) so the lanes of a wave, which read one chunk each, spread
+// over the banks.  `issue` runs between the loads of x and the first wait
+// for them: the caller's weight-tile loads go there, since loads complete
+// in issue order.  Every thread of the workgroup must call this.
+constexpr int kStageMaxIn = 4096;
+constexpr int kStageWords = kStageMaxIn / 4 / kGemvThreads;  // 16-byte words of x per thread
+
+struct StagedX {
+    uint4 x[kStageMaxIn / 4];
+    float red[kGemvThreads / kWave];
+};
+
+template <int BITS, bool NORM, typename Issue>
+__device__ __forceinline__ void stage_x(StagedX &L, const float *x, int in, const void *norm_w, int norm_dtype,
+                                        float eps, Issue issue) {
+    constexpr int kP = codes_per_chunk<BITS>() / 4;  // 16-byte words of x per chunk
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int nx = in / 4;
+    const uint4 *x4 = reinterpret_cast<const uint4 *>(x);
+    uint4 xw[kStageWords], ww[NORM ? kStageWords : 1];
+    // every load unconditional (indices clamped; the repeats hit lines
+    // already requested): branches around them measured slower
+#pragma unroll
+    for (int k = 0; k < kStageWords; ++k) xw[k] = x4[min(k * kGemvThreads + tid, nx - 1)];
+    if constexpr (NORM) {
+        if (norm_dtype == SWQ_F32) {
+            const uint4 *w4 = static_cast<const uint4 *>(norm_w);
+#pragma unroll
+            for (int k = 0; k < kStageWords; ++k) ww[k] = w4[min(k * kGemvThreads + tid, nx - 1)];
+        } else {
+            const uint2 *w2 = static_cast<const uint2 *>(norm_w);
+#pragma unroll
+            for (int k = 0; k < kStageWords; ++k) {
+                const uint2 r = w2[min(k * kGemvThreads + tid, nx - 1)];
+                ww[k] = make_uint4(r.x, r.y, 0u, 0u);
+            }
+        }
+    }
+    issue();
+    float sc = 1.f;
+    if constexpr (NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < kStageWords; ++k) {
+            if (k * kGemvThreads + tid < nx) {
+                const float4 v = __builtin_bit_cast(float4, xw[k]);
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) L.red[wave] = ss;
+        lds_barrier();
+        float tot = 0.f;
+#pragma unroll
+        for (int i = 0; i < kGemvThreads / kWave; ++i) tot += L.red[i];
+        sc = 1.0f / __fsqrt_rn(tot / static_cast<float>(in) + eps);
+    }
+#pragma unroll
+    for (int k = 0; k < kStageWords; ++k) {
+        const int i = k * kGemvThreads + tid;
+        if (i < nx) {
+            float4 v = __builtin_bit_cast(float4, xw[k]);
+            if constexpr (NORM) {
+                float w[4];
+                if (norm_dtype == SWQ_F32) {
+                    const float4 wf = __builtin_bit_cast(float4, ww[k]);
+                    w[0] = wf.x;
+                    w[1] = wf.y;
+                    w[2] = wf.z;
+                    w[3] = wf.w;
+                } else {
+                    const uint32_t h[4] = {ww[k].x & 0xFFFFu, ww[k].x >> 16, ww[k].y & 0xFFFFu, ww[k].y >> 16};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint16_t raw = static_cast<uint16_t>(h[e]);
+                        w[e] = norm_dtype == SWQ_BF16 ? bf16_to_f32(raw) : f16_to_f32(raw);
+                    }
+                }
+                v.x *= sc * w[0];
+                v.y *= sc * w[1];
+                v.z *= sc * w[2];
+                v.w *= sc * w[3];
+            }
+            const int c = i / kP, p = i - c * kP;
+            L.x[c * kP + ((p + c) & (kP - 1))] = __builtin_bit_cast(uint4, v);
+        }
+    }
+    lds_barrier();
+}
+
+// The wave's slice of the staged x, with its chunk sums formed as
+// load_xslice forms them (so results equal those from x read directly).
+template <int BITS, int CPL>
+__device__ __forceinline__ void xslice_from_lds(XSlice<BITS, CPL, kXF32> &xs, const StagedX &L, const QMat &m,
+                                                const LaneMap &lm) {
+    constexpr int kCPC = codes_per_chunk<BITS>(), kP = kCPC / 4;
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+        const int c = min(lm.j + u * lm.lpr, m.chunks - 1);
+#pragma unroll
+        for (int p = 0; p < kP; ++p) {
+            const float4 v = __builtin_bit_cast(float4, L.x[c * kP + ((p + c) & (kP - 1))]);
+            xs.v[u][4 * p + 0] = v.x;
+            xs.v[u][4 * p + 1] = v.y;
+            xs.v[u][4 * p + 2] = v.z;
+            xs.v[u][4 * p + 3] = v.w;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < kCPC; ++i) sum += xs.v[u][i];
+        xs.sum[u] = sum;
+    }
+}
+
 template <int BITS, int CPL, int ES>
 __global__ __launch_bounds__(kGemvThreads) void gemv_vec_kernel(QMat m, int rows, const float *x, float *y) {
     constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
@@ -27,12 +152,15 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_vec_kernel(QMat m, int rows
     const int ntiles = (rows + tile_rows - 1) / tile_rows;
     const int nw = gridDim.x * (kGemvThreads / kWave);
     int t = blockIdx.x * (kGemvThreads / kWave) + wave;
-    if (t >= ntiles) return;
-    XSlice<BITS, CPL, kXF32> xs;
-    load_xslice<SWQ_F32>(xs, m, lm, x, 0);
+    __shared__ StagedX L;
     RowTile<BITS, CPL, ES> cur, next, next2;
-    load_tile(cur, m, 0, lm, t * tile_rows, rows);
-    if (t + nw < ntiles) load_tile(next, m, 0, lm, (t + nw) * tile_rows, rows);
+    stage_x<BITS, false>(L, x, m.in, nullptr, 0, 0.f, [&] {
+        if (t < ntiles) load_tile(cur, m, 0, lm, t * tile_rows, rows);
+        if (t + nw < ntiles) load_tile(next, m, 0, lm, (t + nw) * tile_rows, rows);
+    });
+    if (t >= ntiles) return;  // after the staging, which every wave takes part in
+    XSlice<BITS, CPL, kXF32> xs;
+    xslice_from_lds(xs, L, m, lm);
     for (;;) {
         const int tn = t + nw;
         if (tn + nw < ntiles) load_tile(next2, m, 0, lm, (tn + nw) * tile_rows, rows);
@@ -56,10 +184,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_vec_kernel(QMat m, int rows
 // group, scale dtype) in one launch: their row tiles are numbered
 // consecutively (matrix i owns tiles [tile_end[i-1], tile_end[i])) and the
 // waves walk them as gemv_vec_kernel walks one matrix.  With NORM the input
-// is h and each wave turns its slice into rmsnorm(h) * w in registers: the
-// lanes of row slot 0 hold every chunk of h once, so their squares summed
-// over the wave give sum(h^2); then x = h * (scale * w) (the product order
-// of QwenCPUModel.rmsNorm).
+// is h, and the staging turns it into rmsnorm(h) * w in LDS.
 constexpr int kMultiMax = 4;
 
 struct MultiArgs {
@@ -78,7 +203,7 @@ struct MultiArgs {
 template <int BITS, int CPL, int ES, bool NORM>
 __global__ __launch_bounds__(kGemvThreads) void gemv_multi_kernel(const MultiArgs a) {
     constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
-    constexpr int kCPC = codes_per_chunk<BITS>();
+    __shared__ StagedX L;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const LaneMap lm = lane_map(a.m.lpr_log2, lane);
@@ -86,7 +211,6 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_multi_kernel(const MultiArg
     const int ntiles = a.tile_end[a.n - 1];
     const int nw = gridDim.x * (kGemvThreads / kWave);
     int t = blockIdx.x * (kGemvThreads / kWave) + wave;
-    if (t >= ntiles) return;
     auto mat_of = [&](int tt) {
         int i = 0;
         while (i + 1 < a.n && tt >= a.tile_end[i]) ++i;
@@ -100,61 +224,21 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_multi_kernel(const MultiArg
         return q;
     };
     auto row0_of = [&](int tt, int i) { return (tt - (i ? a.tile_end[i - 1] : 0)) * tile_rows; };
-    // x and the norm weights first: loads complete in issue order, so the
-    // norm arithmetic below waits for these and not for the weight tiles
-    XSlice<BITS, CPL, kXF32> xs;
-    load_xslice<SWQ_F32>(xs, a.m, lm, a.x, 0);
-    constexpr int kWB = NORM ? kCPC * 4 / 16 : 1;  // 16-byte words of a chunk's norm weights (f32 at most)
-    uint4 wraw[CPL][kWB];
-    if constexpr (NORM) {
-        const int wbytes = a.norm_dtype == SWQ_F32 ? 4 : 2;
-#pragma unroll
-        for (int u = 0; u < CPL; ++u) {
-            const int c = min(lm.j + u * lm.lpr, a.m.chunks - 1);
-            const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const uint8_t *>(a.norm_w) +
-                                                               static_cast<int64_t>(c) * kCPC * wbytes);
-            const int kw = kCPC * wbytes / 16;  // words this chunk's weights fill (the rest repeat the last one)
-#pragma unroll
-            for (int k = 0; k < kWB; ++k) wraw[u][k] = src[min(k, kw - 1)];
-        }
-    }
     RowTile<BITS, CPL, ES> cur, next, next2;
-    int mc = mat_of(t);
-    load_tile(cur, qmat(mc), 0, lm, row0_of(t, mc), a.rows[mc]);
-    if (t + nw < ntiles) {
-        const int tn1 = t + nw, mn1 = mat_of(tn1);
-        load_tile(next, qmat(mn1), 0, lm, row0_of(tn1, mn1), a.rows[mn1]);
-    }
-    if constexpr (NORM) {
-        float ss = 0.f;
-#pragma unroll
-        for (int u = 0; u < CPL; ++u) {
-            if (lm.q == 0 && lm.j + u * lm.lpr < a.m.chunks) {
-#pragma unroll
-                for (int i = 0; i < kCPC; ++i) ss += xs.v[u][i] * xs.v[u][i];
-            }
+    int mc = 0;
+    stage_x<BITS, NORM>(L, a.x, a.m.in, a.norm_w, a.norm_dtype, a.eps, [&] {
+        if (t < ntiles) {
+            mc = mat_of(t);
+            load_tile(cur, qmat(mc), 0, lm, row0_of(t, mc), a.rows[mc]);
         }
-        ss = wave_sum(ss);
-        const float sc = 1.0f / __fsqrt_rn(ss / static_cast<float>(a.m.in) + a.eps);
-#pragma unroll
-        for (int u = 0; u < CPL; ++u) {
-            const uint32_t *wr = reinterpret_cast<const uint32_t *>(wraw[u]);
-            float sum = 0.f;
-#pragma unroll
-            for (int i = 0; i < kCPC; ++i) {
-                float wv;
-                if (a.norm_dtype == SWQ_F32) {
-                    wv = __uint_as_float(wr[i]);
-                } else {
-                    const uint16_t raw = static_cast<uint16_t>(wr[i / 2] >> (16 * (i & 1)));
-                    wv = a.norm_dtype == SWQ_BF16 ? bf16_to_f32(raw) : f16_to_f32(raw);
-                }
-                xs.v[u][i] *= sc * wv;
-                sum += xs.v[u][i];
-            }
-            xs.sum[u] = sum;
+        if (t + nw < ntiles) {
+            const int tn1 = t + nw, mn1 = mat_of(tn1);
+            load_tile(next, qmat(mn1), 0, lm, row0_of(tn1, mn1), a.rows[mn1]);
         }
-    }
+    });
+    if (t >= ntiles) return;  // after the staging, which every wave takes part in
+    XSlice<BITS, CPL, kXF32> xs;
+    xslice_from_lds(xs, L, a.m, lm);
     for (;;) {
         const int tn = t + nw;
         if (tn + nw < ntiles) {
@@ -266,7 +350,7 @@ static int launch_gemv(const swq_qlinear *l, int rows, int64_t w_extra, int64_t 
         // 4-bit rows of 65..128 chunks (in_dim up to 4096) with fp32 x: two
         // chunks per lane, a plan only the standalone GEMV compiles
         const bool q4_wide = m.bits == 4 && m.xf == 0 && m.cpl == 2 && m.chunks <= 2 * kWave;
-        if (plan_fits(m) || q4_wide) {
+        if ((plan_fits(m) || q4_wide) && m.in <= kStageMaxIn) {
             const int rows_per_block = (kGemvThreads / kWave) * (4 / m.cpl) * (kWave >> m.lpr_log2);
             const dim3 grid(std::min((rows + rows_per_block - 1) / rows_per_block, kGemvMaxBlocks));
 #define SWQ_GEMV_LAUNCH(B, C, E) \
@@ -303,7 +387,8 @@ extern "C" int swq_encode_gemv_multi(const swq_qlinear *lins, int n, float *cons
     if (norm_weight && norm_dtype != SWQ_F32 && norm_dtype != SWQ_F16 && norm_dtype != SWQ_BF16)
         return SWQ_ERR_UNSUPPORTED_DTYPE;
     if (norm_weight && !(norm_eps >= 0.f)) return SWQ_ERR_INVALID_ARGUMENT;
-    if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return SWQ_ERR_MISALIGNED;
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(norm_weight) % 16 != 0)
+        return SWQ_ERR_MISALIGNED;
     const swq_qlinear &l0 = lins[0];
     MultiArgs a{};
     for (int i = 0; i < n; ++i) {
@@ -324,7 +409,8 @@ extern "C" int swq_encode_gemv_multi(const swq_qlinear *lins, int n, float *cons
     }
     a.m = make_qmat(&l0);
     const bool q4_wide = a.m.bits == 4 && a.m.xf == 0 && a.m.cpl == 2 && a.m.chunks <= 2 * kWave;
-    if (!(plan_fits(a.m) || q4_wide) || a.m.xf != 0) return SWQ_ERR_LIMIT;
+    if (!(plan_fits(a.m) || q4_wide) || a.m.xf != 0 || a.m.in > kStageMaxIn || a.m.in % 4 != 0)
+        return SWQ_ERR_LIMIT;
     const int tile_rows = (4 / a.m.cpl) * (kWave >> a.m.lpr_log2);
     int total = 0;
     for (int i = 0; i < n; ++i) {
