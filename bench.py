@@ -451,7 +451,6 @@ def model_measure(args, torch, lib, shape, moe_layers, moe_ws, tokens=4):
     vv = torch.empty(AKV * ahd, dtype=torch.float32, device=dev)
     y = torch.empty(max(valD, AH * ahd), dtype=torch.float32, device=dev)
     r = torch.empty(H, dtype=torch.float32, device=dev)
-    xf = torch.empty(H, dtype=torch.float32, device=dev)
     logits = torch.empty(LMHEAD_VOCAB, dtype=torch.float32, device=dev)
     n_ws = lib.swq_sample_workspace_bytes(LMHEAD_VOCAB)
     sws = torch.zeros(n_ws, dtype=torch.uint8, device=dev)
@@ -472,6 +471,8 @@ def model_measure(args, torch, lib, shape, moe_layers, moe_ws, tokens=4):
         multi.append(((_lib.QLinear * len(ptrs))(*[l.c() for l in blk.projections]), (ctypes.c_void_p * len(ptrs))(*ptrs)))
     outs_c = [blk.out_proj.c() if kind == "delta" else blk.o_proj.c() for kind, blk, _ in blocks]
     head_c = head.c()
+    head_lins = (_lib.QLinear * 1)(head_c)
+    head_ys = (ctypes.c_void_p * 1)(logits.data_ptr())
     launches = 0
 
     def token(cap, t):
@@ -499,14 +500,13 @@ def model_measure(args, torch, lib, shape, moe_layers, moe_ws, tokens=4):
                                           moe_ws[i].data_ptr(), moe_ws[i].numel(), cap), "moe")
             launches += 3
         hc = hbuf[MODEL_LAYERS % 2]
-        check(lib.swq_rmsnorm(hc.data_ptr(), None, w_final.data_ptr(), _lib.SWQ_BF16, eps, 1, H, xf.data_ptr(),
-                              _lib.SWQ_F32, cap), "final norm")
-        check(lib.swq_encode_gemv(ctypes.byref(head_c), 0, 0, 0, 0, xf.data_ptr(), 0, logits.data_ptr(), 0, cap),
-              "lm_head")
+        # the final norm inside the lm_head's launch
+        check(lib.swq_encode_gemv_multi(head_lins, 1, head_ys, hc.data_ptr(), w_final.data_ptr(), _lib.SWQ_BF16, eps,
+                                        cap), "final norm + lm_head")
         check(lib.swq_sample(logits.data_ptr(), LMHEAD_VOCAB, ctypes.byref(opt), seen.data_ptr(), counts.data_ptr(),
                              64, banned.data_ptr(), 1, ctypes.c_float(0.5), tok.data_ptr(), sws.data_ptr(), n_ws, cap),
               "sample")
-        launches += 4
+        launches += 2
 
     gr = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gr):
@@ -527,7 +527,8 @@ def model_measure(args, torch, lib, shape, moe_layers, moe_ws, tokens=4):
     return {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1), "layers": MODEL_LAYERS,
             "attention_context": pos + 1, "launches_per_token": launches // tokens,
             "note": "one decode token of the 35B-A3B-shape 4-bit model (30 DeltaNet + 10 attention layers, 40 MoE "
-                    "steps, final norm, 248,320-row lm_head, sampling), all on the device, graph of 4 tokens; "
+                    "steps, final norm inside the 248,320-row lm_head's launch, sampling), all on the device, graph of 4 "
+                    "tokens; "
                     "synthetic weights; context only: the reference publishes 7-11 tok/s for this model on an "
                     "M5 Mac (README.md:21), whole decode including its SSD expert streaming"}
 
@@ -787,10 +788,11 @@ LMHEAD_VOCAB = 248320  # qwen3.6-35b vocab_size (model config)
 
 
 def lmhead_measure(args, torch, lib, hidden):
-    """Final RMSNorm (swq_rmsnorm), the q4 lm_head GEMV (swq_encode_gemv) and
-    Qwen's default sampling (swq_sample: T 0.7, top-k 20, top-p 0.8, presence
-    1.5, frequency 0.5, 64 seen tokens) per token, as a graph over two
-    resident lm_heads (2 x 286 MB, more than the 256 MB MALL)."""
+    """Final RMSNorm and the q4 lm_head GEMV in one launch
+    (swq_encode_gemv_multi with the norm weight), then Qwen's default sampling
+    (swq_sample: T 0.7, top-k 20, top-p 0.8, presence 1.5, frequency 0.5, 64
+    seen tokens) per token, as a graph over two resident lm_heads (2 x 286 MB,
+    more than the 256 MB MALL).  gemv_us: the GEMV alone (swq_encode_gemv)."""
     from swiftlet_amd import _lib, moe
     from swiftlet_amd._lib import check
     dev = "cuda"
@@ -798,7 +800,8 @@ def lmhead_measure(args, torch, lib, hidden):
     heads = [moe.synth_linear(args.seed, 900 + r, "router", None, V, hidden, 4, 64, dev) for r in range(R)]
     h = torch.randn((R, hidden), dtype=torch.float32, device=dev)
     wn = (1.0 + 0.1 * torch.randn(hidden, device=dev)).to(torch.bfloat16)
-    x = torch.empty((R, hidden), dtype=torch.float32, device=dev)
+    # the GEMV-alone graph's input: the normalised rows the fused launch computes
+    x = ((h * torch.rsqrt((h * h).mean(dim=1, keepdim=True) + 1e-6)) * wn.float()).contiguous()
     logits = torch.empty((R, V), dtype=torch.float32, device=dev)
     n_ws = lib.swq_sample_workspace_bytes(V)
     wss = [torch.zeros(n_ws, dtype=torch.uint8, device=dev) for _ in range(R)]
@@ -808,6 +811,8 @@ def lmhead_measure(args, torch, lib, hidden):
     toks = torch.empty(R, dtype=torch.int32, device=dev)
     opt = _lib.SampleOptions(0.7, 20, 0.8, 1.5, 0.5)
     cs = [c.c() for c in heads]
+    lins1 = [(_lib.QLinear * 1)(c) for c in cs]
+    ys1 = [(ctypes.c_void_p * 1)(logits[r].data_ptr()) for r in range(R)]
 
     def graph_of(parts):
         g = torch.cuda.CUDAGraph()
@@ -815,9 +820,9 @@ def lmhead_measure(args, torch, lib, hidden):
             cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
             for i in range(K):
                 r = i % R
-                if "norm" in parts:
-                    check(lib.swq_rmsnorm(h[r].data_ptr(), None, wn.data_ptr(), _lib.SWQ_BF16, ctypes.c_float(1e-6),
-                                          1, hidden, x[r].data_ptr(), _lib.SWQ_F32, cap), "rmsnorm")
+                if "norm+gemv" in parts:
+                    check(lib.swq_encode_gemv_multi(lins1[r], 1, ys1[r], h[r].data_ptr(), wn.data_ptr(), _lib.SWQ_BF16,
+                                                    ctypes.c_float(1e-6), cap), "final norm + lm_head")
                 if "gemv" in parts:
                     check(lib.swq_encode_gemv(ctypes.byref(cs[r]), 0, 0, 0, 0, x[r].data_ptr(), 0,
                                               logits[r].data_ptr(), 0, cap), "lm_head gemv")
@@ -837,7 +842,7 @@ def lmhead_measure(args, torch, lib, hidden):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1000.0 / K
 
-    us_step = timed(graph_of(("norm", "gemv", "sample")))
+    us_step = timed(graph_of(("norm+gemv", "sample")))
     us_gemv = timed(graph_of(("gemv",)))
     us_sample = timed(graph_of(("sample",)))
     gemv_bytes = heads[0].matrix_bytes + hidden * 4 + V * 4
@@ -848,8 +853,8 @@ def lmhead_measure(args, torch, lib, hidden):
     return {"vocab": V, "us_per_token": round(us_step, 3), "gemv_us": round(us_gemv, 3),
             "sample_us": round(us_sample, 3), "gemv_bytes": int(gemv_bytes), "gemv_gbs": round(gbs, 1),
             "gemv_frac": round(gbs / 8000.0, 4),
-            "note": "final norm + q4 lm_head GEMV + top-k/top-p sampling per token, graph of 64 tokens "
-                    "over 2 resident lm_heads; gemv_us from a graph of the GEMV alone"}
+            "note": "final norm + q4 lm_head GEMV (one launch) + top-k/top-p sampling per token, graph of 64 "
+                    "tokens over 2 resident lm_heads; gemv_us from a graph of the GEMV alone"}
 
 
 def prefill_measure(args, torch, lib, name):
