@@ -121,6 +121,25 @@ def test_gemv_validation(lib):
     assert lib.swq_encode_silu_mul(FAKE, 0, 0, 0, 0, None) == _lib.SWQ_ERR_INVALID_ARGUMENT
 
 
+def test_gemv_multi_validation(lib):
+    """swq_encode_gemv_multi rejects bad calls before any launch (every call
+    here fails validation: no kernel ever sees the fake addresses)."""
+    F = _lib.SWQ_F32
+    two = (QLinear * 2)(lin(64, 2048), lin(32, 2048))
+    ys = (ctypes.c_void_p * 2)(FAKE, FAKE)
+    call = lib.swq_encode_gemv_multi
+    assert call(two, 0, ys, FAKE, None, F, 1e-6, None) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    assert call(two, 5, ys, FAKE, None, F, 1e-6, None) == _lib.SWQ_ERR_LIMIT  # more than four matrices
+    assert call(two, 2, ys, FAKE + 4, None, F, 1e-6, None) == _lib.SWQ_ERR_MISALIGNED  # x
+    assert call(two, 2, ys, FAKE, FAKE + 8, _lib.SWQ_BF16, 1e-6, None) == _lib.SWQ_ERR_MISALIGNED  # norm weight
+    assert call(two, 2, ys, FAKE, FAKE, 7, 1e-6, None) == _lib.SWQ_ERR_UNSUPPORTED_DTYPE
+    assert call(two, 2, ys, FAKE, FAKE, F, -1.0, None) == _lib.SWQ_ERR_INVALID_ARGUMENT
+    mixed = (QLinear * 2)(lin(64, 2048), lin(32, 1024))
+    assert call(mixed, 2, ys, FAKE, None, F, 1e-6, None) == _lib.SWQ_ERR_BAD_SHAPE  # in_dim differs
+    wide = (QLinear * 1)(lin(64, 8192))
+    assert call(wide, 1, ys, FAKE, None, F, 1e-6, None) == _lib.SWQ_ERR_LIMIT  # in_dim above 4096
+
+
 def test_rmsnorm_validation(lib):
     F = _lib.SWQ_F32
     assert lib.swq_rmsnorm(0, None, None, F, 1e-6, 1, 64, FAKE, F, None) == _lib.SWQ_ERR_INVALID_ARGUMENT
