@@ -61,11 +61,21 @@ PREFILL_STAGES = [("prep", 1), ("router", 2), ("route", 4), ("gate_up", 8), ("do
 
 CONFIGS = {
     # name: (shape key, batch)
+    "single-expert-q4-b1": ("single-expert-q4", 1),
     "qwen3.6-35b-a3b-q4-b1": ("qwen3.6-35b-a3b-q4", 1),
     "qwen3-next-80b-a3b-q4-b1": ("qwen3-next-80b-a3b-q4", 1),
     "qwen3.6-35b-a3b-q8-b1": ("qwen3.6-35b-a3b-q8", 1),
     "qwen3.6-35b-a3b-q8-b4": ("qwen3.6-35b-a3b-q8", 4),
 }
+
+
+# the other decode workloads the default line summarises, and the resident
+# layers each cycles (enough distinct bytes to exceed the 256 MB MALL: one
+# 1.77 MB expert per layer for the single expert; 48 layers for the 80B stack)
+OTHER_DECODE_CONFIGS = ["single-expert-q4-b1", "qwen3-next-80b-a3b-q4-b1", "qwen3.6-35b-a3b-q8-b1",
+                        "qwen3.6-35b-a3b-q8-b4"]
+DEFAULT_REPLICAS = {"single-expert-q4-b1": 256, "qwen3-next-80b-a3b-q4-b1": 48, "qwen3.6-35b-a3b-q8-b1": 48,
+                    "qwen3.6-35b-a3b-q8-b4": 48, "qwen3.6-35b-a3b-q4-b1": 48}
 
 
 def parse():
@@ -75,6 +85,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=96)
     ap.add_argument("--config", default="qwen3.6-35b-a3b-q4-b1", choices=sorted(CONFIGS) + sorted(PREFILL_CONFIGS))
     ap.add_argument("--no-prefill", action="store_true", help="decode line without the prefill summary")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="decode line without the single-expert, 80B, q8 batch-1 and batch-4 summaries")
     ap.add_argument("--no-lmhead", action="store_true", help="decode line without the lm_head + sampling summary")
     ap.add_argument("--no-load", action="store_true", help="decode line without the qpack layer-load rate")
     ap.add_argument("--no-deltanet", action="store_true", help="decode line without the DeltaNet layer summary")
@@ -142,68 +154,28 @@ def main():
 
     shape_key, batch = CONFIGS[args.config]
     path = args.path if args.path != "auto" else ("fused" if batch == 1 else "staged")
-    MASK = _lib.SWQ_STAGES_FUSED if path == "fused" else 7
     shape = synth.SHAPES[shape_key]
-    R = args.replicas
-    dev = "cuda"
     torch.cuda.init()
+    K, W = args.steps, args.warmup
+    m = decode_measure(args, torch, lib, args.config, args.replicas, K, W, path, keep=True)
+    layers, wss, calls, ids, wts, xs_bits = m.pop("_keep")
+    R = len(layers)
+    dev = "cuda"
     stream = torch.cuda.current_stream()
     sh = ctypes.c_void_p(stream.cuda_stream)
-
-
-    # ---- resident weights: R distinct layers, all experts --------------
-    layers = [moe.synth_layer(shape, args.seed, r, dev) for r in range(R)]
-    xs_bits = synth.activations_bf16(args.seed + 7, R * batch, shape.hidden).reshape(R, batch, shape.hidden)
-    xs = torch.from_numpy(xs_bits.view(np.int16)).view(torch.bfloat16).to(dev)
-    wss = [l.new_workspace(batch) for l in layers]
-    outs = torch.empty((R, batch, shape.hidden), dtype=torch.bfloat16, device=dev)
-    ids = torch.empty((R, batch, shape.top_k), dtype=torch.int32, device=dev)
-    wts = torch.empty((R, batch, shape.top_k), dtype=torch.float32, device=dev)
-    torch.cuda.synchronize()
-
-    # prebuilt ctypes argument tuples, one per replica
-    calls = []
-    for r, l in enumerate(layers):
-        calls.append((ctypes.byref(l._c), ctypes.c_void_p(xs[r].data_ptr()), _lib.SWQ_BF16, batch,
-                      ctypes.c_void_p(outs[r].data_ptr()), _lib.SWQ_BF16, ctypes.c_void_p(ids[r].data_ptr()),
-                      ctypes.c_void_p(wts[r].data_ptr()), ctypes.c_void_p(wss[r].data_ptr()), wss[r].numel(), 0))
+    MASK = _lib.SWQ_STAGES_FUSED if path == "fused" else 7
 
     def step(i, mask=MASK):
-        c = calls[i % R]
-        check(lib.swq_moe_decode_stages(*c, mask, sh), "moe_decode")
-
-    # ---- graph of K steps -----------------------------------------------
-    K, W = args.steps, args.warmup
-    for i in range(min(W, R)):
-        step(i)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-        for i in range(K):
-            c = calls[i % R]
-            check(lib.swq_moe_decode_stages(*c, MASK, cap), "moe_decode (capture)")
-    torch.cuda.synchronize()
-    for _ in range(max(1, (W + K - 1) // K)):
-        graph.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    graph_ms = e0.elapsed_time(e1)
-    us_per_step = graph_ms * 1000.0 / K
+        check(lib.swq_moe_decode_stages(*calls[i % R], mask, sh), "moe_decode")
 
     # ---- per-kernel durations ------------------------------------------------
     # fused: one kernel per step, so the graph's average step is its average
     # launch.  staged: graphs of single-stage steps (each replica's workspace
     # already holds its routing from the replays above, so a stage on its own
     # reads valid inputs); HIP events around one replay give the average launch.
-    n_st = min(K, 4 * R)
+    n_st = max(R, min(K, 4 * R))
     if path == "fused":
-        stage_us = [us_per_step]
+        stage_us = [m["us_per_step"]]
     else:
         stage_us = []
         for mask in (1, 2, 4):
@@ -211,8 +183,7 @@ def main():
             with torch.cuda.graph(g):
                 cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
                 for i in range(n_st):
-                    c = calls[i % R]
-                    check(lib.swq_moe_decode_stages(*c, mask, cap), "moe_decode stage (capture)")
+                    check(lib.swq_moe_decode_stages(*calls[i % R], mask, cap), "moe_decode stage (capture)")
             g.replay()
             torch.cuda.synchronize()
             a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -248,10 +219,11 @@ def main():
              ctypes.c_void_p(hs[r].data_ptr()), _lib.SWQ_F32, ctypes.c_void_p(ids[r].data_ptr()),
              ctypes.c_void_p(wts[r].data_ptr()), ctypes.c_void_p(wss[r].data_ptr()), wss[r].numel(),
              _lib.SWQ_MOE_ACCUMULATE)))
+    n_tail = max(R, K)
     gt = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gt):
         cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-        for i in range(K):
+        for i in range(n_tail):
             nrm, dec = tail_calls[i % R]
             check(lib.swq_rmsnorm(*nrm, cap), "rmsnorm (capture)")
             check(lib.swq_moe_decode_stages(*dec, MASK, cap), "moe_decode (capture)")
@@ -262,7 +234,7 @@ def main():
     gt.replay()
     b1.record()
     torch.cuda.synchronize()
-    tail_sep_us = b0.elapsed_time(b1) * 1000.0 / K
+    tail_sep_us = b0.elapsed_time(b1) * 1000.0 / n_tail
     del gt
     # the same tail with the residual add and the norm folded into the MoE
     # step's launch (swq_moe_decode_norm; batch 1, the single-launch path)
@@ -279,7 +251,7 @@ def main():
             gf = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gf):
                 cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-                for i in range(K):
+                for i in range(n_tail):
                     check(lib.swq_moe_decode_norm(*fold_calls[i % R], cap), "moe_decode_norm (capture)")
             gf.replay()
             torch.cuda.synchronize()
@@ -287,28 +259,27 @@ def main():
             gf.replay()
             b1.record()
             torch.cuda.synchronize()
-            tail_us = b0.elapsed_time(b1) * 1000.0 / K
+            tail_us = b0.elapsed_time(b1) * 1000.0 / n_tail
             tail_folded = True
             del gf
-
-    # unique experts per step (batch > 1 reads each distinct expert once)
-    ids_h = ids.cpu().numpy()
-    uniq = [len(np.unique(ids_h[r])) for r in range(R)]
-    mean_uniq = float(np.mean(uniq))
+    for r in range(R):
+        check(layers[r].workspace_status(wss[r]), "workspace status after the timed replays")
 
     H, I, Is, E = shape.hidden, shape.inter, shape.shared_inter, shape.experts
     mb = shape.matrix_bytes
     eb, rb = shape.expert_bits, shape.router_bits
     xb = batch * H * 2
-    step_bytes = shape.decode_bytes(mean_uniq, batch)
+    mean_uniq = m["unique_experts_per_step"]
+    step_bytes = m["step_bytes"]
     if path == "fused":
         stage_bytes = [step_bytes]
         kernels = ["moe_fused"]
     else:
+        sh_b = (2 * mb(Is, H, eb) + mb(1, H, rb)) if Is else 0
         stage_bytes = [
-            mb(E, H, rb) + mb(1, H, rb) + 2 * mb(Is, H, eb) + xb,    # router + shared gate + shared gate/up
+            mb(E, H, rb) + sh_b + xb,                                # router + shared gate + shared gate/up
             mean_uniq * 2 * mb(I, H, eb) + xb,                       # routed gate/up
-            mean_uniq * mb(H, I, eb) + mb(H, Is, eb) + xb,           # routed + shared down, bf16 out
+            mean_uniq * mb(H, I, eb) + (mb(H, Is, eb) if Is else 0) + xb,  # routed + shared down, bf16 out
         ]
         kernels = ["moe_stage1", "moe_stage2", "moe_stage3"]
     dom = int(np.argmax(stage_us))
@@ -317,32 +288,30 @@ def main():
 
     result = {
         "metric": "us per MoE-layer decode step; achieved HBM GB/s as fraction of peak (1 GPU)",
-        "value": round(us_per_step, 3),
+        "value": m["value"],
         "unit": "us/layer-step",
         "n_gpus": 1,
         "steps": K,
         "warmup": W,
-        "ms_per_step": round(us_per_step / 1000.0, 6),
+        "ms_per_step": round(m["value"] / 1000.0, 6),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4-affine x bf16, fp32 accumulate" if eb == 4 else "q8-affine x bf16, fp32 accumulate",
-        "data": f"synthetic seeded weights (seed {args.seed}), {R} distinct resident layers cycled, bf16 x ~N(0,1)",
-        "config": {"workload": args.config, "hidden": H, "experts": E, "top_k": shape.top_k,
-                   "moe_intermediate": I, "shared_intermediate": Is, "expert_bits": eb,
-                   "router_bits": rb, "group": shape.group, "batch": batch, "replicas": R,
-                   "parallelism": "single GPU"},
+        "data": m["data"],
+        "config": m["config"],
         "roofline": {"bound": "hbm", "kernel": dom_kernel,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": MEASURED_TRAFFIC.get((args.config, dom_kernel)),
                      "algorithmic_bytes_per_launch": int(stage_bytes[dom]),
                      "avg_launch_us": round(stage_us[dom], 3)},
+        "step_us_distribution": m["distribution"],
         "path": path,
         "kernel_us": dict(zip(kernels, [round(v, 3) for v in stage_us])),
         "kernel_bytes": dict(zip(kernels, [int(v) for v in stage_bytes])),
         "step_bytes": int(step_bytes),
-        "step_gbs_wall": round(step_bytes / (us_per_step * 1e-6) / 1e9, 1),
+        "step_gbs_wall": m["step_gbs"],
         "step_gbs_kernels": round(step_bytes / (sum(stage_us) * 1e-6) / 1e9, 1),
         "eager_us_per_step": round(eager_us_per_step, 3),
         "layer_tail_us": round(tail_us, 3),
@@ -377,16 +346,124 @@ def main():
     if not args.no_load and shape_key.startswith("qwen3.6-35b"):
         result["qpack_load"] = qpack_load_measure(torch, lib, shape)
 
+    del layers, wss, calls
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+    # ---- the other decode workloads, each on its own resident stack ---------
+    if not args.no_configs and args.config == "qwen3.6-35b-a3b-q4-b1":
+        result["configs"] = {}
+        for name in OTHER_DECODE_CONFIGS:
+            sm = decode_measure(args, torch, lib, name, None, None, None, "auto")
+            result["configs"][name] = {k: sm[k] for k in (
+                "value", "unit", "distribution", "roofline", "step_bytes", "unique_experts_per_step", "config",
+                "data")}
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+
     # ---- the prefill chunk, summarised --------------------------------------
     if not args.no_prefill:
-        del layers, wss, graph
-        torch.cuda.synchronize()
-        torch.cuda.empty_cache()
         res = prefill_measure(args, torch, lib, "qwen3.6-35b-a3b-q4-prefill512")
         line = prefill_line(args, res)
         result["prefill"] = {k: line[k] for k in ("config", "value", "unit", "roofline", "kernel_us", "mfma")}
 
     print(json.dumps(result), flush=True)
+
+
+def decode_measure(args, torch, lib, name, R=None, K=None, W=None, path="auto", keep=False):
+    """µs per MoE-layer decode step of workload `name` on R resident seeded
+    layers (all experts each), cycled with a distinct input per layer.
+
+    K steps are captured in one HIP graph (step i runs layer i mod R).  The
+    first timed replay, bracketed by a synchronize on both sides, gives
+    `value` (K steps exactly); further replays of the same graph, at least
+    100 steps in all and at least 11 replays, give the distribution of the
+    per-step time over replays (median, p10, p90).  Algorithmic bytes count
+    each distinct expert of a step once, from the ids the timed steps wrote
+    (only the layers the graph ran)."""
+    from swiftlet_amd import _lib, moe, synth
+    from swiftlet_amd._lib import check
+    shape_key, batch = CONFIGS[name]
+    shape = synth.SHAPES[shape_key]
+    R = R or DEFAULT_REPLICAS.get(name, 48)
+    K = K or max(R, 96)
+    W = W if W is not None else R
+    path = path if path != "auto" else ("fused" if batch == 1 else "staged")
+    mask = _lib.SWQ_STAGES_FUSED if path == "fused" else 7
+    dev = "cuda"
+    layers = [moe.synth_layer(shape, args.seed, r, dev) for r in range(R)]
+    xs_bits = synth.activations_bf16(args.seed + 7, R * batch, shape.hidden).reshape(R, batch, shape.hidden)
+    xs = torch.from_numpy(xs_bits.view(np.int16)).view(torch.bfloat16).to(dev)
+    wss = [l.new_workspace(batch) for l in layers]
+    outs = torch.empty((R, batch, shape.hidden), dtype=torch.bfloat16, device=dev)
+    ids = torch.full((R, batch, shape.top_k), -1, dtype=torch.int32, device=dev)
+    wts = torch.empty((R, batch, shape.top_k), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    calls = [(ctypes.byref(l._c), ctypes.c_void_p(xs[r].data_ptr()), _lib.SWQ_BF16, batch,
+              ctypes.c_void_p(outs[r].data_ptr()), _lib.SWQ_BF16, ctypes.c_void_p(ids[r].data_ptr()),
+              ctypes.c_void_p(wts[r].data_ptr()), ctypes.c_void_p(wss[r].data_ptr()), wss[r].numel(), 0)
+             for r, l in enumerate(layers)]
+    sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for i in range(W):
+        check(lib.swq_moe_decode_stages(*calls[i % R], mask, sh), "moe_decode")
+    torch.cuda.synchronize()
+    ids.fill_(-1)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for i in range(K):
+            check(lib.swq_moe_decode_stages(*calls[i % R], mask, cap), "moe_decode (capture)")
+    torch.cuda.synchronize()
+    graph.replay()  # warm: the graph's own first replay
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    samples = []
+    n_rep = max(11, -(-100 // K))
+    for _ in range(n_rep):
+        torch.cuda.synchronize()
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        samples.append(e0.elapsed_time(e1) * 1000.0 / K)
+    for r in range(min(K, R)):
+        check(layers[r].workspace_status(wss[r]), f"{name}: workspace status after the timed replays")
+    ran = min(K, R)
+    ids_h = ids.cpu().numpy()[:ran]
+    assert (ids_h >= 0).all(), "a timed step did not write its routing"
+    uniq = float(np.mean([len(np.unique(ids_h[r])) for r in range(ran)]))
+    step_bytes = shape.decode_bytes(uniq, batch)
+    value = samples[0]
+    med = float(np.median(samples))
+    achieved = step_bytes / (med * 1e-6) / 1e9
+    out = {
+        "value": round(value, 3),
+        "unit": "us/layer-step",
+        "us_per_step": med,
+        "distribution": {"median": round(med, 3), "p10": round(float(np.percentile(samples, 10)), 3),
+                         "p90": round(float(np.percentile(samples, 90)), 3), "replays": n_rep,
+                         "steps_per_replay": K, "timed_steps": n_rep * K,
+                         "note": "per-step time of each graph replay (K steps, event-timed)"},
+        "roofline": {"bound": "hbm", "kernel": "moe_fused" if path == "fused" else "three launches",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": int(step_bytes),
+                     "avg_launch_us": round(med, 3)},
+        "step_bytes": int(step_bytes),
+        "step_gbs": round(step_bytes / (value * 1e-6) / 1e9, 1),
+        "unique_experts_per_step": uniq,
+        "data": f"synthetic seeded weights (seed {args.seed}), {ran} distinct resident layers cycled by the "
+                f"{K} timed steps ({R} resident), bf16 x ~N(0,1), a distinct x per layer",
+        "config": {"workload": name, "hidden": shape.hidden, "experts": shape.experts, "top_k": shape.top_k,
+                   "moe_intermediate": shape.inter, "shared_intermediate": shape.shared_inter,
+                   "expert_bits": shape.expert_bits, "router_bits": shape.router_bits, "group": shape.group,
+                   "batch": batch, "replicas": R, "layers_cycled": ran, "path": path,
+                   "parallelism": "single GPU"},
+    }
+    if keep:
+        out["_keep"] = (layers, wss, calls, ids, wts, xs_bits)
+    else:
+        del graph, layers, wss, calls
+    return out
 
 
 MODEL_LAYERS = 40  # qwen3.6-35b: 30 DeltaNet layers, every 4th one full attention

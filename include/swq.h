@@ -48,7 +48,9 @@ enum {
     SWQ_ERR_LIMIT = -10,            /* batch / top_k above compiled maximum   */
     SWQ_ERR_MISSING_TENSOR = -11,   /* Checkpoint.Error.missingTensor         */
     SWQ_ERR_IO = -12,               /* a file could not be opened or read     */
-    SWQ_ERR_FORMAT = -13            /* malformed safetensors / JSON / qpack   */
+    SWQ_ERR_FORMAT = -13,           /* malformed safetensors / JSON / qpack   */
+    SWQ_ERR_STALLED = -14           /* a single-launch MoE call ran out of a
+                                       bounded wait (see swq_moe_workspace_status) */
 };
 
 /* Scale, bias and activation dtypes.  The values equal
@@ -412,6 +414,19 @@ size_t swq_moe_decode_workspace_bytes(const swq_moe_layer *layer, int batch);
  * workspace, outside stream capture; swq_moe_decode leaves it ready for the
  * next call. */
 int swq_moe_workspace_init(void *ws, size_t ws_bytes, void *stream);
+
+/* Whether every swq_moe_decode / swq_moe_decode_norm call on this workspace
+ * since the last cleared check completed normally: SWQ_OK, or
+ * SWQ_ERR_STALLED when one ran out of a bounded wait.  The single-launch
+ * (batch 1) kernel has one workgroup per CU and hands data between them
+ * through the workspace; it assumes the whole grid is resident at once,
+ * which holds on a device running nothing else.  If other work occupies
+ * CUs, a wait can last about a second and then give up, and that call's
+ * outputs are invalid (the reference throws, MetalEngine.swift:8-11;
+ * a stream-ordered call cannot, so the failure is recorded here).
+ * Blocking: waits for the stream's earlier work, then reads the record
+ * (one 4-byte copy) and, when clear != 0, resets it.  Not capturable. */
+int swq_moe_workspace_status(void *ws, size_t ws_bytes, int clear, void *stream);
 
 /* One MoE-layer decode step for `batch` independent tokens, entirely on the
  * device.  Batch 1 runs as one launch (router, softmax, top-k with ties to the

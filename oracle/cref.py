@@ -68,8 +68,12 @@ class CMoE:
         dense = lambda k: np.ascontiguousarray(R.dequantize(arrays[k][0], arrays[k][1], arrays[k][2],
                                                             arrays[k][3], group, R.F16))
         self.router = dense("router")
-        self.sh_gate, self.sh_up, self.sh_down = dense("sh_gate"), dense("sh_up"), dense("sh_down")
-        self.seg = dense("seg").reshape(-1)
+        self.has_shared = shared_inter > 0
+        if self.has_shared:
+            self.sh_gate, self.sh_up, self.sh_down = dense("sh_gate"), dense("sh_up"), dense("sh_down")
+            self.seg = dense("seg").reshape(-1)
+        else:  # never read: the C oracle skips the shared expert
+            self.sh_gate = self.sh_up = self.sh_down = self.seg = np.zeros(1, dtype=np.float32)
         self.gate = CStack(*arrays["gate"][:3], arrays["gate"][3], group)
         self.up = CStack(*arrays["up"][:3], arrays["up"][3], group)
         self.down = CStack(*arrays["down"][:3], arrays["down"][3], group)
@@ -84,7 +88,7 @@ class CMoE:
         w = np.empty((S, self.K), dtype=np.float32)
         p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
         st = load().oracle_moe_forward(
-            p(x), S, self.H, self.E, self.K, self.I, self.Is, int(self.norm), 1,
+            p(x), S, self.H, self.E, self.K, self.I, self.Is, int(self.norm), int(self.has_shared),
             p(self.router), ctypes.byref(self.gate.mat), ctypes.byref(self.up.mat), ctypes.byref(self.down.mat),
             p(self.sh_gate), p(self.sh_up), p(self.sh_down), p(self.seg), p(out), p(ids), p(w),
             p(self.scratch), threads)

@@ -24,6 +24,7 @@ SWQ_ERR_LIMIT = -10
 SWQ_ERR_MISSING_TENSOR = -11
 SWQ_ERR_IO = -12
 SWQ_ERR_FORMAT = -13
+SWQ_ERR_STALLED = -14
 
 SWQ_F32, SWQ_F16, SWQ_BF16 = 0, 1, 2
 SWQ_MAX_BATCH, SWQ_MAX_TOPK = 16, 16
@@ -151,6 +152,7 @@ SIGNATURES = {
     "swq_qpack_expert_linear": (_I, [_P, _P, _c.c_char_p, _c.POINTER(QLinear)]),
     "swq_moe_decode_workspace_bytes": (_SZ, [_c.POINTER(MoELayer), _I]),
     "swq_moe_workspace_init": (_I, [_P, _SZ, _P]),
+    "swq_moe_workspace_status": (_I, [_P, _SZ, _I, _P]),
     "swq_moe_decode": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _I, _P]),
     "swq_moe_decode_norm": (_I, [_c.POINTER(MoELayer), _P, _P, _P, _I, _c.c_float, _P, _P, _P, _P, _SZ, _P]),
     "swq_synth_u32": (_I, [_P, _I64, _U64, _U64, _I64, _P]),

@@ -17,6 +17,8 @@ extern "C" const char *swq_strerror(int status) {
         case SWQ_ERR_MISSING_TENSOR: return "tensor or section not found";
         case SWQ_ERR_IO: return "file open or read failed";
         case SWQ_ERR_FORMAT: return "malformed checkpoint, JSON or qpack layout";
+        case SWQ_ERR_STALLED:
+            return "a single-launch MoE call ran out of a bounded wait (workgroups not co-resident); its outputs are invalid";
         default: return "unknown status";
     }
 }

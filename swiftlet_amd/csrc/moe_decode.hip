@@ -521,6 +521,28 @@ __global__ __launch_bounds__(kStage3MaxWaves * 64) void moe_stage3(MoEArgs a) {
     }
 }
 
+// Zero-fills n bytes (a fill kernel rather than hipMemsetAsync, so that a
+// caller may also record it into a graph).
+__global__ void zero_bytes_kernel(uint8_t *p, size_t n) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+        const size_t n16 = n / 16;
+        for (size_t j = i; j < n16; j += stride) reinterpret_cast<uint4 *>(p)[j] = make_uint4(0, 0, 0, 0);
+        for (size_t j = n16 * 16 + i; j < n; j += stride) p[j] = 0;
+    } else {
+        for (size_t j = i; j < n; j += stride) p[j] = 0;
+    }
+}
+
+int zero_fill(void *p, size_t n, hipStream_t stream) {
+    if (n == 0) return SWQ_OK;
+    const size_t blocks = min(static_cast<size_t>(1024), (n / 16 + 255) / 256 + 1);
+    hipLaunchKernelGGL(zero_bytes_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       static_cast<uint8_t *>(p), n);
+    return launch_status();
+}
+
 // ---------------------------------------------------------------------------
 // host side
 
@@ -537,12 +559,29 @@ extern "C" int swq_moe_workspace_init(void *ws, size_t ws_bytes, void *stream) {
     if (!ws || ws_bytes < 256) return SWQ_ERR_WORKSPACE;
     const int st = fused_probe_device(static_cast<hipStream_t>(stream));
     if (st != SWQ_OK) return st;
-    return hip_status(hipMemsetAsync(ws, 0, ws_bytes, static_cast<hipStream_t>(stream)));
+    return zero_fill(ws, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t swq_moe_workspace_error_offset(const swq_moe_layer *layer, int batch) {
     if (check_layer(layer, batch, SWQ_BF16) != SWQ_OK) return 0;
-    return fused_err_offset(layer, ws_layout(layer, batch).total);
+    return kWsErrByte;
+}
+
+extern "C" int swq_moe_workspace_status(void *ws, size_t ws_bytes, int clear, void *stream) {
+    if (!ws || ws_bytes < 256) return SWQ_ERR_WORKSPACE;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint32_t *word = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(ws) + kWsErrByte);
+    uint32_t v = 0;
+    hipError_t e = hipMemcpyAsync(&v, word, 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return SWQ_ERR_HIP;
+    if (v != 0 && clear) {
+        const uint32_t zero = 0;
+        e = hipMemcpyAsync(word, &zero, 4, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) return SWQ_ERR_HIP;
+    }
+    return v != 0 ? SWQ_ERR_STALLED : SWQ_OK;
 }
 
 // stage_mask: bits 0-2 run the staged kernels' stages; SWQ_STAGES_FUSED

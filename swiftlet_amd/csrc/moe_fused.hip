@@ -845,7 +845,7 @@ int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int bat
     a.user_ids = topk_ids;
     a.user_w = topk_weights;
     a.gen = reinterpret_cast<uint32_t *>(wsb + fl.gen);
-    a.err = reinterpret_cast<uint32_t *>(wsb + fl.err);
+    a.err = reinterpret_cast<uint32_t *>(wsb + kWsErrByte);
     a.logit_x = reinterpret_cast<uint64_t *>(wsb + fl.logit_x);
     a.hsh_x = reinterpret_cast<uint64_t *>(wsb + fl.hsh_x);
     a.h_x = reinterpret_cast<uint64_t *>(wsb + fl.h_x);

@@ -7,6 +7,10 @@
 namespace swq {
 
 constexpr int kMaxExperts = 1024;
+// Byte offset, in the 256-byte workspace header, of the word the
+// single-launch path sets when one of its bounded waits runs out.
+constexpr size_t kWsErrByte = 64;
+int zero_fill(void *p, size_t n, hipStream_t stream);
 
 struct WsLayout {
     size_t header, logits, sg, h_sh, ids, wts, n_unique, uniq_e, uniq_np, uniq_pairs, h, total;
@@ -23,7 +27,7 @@ inline WsLayout ws_layout(const swq_moe_layer *l, int B) {
         return o;
     };
     const size_t P = static_cast<size_t>(B) * l->top_k;
-    w.header = take(256);  // reserved; zeroed by swq_moe_workspace_init
+    w.header = take(256);  // zeroed by swq_moe_workspace_init; word kWsErrByte/4: the stall record
     w.logits = take(static_cast<size_t>(B) * l->num_experts * 4);
     w.sg = take(static_cast<size_t>(B) * 4);
     w.h_sh = take(static_cast<size_t>(B) * (l->has_shared ? l->shared_intermediate : 1) * 4);

@@ -70,9 +70,17 @@ class MoELayerGPU:
     # -- decode --------------------------------------------------------
     def workspace_error(self, ws, batch: int = 1) -> int:
         """The word the single-launch path sets if one of its bounded waits ran
-        out (0 when every call so far completed normally)."""
+        out (0 when every call so far completed normally); leaves it as it is."""
         off = self.lib.swq_moe_workspace_error_offset(ctypes.byref(self._c), batch)
         return int(ws[off:off + 4].cpu().numpy().view(np.uint32)[0])
+
+    def workspace_status(self, ws, clear: bool = True, stream=None) -> int:
+        """swq_moe_workspace_status: SWQ_OK, or SWQ_ERR_STALLED when a call on
+        this workspace since the last check ran out of one of its bounded
+        waits (its outputs are then invalid).  Blocks until the stream's
+        earlier work is done; clears the record unless ``clear`` is False."""
+        return self.lib.swq_moe_workspace_status(ws.data_ptr(), ws.numel(), 1 if clear else 0,
+                                                 _stream_handle(stream))
 
     def decode(self, x, out=None, out_dtype=None, ws=None, accumulate: bool = False,
                topk_ids=None, topk_weights=None, stream=None, path: str = "auto"):
@@ -223,11 +231,14 @@ def synth_layer(shape: synth.MoEShape, seed: int, layer: int, device="cuda", str
     H, E, I, Is = shape.hidden, shape.experts, shape.inter, shape.shared_inter
     eb, rb, g = shape.expert_bits, shape.router_bits, shape.group
     mk = lambda kind, ex, rows, cols, bits: synth_linear(seed, layer, kind, ex, rows, cols, bits, g, device, stream)
+    sh = shape.has_shared
     return MoELayerGPU(
         router=mk("router", None, E, H, rb),
         gate=mk("gate", E, I, H, eb), up=mk("up", E, I, H, eb), down=mk("down", E, H, I, eb),
-        shared_gate=mk("sh_gate", None, Is, H, eb), shared_up=mk("sh_up", None, Is, H, eb),
-        shared_down=mk("sh_down", None, H, Is, eb), shared_expert_gate=mk("seg", None, 1, H, rb),
+        shared_gate=mk("sh_gate", None, Is, H, eb) if sh else None,
+        shared_up=mk("sh_up", None, Is, H, eb) if sh else None,
+        shared_down=mk("sh_down", None, H, Is, eb) if sh else None,
+        shared_expert_gate=mk("seg", None, 1, H, rb) if sh else None,
         top_k=shape.top_k, norm_topk_prob=shape.norm_topk_prob)
 
 
@@ -237,13 +248,14 @@ def host_layer_arrays(shape: synth.MoEShape, seed: int, layer: int, experts: lis
     stacked tensors to those expert ids (a dict per expert then)."""
     H, E, I, Is = shape.hidden, shape.experts, shape.inter, shape.shared_inter
     eb, rb, g = shape.expert_bits, shape.router_bits, shape.group
-    out = {
-        "router": synth.qmatrix(seed, layer, "router", None, E, H, rb, g) + (rb,),
-        "sh_gate": synth.qmatrix(seed, layer, "sh_gate", None, Is, H, eb, g) + (eb,),
-        "sh_up": synth.qmatrix(seed, layer, "sh_up", None, Is, H, eb, g) + (eb,),
-        "sh_down": synth.qmatrix(seed, layer, "sh_down", None, H, Is, eb, g) + (eb,),
-        "seg": synth.qmatrix(seed, layer, "seg", None, 1, H, rb, g) + (rb,),
-    }
+    out = {"router": synth.qmatrix(seed, layer, "router", None, E, H, rb, g) + (rb,)}
+    if shape.has_shared:
+        out.update({
+            "sh_gate": synth.qmatrix(seed, layer, "sh_gate", None, Is, H, eb, g) + (eb,),
+            "sh_up": synth.qmatrix(seed, layer, "sh_up", None, Is, H, eb, g) + (eb,),
+            "sh_down": synth.qmatrix(seed, layer, "sh_down", None, H, Is, eb, g) + (eb,),
+            "seg": synth.qmatrix(seed, layer, "seg", None, 1, H, rb, g) + (rb,),
+        })
     if experts is None:
         for kind, rows, cols in (("gate", I, H), ("up", I, H), ("down", H, I)):
             out[kind] = synth.qmatrix(seed, layer, kind, E, rows, cols, eb, g) + (eb,)

@@ -132,7 +132,13 @@ class MoEShape:
         H, I, b = self.hidden, self.inter, self.expert_bits
         return 2 * self.matrix_bytes(I, H, b) + self.matrix_bytes(H, I, b)
 
+    @property
+    def has_shared(self) -> bool:
+        return self.shared_inter > 0
+
     def shared_bytes(self) -> int:
+        if not self.has_shared:
+            return 0
         H, I, b = self.hidden, self.shared_inter, self.expert_bits
         return 2 * self.matrix_bytes(I, H, b) + self.matrix_bytes(H, I, b)
 
@@ -140,7 +146,7 @@ class MoEShape:
         return self.matrix_bytes(self.experts, self.hidden, self.router_bits)
 
     def seg_bytes(self) -> int:
-        return self.matrix_bytes(1, self.hidden, self.router_bits)
+        return self.matrix_bytes(1, self.hidden, self.router_bits) if self.has_shared else 0
 
     def decode_bytes(self, unique_experts: int, batch: int = 1) -> int:
         """Algorithmic HBM bytes of one decode step: every matrix touched once
@@ -153,6 +159,10 @@ SHAPES = {
     "qwen3.6-35b-a3b-q4": MoEShape("qwen3.6-35b-a3b-q4", 2048, 256, 8, 512, 512, 4),
     "qwen3-next-80b-a3b-q4": MoEShape("qwen3-next-80b-a3b-q4", 2048, 512, 10, 512, 512, 4),
     "qwen3.6-35b-a3b-q8": MoEShape("qwen3.6-35b-a3b-q8", 2048, 256, 8, 512, 512, 8),
+    # one routed SwiGLU expert at the 35B shape (x [2048], gate/up [512 x 2048],
+    # down [2048 x 512], 4-bit): a one-expert router (1 x 2048, 8-bit) picks it
+    # with weight 1, no shared expert
+    "single-expert-q4": MoEShape("single-expert-q4", 2048, 1, 1, 512, 0, 4),
 }
 
 

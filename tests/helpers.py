@@ -70,15 +70,16 @@ def qlin(seed, layer, kind, rows, cols, bits, group) -> R.QLinear:
 def ref_layer(shape: synth.MoEShape, seed: int, layer: int) -> R.MoELayerRef:
     H, E, I, Is = shape.hidden, shape.experts, shape.inter, shape.shared_inter
     eb, rb, g = shape.expert_bits, shape.router_bits, shape.group
+    sh = shape.has_shared
     return R.MoELayerRef(
         router=qlin(seed, layer, "router", E, H, rb, g),
         gate=LazyStack(seed, layer, "gate", E, I, H, eb, g),
         up=LazyStack(seed, layer, "up", E, I, H, eb, g),
         down=LazyStack(seed, layer, "down", E, H, I, eb, g),
-        shared_gate=qlin(seed, layer, "sh_gate", Is, H, eb, g),
-        shared_up=qlin(seed, layer, "sh_up", Is, H, eb, g),
-        shared_down=qlin(seed, layer, "sh_down", H, Is, eb, g),
-        shared_expert_gate=qlin(seed, layer, "seg", 1, H, rb, g),
+        shared_gate=qlin(seed, layer, "sh_gate", Is, H, eb, g) if sh else None,
+        shared_up=qlin(seed, layer, "sh_up", Is, H, eb, g) if sh else None,
+        shared_down=qlin(seed, layer, "sh_down", H, Is, eb, g) if sh else None,
+        shared_expert_gate=qlin(seed, layer, "seg", 1, H, rb, g) if sh else None,
         top_k=shape.top_k, norm_topk_prob=shape.norm_topk_prob)
 
 

@@ -39,7 +39,7 @@ def test_exports_every_declared_symbol(lib):
 
 def test_strerror_and_version(lib):
     assert lib.swq_version() >= 100
-    for code in range(0, -11, -1):
+    for code in range(0, -15, -1):
         s = lib.swq_strerror(code).decode()
         assert s and s != "unknown status", code
     assert lib.swq_strerror(-99).decode() == "unknown status"
@@ -61,6 +61,17 @@ def layer(H=2048, E=256, K=8, I=512, Is=512, bits=4, rbits=8, **kw):
              shared_intermediate=Is, norm_topk_prob=1, has_shared=1, reserved=0)
     d.update(kw)
     return MoELayer(**d)
+
+
+def test_workspace_status_validation(lib):
+    """The stall record of the single-launch path sits in the workspace
+    header at a fixed offset; the query rejects a missing or short
+    workspace before touching a device."""
+    assert lib.swq_moe_workspace_status(None, 1 << 20, 1, None) == _lib.SWQ_ERR_WORKSPACE
+    assert lib.swq_moe_workspace_status(FAKE, 255, 1, None) == _lib.SWQ_ERR_WORKSPACE
+    L = layer()
+    assert lib.swq_moe_workspace_error_offset(ctypes.byref(L), 1) == 64
+    assert lib.swq_strerror(_lib.SWQ_ERR_STALLED).decode().startswith("a single-launch MoE call")
 
 
 def test_workspace_query(lib):

@@ -95,6 +95,18 @@ def test_prefill_odd_shapes(E, K, I, Is, H, bits, norm, T):
     _check(shape, xf, out, ids.cpu().numpy(), w.cpu().numpy(), seed=77)
 
 
+def test_prefill_without_shared_expert():
+    """has_shared = 0: no shared tiles, no shared-gate logit (QwenCPUModel.swift:559-566)."""
+    import torch
+    shape = synth.MoEShape("no-shared", 2048, 256, 8, 512, 0, 4)
+    print("prefill without a shared expert, T=24", flush=True)
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    x, xf = _x(helpers.SEED + 77, 24, shape.hidden)
+    out, ids, w = gpu.prefill(x)
+    torch.cuda.synchronize()
+    _check(shape, xf, out, ids.cpu().numpy(), w.cpu().numpy(), rows=[0, 11, 23])
+
+
 def test_prefill_f32_x_bf16_out():
     import torch
     shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
