@@ -1,0 +1,837 @@
+// MoE-layer decode step for one token in a single launch on gfx950.
+//
+// One workgroup of four waves (one wave per SIMD) per CU, launched as an
+// ordinary kernel: on a device with no other work the whole grid is resident
+// at once, and a grid of four-wave workgroups, one per CU, has every wave
+// running within ~0.7 us of the launch (eight-wave workgroups take ~2.4 us
+// to start on MI355X, measured).  The stages hand data to each other through
+// the workspace instead of kernel boundaries: every value crossing
+// workgroups is one 8-byte word (fp32 value, call epoch), written and polled
+// with relaxed device-scope atomics, so a consumer polls the data itself and
+// needs no separate flag, fence or cache write-back.
+//
+// Workgroup b belongs to XCD group grp = b mod 8 (the hardware hands
+// workgroups to the eight XCDs round robin; checked once per device) with
+// rank b / 8 inside it.  Group grp owns routed slots grp, grp + 8, ...: their
+// gate/up rows, the SwiGLU activations between them (exchanged inside the
+// XCD's L2) and their down rows.
+//
+//   phase A  (routing-independent, from the first instruction) router rows,
+//            one pass of rows per wave, -> logits, written to one replica
+//            per XCD group; shared-expert gate/up rows -> SwiGLU
+//            activations; the shared-expert gate logit (every workgroup, for
+//            its own combine); then the shared expert's down rows of the
+//            workgroup's own output rows.
+//   routing  wave 0 polls its replica of the logits and runs the top-k
+//            rounds; each pick goes to LDS the moment its round ends, so a
+//            group starts loading its expert's rows after round grp + 1
+//            while the other groups' rounds continue: the routed weight
+//            stream is spread over the rounds instead of waiting for all of
+//            them.  The rounds of picks the workgroup does not own, and the
+//            combine weights, finish after its routed work.
+//   routed   per owned slot: gate/up rows (+ SwiGLU) -> activations in the
+//            XCD's L2; the slot's activations -> LDS (each wave polls a
+//            quarter); down rows (their loads issued with the gate/up
+//            loads) -> partial outputs, one word per (slot, output row).
+//   combine  the workgroup's output rows: routed partials in pick order,
+//            then the gated shared expert (+ the residual stream).
+//
+// Numerics are those of the staged kernels (QwenCPUModel.moeForward,
+// QwenCPUModel.swift:500-569): the same lane plans, per-row reductions and
+// summation orders, so both paths agree bit for bit.
+//
+// Epochs: workgroup b keeps gen[b] (written only by itself); every call
+// increments all of them, so every workgroup derives the same epoch
+// g = gen[b] + 1 without communicating, and stale words of earlier calls
+// never match.  Every wait is bounded (about a second); one that runs out
+// records itself in the workspace header (swq_moe_workspace_status) and the
+// workgroup carries on.
+#pragma once
+
+#include "../../include/swq_bench.h"
+#include "moe_host.hpp"
+#include "route.hpp"
+#include "tile.hpp"
+
+#include <utility>
+
+// Phase stamps for timing studies: SWQ_FUSED_TRACE builds record
+// s_memrealtime per (workgroup, wave, point); product builds compile them out.
+#ifdef SWQ_FUSED_TRACE
+static __device__ unsigned long long g_swq_fused_trace[1024 * 4 * 16];
+// host access to one translation unit's stamps (the array is per code object)
+#define SWQ_TRACE_ACCESSOR(name)                                                                        \
+    extern "C" int name(void *host, size_t bytes, int clear) {                                          \
+        if (clear) {                                                                                    \
+            static unsigned long long z[1024 * 4 * 16];                                                 \
+            return hipMemcpyToSymbol(HIP_SYMBOL(g_swq_fused_trace), z, sizeof(z)) == hipSuccess ? 0 : -1; \
+        }                                                                                               \
+        return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_swq_fused_trace), bytes) == hipSuccess ? 0 : -1;  \
+    }
+#define SWQ_STAMP(n)                                                                                  \
+    do {                                                                                              \
+        if ((threadIdx.x & 63) == 0)                                                                  \
+            g_swq_fused_trace[(blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + (n)] =                     \
+                __builtin_amdgcn_s_memrealtime();                                                     \
+    } while (0)
+#else
+#define SWQ_STAMP(n) \
+    do {             \
+    } while (0)
+#endif
+
+namespace swq {
+
+constexpr int kFusedWaves = 4;
+constexpr int kFusedThreads = kFusedWaves * kWave;
+constexpr int kGroups = 8;
+constexpr int kFusedMaxBlocks = 1024;      // gen[] entries kept in step
+constexpr int kReplicas = kGroups;         // logit replicas (one per XCD group)
+constexpr int kMaxInterFused = 2048;       // activations of one slot
+constexpr int kMaxCombineRows = 16;        // output rows per workgroup
+constexpr int kPrenormMaxHidden = 4096;    // hidden size the folded-in norm holds in LDS
+constexpr uint32_t kSpinLimit = 1u << 20;  // polls of ~0.1-1 us each: about a second
+
+struct FusedArgs {
+    QMat router, gate, up, down, sh_gate, sh_up, sh_down, seg;
+    const void *x;
+    void *out;
+    int32_t *user_ids;
+    float *user_w;
+    uint32_t *gen;      // [kFusedMaxBlocks]
+    uint32_t *err;      // the workspace's stall record
+    uint64_t *logit_x;  // [kReplicas][rep_stride] (logit, epoch)
+    uint64_t *hsh_x;    // [Is] shared SwiGLU activations
+    uint64_t *h_x;      // [K][I] routed SwiGLU activations
+    uint64_t *part_x;   // [K][H] routed down outputs
+    int32_t rep_stride;
+    int32_t odt, accumulate;
+    int32_t H, E, K, I, Is, norm, has_shared;
+    int32_t nb;
+    int32_t sh_tiles;   // shared gate/up tiles (one pass of rows each)
+    int32_t gu_tpe;     // routed gate/up tiles per slot
+    int32_t dn_tpe;     // routed down tiles per slot
+    int32_t local;      // a group's workgroups share an XCD (verified on the host)
+    int32_t rows_cmb;   // output rows combined per workgroup
+    // the layer's post-attention norm folded in (the PN kernels):
+    // x = rmsnorm(h_in + res_in) * norm_w, out = (h_in + res_in) + moe(x)
+    const float *h_in, *res_in;
+    const void *norm_w;
+    int32_t norm_dtype;
+    float norm_eps;
+};
+
+// ---------------------------------------------------------------------------
+// kernel arguments: the compiler loads them lazily, each scalar load followed
+// by a wait, so a phase that first touches a matrix descriptor pays a round
+// trip per line.  One scalar load per 64-byte line of the argument block,
+// all issued before a single wait, brings it into the scalar cache up front.
+// The loads and the wait are one asm statement with a distinct output per
+// load: scalar loads complete out of order, and a destination register the
+// compiler considered free before the wait could be overwritten by a load
+// still in flight (outputs are early-clobber, so none shares the base).
+__device__ __forceinline__ void prefetch_kernargs() {
+    static_assert(sizeof(FusedArgs) > 896 && sizeof(FusedArgs) <= 960, "fifteen 64-byte lines");
+    const auto *kp = __builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t d0, d1, d2, d3, d4, d5, d6, d7, d8, d9, d10, d11, d12, d13, d14;
+    asm volatile(
+        "s_load_dword %0, %15, 0x0\n\ts_load_dword %1, %15, 0x40\n\t"
+        "s_load_dword %2, %15, 0x80\n\ts_load_dword %3, %15, 0xc0\n\t"
+        "s_load_dword %4, %15, 0x100\n\ts_load_dword %5, %15, 0x140\n\t"
+        "s_load_dword %6, %15, 0x180\n\ts_load_dword %7, %15, 0x1c0\n\t"
+        "s_load_dword %8, %15, 0x200\n\ts_load_dword %9, %15, 0x240\n\t"
+        "s_load_dword %10, %15, 0x280\n\ts_load_dword %11, %15, 0x2c0\n\t"
+        "s_load_dword %12, %15, 0x300\n\ts_load_dword %13, %15, 0x340\n\t"
+        "s_load_dword %14, %15, 0x380\n\ts_waitcnt lgkmcnt(0)"
+        : "=&s"(d0), "=&s"(d1), "=&s"(d2), "=&s"(d3), "=&s"(d4), "=&s"(d5), "=&s"(d6), "=&s"(d7), "=&s"(d8),
+          "=&s"(d9), "=&s"(d10), "=&s"(d11), "=&s"(d12), "=&s"(d13), "=&s"(d14)
+        : "s"(kp)
+        : "memory");
+}
+
+// ---------------------------------------------------------------------------
+// (value, epoch) words
+
+__device__ __forceinline__ uint64_t pack_pair(float v, uint32_t g) {
+    return (static_cast<uint64_t>(g) << 32) | __float_as_uint(v);
+}
+
+__device__ __forceinline__ void put_pair(uint64_t *p, float v, uint32_t g) {
+    __hip_atomic_store(p, pack_pair(v, g), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A word for readers on this XCD only: a plain store, which stays in the
+// XCD's L2, where their device-scope loads find it.  Used only when the host
+// has verified that a group's workgroups share an XCD.
+__device__ __forceinline__ void put_pair_group(uint64_t *p, float v, uint32_t g, int local) {
+    if (local) __hip_atomic_store(p, pack_pair(v, g), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else __hip_atomic_store(p, pack_pair(v, g), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t get_pair(const uint64_t *p) {
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void record_stall(uint32_t *err, uint32_t bit) {
+    __hip_atomic_fetch_or(err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Each lane waits for its N words p[c] (where live[c]) to carry epoch g and
+// returns their values.  All loads of a round are in flight together; a lane
+// stops loading a word once it is valid.
+template <int N>
+__device__ __forceinline__ void poll_words(const uint64_t *const (&p)[N], const bool (&live)[N], uint32_t g,
+                                           float (&v)[N], uint32_t *err, uint32_t bit) {
+    bool pend[N];
+#pragma unroll
+    for (int c = 0; c < N; ++c) {
+        pend[c] = live[c];
+        v[c] = 0.f;
+    }
+    for (uint32_t it = 0;; ++it) {
+        uint64_t w[N];
+#pragma unroll
+        for (int c = 0; c < N; ++c) w[c] = pend[c] ? get_pair(p[c]) : 0;
+        bool any = false;
+#pragma unroll
+        for (int c = 0; c < N; ++c) {
+            if (pend[c] && static_cast<uint32_t>(w[c] >> 32) == g) {
+                v[c] = __uint_as_float(static_cast<uint32_t>(w[c]));
+                pend[c] = false;
+            }
+            any = any || pend[c];
+        }
+        if (__ballot(any) == 0) return;
+        if (it > kSpinLimit) {
+            if ((threadIdx.x & 63) == 0) record_stall(err, bit);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Bounded wait until the LDS word becomes non-negative; returns it (0 if the
+// wait ran out).
+__device__ __forceinline__ int32_t wait_lds_nonneg(int32_t *p, uint32_t *err) {
+    for (uint32_t it = 0;; ++it) {
+        const int32_t v = __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (v >= 0) return v;
+        if (it > kSpinLimit) {
+            if ((threadIdx.x & 63) == 0) record_stall(err, 4u);
+            return 0;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One tile's row dot products through dot_tiles (chunks interleaved).
+template <int BITS, int CPL, int ES, int XF, int RI>
+__device__ __forceinline__ void dot_rows(float (&res)[RI], const RowTile<BITS, CPL, ES, RI> &rt, const QMat &m,
+                                         const XSlice<BITS, CPL, XF> &xs, const LaneMap &lm) {
+    const RowTile<BITS, CPL, ES, RI> *tiles[1] = {&rt};
+    const QMat *mats[1] = {&m};
+    float r[1][RI];
+    dot_tiles<1>(r, tiles, mats, xs, lm);
+#pragma unroll
+    for (int i = 0; i < RI; ++i) res[i] = r[0][i];
+}
+
+// The gate and up tiles' row dot products, their chunks interleaved.
+template <int BITS, int CPL, int ES, int XF, int RI>
+__device__ __forceinline__ void dot_rows2(float (&rg)[RI], float (&ru)[RI], const RowTile<BITS, CPL, ES, RI> &tg,
+                                          const RowTile<BITS, CPL, ES, RI> &tu, const QMat &mg, const QMat &mu,
+                                          const XSlice<BITS, CPL, XF> &xs, const LaneMap &lm) {
+    const RowTile<BITS, CPL, ES, RI> *tiles[2] = {&tg, &tu};
+    const QMat *mats[2] = {&mg, &mu};
+    float r[2][RI];
+    dot_tiles<2>(r, tiles, mats, xs, lm);
+#pragma unroll
+    for (int i = 0; i < RI; ++i) {
+        rg[i] = r[0][i];
+        ru[i] = r[1][i];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// activations in LDS for the down rows
+//
+// 4-bit down rows take each fp32 activation as hi = bf16(x), lo = bf16(x -
+// hi) in pair words (the kXBF16X2 format): chunk c (32 activations) is words
+// [32c, 32c + 32), its eight 16-byte groups (hi words 0-3, 4-7, 8-11, 12-15,
+// then lo) with group i stored at (i + c) mod 8, so the lanes of a down tile,
+// which read chunk j each, spread over the LDS banks.  Pair p of the
+// activations (p < n/2) is {x[e], x[e + 4]}, e = 32(p/16) + 8((p%16)/4) +
+// p%4.  8-bit down rows take the fp32 activations as they are (pair p =
+// {x[2p], x[2p + 1]}).
+__device__ __forceinline__ int x2_word(int c, int grp16, int d) { return 32 * c + 4 * ((grp16 + c) & 7) + d; }
+
+template <int DB>
+__device__ __forceinline__ int pair_first(int p) {
+    if constexpr (DB == 4) return 32 * (p >> 4) + 8 * ((p & 15) >> 2) + (p & 3);
+    else return 2 * p;
+}
+
+template <int DB>
+__device__ __forceinline__ int pair_second(int p) {
+    if constexpr (DB == 4) return pair_first<4>(p) + 4;
+    else return 2 * p + 1;
+}
+
+template <int DB>
+__device__ __forceinline__ void store_pair_lds(uint32_t *buf, int p, float x0, float x1) {
+    if constexpr (DB == 4) {
+        uint32_t hi, lo;
+        split_pair(x0, x1, hi, lo);
+        const int c = p >> 4, w = p & 15;
+        buf[x2_word(c, w >> 2, w & 3)] = hi;
+        buf[x2_word(c, 4 + (w >> 2), w & 3)] = lo;
+    } else {
+        buf[2 * p] = __float_as_uint(x0);
+        buf[2 * p + 1] = __float_as_uint(x1);
+    }
+}
+
+// Pairs [p0, p1) of the activation words at src into LDS, polled by one
+// wave, two pairs per lane and round.
+template <int DB>
+__device__ __forceinline__ void fetch_acts(const uint64_t *src, int p0, int p1, uint32_t g, uint32_t *buf, int lane,
+                                           uint32_t *err) {
+    for (int q = p0; q < p1; q += 2 * kWave) {
+        const uint64_t *pp[4];
+        bool live[4];
+        int pr[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            pr[c] = q + c * kWave + lane;
+            live[2 * c] = live[2 * c + 1] = pr[c] < p1;
+            const int pc = min(pr[c], p1 - 1);
+            pp[2 * c] = src + pair_first<DB>(pc);
+            pp[2 * c + 1] = src + pair_second<DB>(pc);
+        }
+        float v[4];
+        poll_words<4>(pp, live, g, v, err, 1u);
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+            if (live[2 * c]) store_pair_lds<DB>(buf, pr[c], v[2 * c], v[2 * c + 1]);
+    }
+}
+
+// Dot products of a down tile with the activations in LDS.
+template <int DB, int DRI>
+__device__ __forceinline__ void down_dot(float (&res)[DRI], const RowTile<DB, 1, 2, DRI> &dt, const QMat &m,
+                                         const LaneMap &lm, const uint32_t *buf) {
+    const int c = min(lm.j, m.chunks - 1);
+    if constexpr (DB == 4) {
+        XSlice<4, 1, kXBF16X2> xs;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 h = *reinterpret_cast<const uint4 *>(buf + x2_word(c, i, 0));
+            const uint4 l = *reinterpret_cast<const uint4 *>(buf + x2_word(c, 4 + i, 0));
+            xs.hi[0][4 * i] = h.x;
+            xs.hi[0][4 * i + 1] = h.y;
+            xs.hi[0][4 * i + 2] = h.z;
+            xs.hi[0][4 * i + 3] = h.w;
+            xs.lo[0][4 * i] = l.x;
+            xs.lo[0][4 * i + 1] = l.y;
+            xs.lo[0][4 * i + 2] = l.z;
+            xs.lo[0][4 * i + 3] = l.w;
+        }
+        xs.sum[0] = pair_sum(xs.hi[0], xs.lo[0]);
+        dot_rows(res, dt, m, xs, lm);
+    } else {
+        XSlice<8, 1, kXF32> xs;
+        const float4 *p = reinterpret_cast<const float4 *>(buf + c * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = p[i];
+            xs.v[0][4 * i] = v.x;
+            xs.v[0][4 * i + 1] = v.y;
+            xs.v[0][4 * i + 2] = v.z;
+            xs.v[0][4 * i + 3] = v.w;
+        }
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s += xs.v[0][i];
+        xs.sum[0] = s;
+        dot_rows(res, dt, m, xs, lm);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// routing: the top-k rounds on one wave with the keys in registers
+//
+// Lane l holds experts l*M .. l*M+M-1, sorted by (logit desc, id asc) with a
+// stable odd-even transposition sort.  Each round takes the wave-wide
+// maximum head; the lowest lane holding it wins (lower lanes hold lower
+// ids) and pops its head.  Selection by logit with ties to the lower id
+// equals the reference's selection by probability (QwenCPUModel.swift:
+// 508-522) except where two distinct logits give the same fp32 probability.
+
+template <int M>
+struct Rounds {
+    uint32_t key[M];
+    int32_t jj[M];
+    float lg[M];        // the lane's logits in expert order (-inf past E)
+    uint32_t my_key;    // lane k: the key of pick k
+    uint32_t top_key;   // the largest key
+    int done;           // rounds finished
+};
+
+template <int CTRL, int RM>
+__device__ __forceinline__ uint32_t dpp_max_step(uint32_t v) {
+    return max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, RM, 0xF, false)));
+}
+
+// The maximum over the wave, read from lane 63.
+__device__ __forceinline__ uint32_t wave_max_bcast(uint32_t v) {
+    v = dpp_max_step<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    v = dpp_max_step<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    v = dpp_max_step<0x141, 0xF>(v);  // row_half_mirror
+    v = dpp_max_step<0x140, 0xF>(v);  // row_mirror
+    v = dpp_max_step<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+    v = dpp_max_step<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+template <int M>
+__device__ __forceinline__ void rounds_init(Rounds<M> &r, const float (&v)[M], int E, int lane) {
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+        const bool valid = lane * M + j < E;
+        r.lg[j] = valid ? v[j] : -INFINITY;
+        r.key[j] = valid ? orderable(v[j]) : 0u;
+        r.jj[j] = j;
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+#pragma unroll
+        for (int j = i & 1; j + 1 < M; j += 2) {
+            const bool sw = r.key[j] < r.key[j + 1];
+            const uint32_t k0 = r.key[j], k1 = r.key[j + 1];
+            const int32_t i0 = r.jj[j], i1 = r.jj[j + 1];
+            r.key[j] = sw ? k1 : k0;
+            r.key[j + 1] = sw ? k0 : k1;
+            r.jj[j] = sw ? i1 : i0;
+            r.jj[j + 1] = sw ? i0 : i1;
+        }
+    }
+    r.my_key = 0;
+    r.top_key = 0;
+    r.done = 0;
+}
+
+// Rounds up to (not including) `upto`; pick k goes to s_ids[k] the moment
+// its round ends.
+template <int M>
+__device__ __forceinline__ void rounds_run(Rounds<M> &r, int upto, int lane, int32_t *s_ids) {
+    for (int k = r.done; k < upto; ++k) {
+        const uint32_t gmax = wave_max_bcast(r.key[0]);
+        const uint64_t cand = __ballot(r.key[0] == gmax);
+        const int wl = static_cast<int>(__builtin_ctzll(cand));
+        const int32_t e = wl * M + __builtin_amdgcn_readlane(r.jj[0], wl);
+        if (lane == 0) __hip_atomic_store(&s_ids[k], e, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (k == 0) r.top_key = gmax;
+        r.my_key = lane == k ? gmax : r.my_key;
+        const bool pop = lane == wl;
+#pragma unroll
+        for (int j = 0; j + 1 < M; ++j) {
+            r.key[j] = pop ? r.key[j + 1] : r.key[j];
+            r.jj[j] = pop ? r.jj[j + 1] : r.jj[j];
+        }
+        r.key[M - 1] = pop ? 0u : r.key[M - 1];
+    }
+    r.done = max(r.done, upto);
+}
+
+// Combine weights: p_k = exp(l_k - max) / sum_e exp(l_e - max) (:65-71),
+// w_k = p_k / sum_j p_j when norm (:546-550); the staged path's sums in the
+// same order.
+template <int M>
+__device__ __forceinline__ float rounds_weight(const Rounds<M> &r, int K, int norm, int lane) {
+    const float top = from_orderable(r.top_key);
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < M; ++j) part += expf(r.lg[j] - top);  // -inf padding adds 0
+    const float denom = wave_sum_all(part);
+    const float pk = lane < K ? expf(from_orderable(r.my_key) - top) / denom : 0.f;
+    const float total = wave_sum_all(pk);
+    return norm ? pk / total : pk;
+}
+
+// ---------------------------------------------------------------------------
+// the kernel.  XDT activation dtype; GB/GC/GX/GRI the gate/up format (bits,
+// chunks per lane, activation format) and passes per tile; DB/DRI the down
+// rows' bits (routed and shared alike) and passes per tile; RC chunks per
+// lane of the 8-bit router and shared-expert gate rows; M logits per lane
+// of the routing wave.
+
+template <int XDT, int GB, int GC, int GX, int GRI, int DB, int DRI, int RC, int M, bool PN>
+__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void moe_fused(FusedArgs a) {
+    __shared__ int32_t s_ids[SWQ_MAX_TOPK];
+    __shared__ float s_w[SWQ_MAX_TOPK];
+    __shared__ __attribute__((aligned(16))) uint32_t s_hb[kMaxInterFused];   // a routed slot's activations
+    __shared__ __attribute__((aligned(16))) uint32_t s_hsh[kMaxInterFused];  // the shared expert's
+    __shared__ float s_cmb[SWQ_MAX_TOPK * kMaxCombineRows];
+    __shared__ float s_shd[kMaxCombineRows];  // shared-expert down rows of the combine rows
+    __shared__ float s_sg;                    // shared-expert gate logit
+    __shared__ int32_t s_arrive;              // waves with their third of the shared activations in
+    __shared__ __attribute__((aligned(16))) float s_x[PN ? kPrenormMaxHidden : 4];  // the normalised input
+    __shared__ float s_red[kFusedWaves];
+
+    static_assert(sizeof(FusedArgs) <= 1024, "kernel arguments");
+    prefetch_kernargs();
+    SWQ_STAMP(0);
+    const int wave = threadIdx.x >> 6;
+    // Each phase takes the lane index through an empty asm: its per-lane
+    // address arithmetic then cannot be hoisted to the top of the kernel,
+    // where it would stay live across the earlier phases.
+    int lane = threadIdx.x & 63;
+    const int b = blockIdx.x, NB = a.nb;
+    const int grp = b % kGroups, rank = b / kGroups, NPG = NB / kGroups;
+    if (threadIdx.x < SWQ_MAX_TOPK) s_ids[threadIdx.x] = -1;
+    if (threadIdx.x == 0) s_arrive = 0;
+    const void *x = a.x;
+    if constexpr (PN) {
+        // the post-attention RMSNorm of the layer, per workgroup into LDS:
+        // s_x = (h_in + res_in) * (scale * w) (QwenCPUModel.rmsNorm and the
+        // residual add before it, QwenCPUModel.swift:47-59, :276-277); one
+        // round trip, indices clamped, values past H masked
+        constexpr int kPer = kPrenormMaxHidden / kFusedThreads;
+        const bool has_r = a.res_in != nullptr, wf32 = a.norm_dtype == SWQ_F32;
+        const float *rp = has_r ? a.res_in : a.h_in;
+        float hr[kPer], rr[kPer];
+        uint32_t wr[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int ic = min(static_cast<int>(threadIdx.x) + k * kFusedThreads, a.H - 1);
+            hr[k] = a.h_in[ic];
+            rr[k] = rp[ic];
+            wr[k] = wf32 ? static_cast<const uint32_t *>(a.norm_w)[ic] : static_cast<const uint16_t *>(a.norm_w)[ic];
+        }
+        float v[kPer], wv[kPer];
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const bool valid = static_cast<int>(threadIdx.x) + k * kFusedThreads < a.H;
+            v[k] = valid ? (has_r ? hr[k] + rr[k] : hr[k]) : 0.f;
+            wv[k] = wf32 ? __uint_as_float(wr[k])
+                         : (a.norm_dtype == SWQ_BF16 ? bf16_to_f32(static_cast<uint16_t>(wr[k]))
+                                                     : f16_to_f32(static_cast<uint16_t>(wr[k])));
+            ss += v[k] * v[k];
+        }
+        ss = wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int i = 0; i < kFusedWaves; ++i) tot += s_red[i];
+        const float sc = 1.0f / __fsqrt_rn(tot / static_cast<float>(a.H) + a.norm_eps);
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int i = threadIdx.x + k * kFusedThreads;
+            if (i < a.H) s_x[i] = v[k] * (sc * wv[k]);
+        }
+        x = s_x;
+    }
+    __syncthreads();
+    const int r0 = b * a.rows_cmb;                      // this workgroup's output rows
+    const int nr = max(0, min(a.rows_cmb, a.H - r0));
+
+    // ---- phase A ------------------------------------------------------------
+    // Every load first (weights, then activations), conversions after: the
+    // router row is on the critical path, and a conversion between two loads
+    // would make the second wait for the first.
+    asm volatile("" : "+v"(lane));
+    const LaneMap lmg = lane_map(a.gate.lpr_log2, lane);
+    const LaneMap lmr = lane_map(a.router.lpr_log2, lane);
+    const int t_r = b + NB * wave;                            // first router tile of this wave
+    const bool has_r = t_r * lmr.rpw < a.E;
+    const bool do_seg = a.has_shared && wave == 1;
+    const int t_s = b + NB * (kFusedWaves - 1 - wave);        // first shared gate/up tile
+    const bool has_s = a.has_shared && t_s < a.sh_tiles;
+    RowTile<8, RC, 2, 1> rt;
+    if (has_r) load_tile(rt, a.router, 0, lmr, t_r * lmr.rpw, a.E);
+    else if (do_seg) load_tile(rt, a.seg, 0, lmr, 0, 1);
+    RowTile<GB, GC, 2, 1> stg, stu;
+    if (has_s) {
+        load_tile(stg, a.sh_gate, 0, lmg, t_s * lmg.rpw, a.Is);
+        load_tile(stu, a.sh_up, 0, lmg, t_s * lmg.rpw, a.Is);
+    }
+    // the shared expert's down tile of this workgroup's output rows (wave 1),
+    // held until the shared activations are in
+    // the shared expert's down rows of this workgroup's output rows: one
+    // pass of rows each for waves 1-3, loaded now, used once the shared
+    // activations are in
+    const LaneMap lms = lane_map(a.sh_down.lpr_log2, lane);
+    const bool sh_rows = a.has_shared && nr > 0;
+    const int sh_passes = sh_rows ? (nr + lms.rpw - 1) / lms.rpw : 0;
+    const int sp0 = wave - 1;
+    RowTile<DB, 1, 2, 1> sdt;
+    if (wave >= 1 && sp0 < sh_passes) load_tile(sdt, a.sh_down, 0, lms, r0 + sp0 * lms.rpw, r0 + nr);
+    XRaw<XDT, 8, RC> xrr;
+    if (has_r || do_seg) load_xraw<XDT>(xrr, a.router, lmr, x, 0);
+    XRaw<XDT, GB, GC> xgr;
+    load_xraw<XDT>(xgr, a.gate, lmg, x, 0);
+    // The call's epoch, loaded after every other load of phase A: vector
+    // loads complete in issue order, so the first wait for it waits for them
+    // too, which the router row needs anyway; issued first, any wait for it
+    // after the roles' branches would drain every load.
+    asm volatile("" ::: "memory");
+    const uint32_t g = __hip_atomic_load(a.gen + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    if (has_r || do_seg) {
+        XSlice<8, RC, kXF32> xr;
+        xslice_convert(xr, xrr);
+        for (int t = t_r; t * lmr.rpw < a.E; t += NB * kFusedWaves) {
+            // router tiles t_r, t_r + 4 NB, ...: one pass of rows each -> logits
+            if (t != t_r) load_tile(rt, a.router, 0, lmr, t * lmr.rpw, a.E);
+            float res[1];
+            dot_rows(res, rt, a.router, xr, lmr);
+            const int row = t * lmr.rpw + lmr.q;
+            if (lmr.j == lmr.lpr - 1 && row < a.E) {
+#pragma unroll
+                for (int r = 0; r < kReplicas; ++r) put_pair(a.logit_x + r * a.rep_stride + row, res[0], g);
+            }
+            SWQ_STAMP(10);
+        }
+        if (do_seg) {
+            // the shared-expert gate logit <w_sg, x> (this workgroup's combine)
+            if (has_r) load_tile(rt, a.seg, 0, lmr, 0, 1);
+            float res[1];
+            dot_rows(res, rt, a.seg, xr, lmr);
+            if (lane == lmr.lpr - 1) s_sg = res[0];
+        }
+    }
+    // activations in the gate/up format (shared and routed rows), held for
+    // the whole call
+    XSlice<GB, GC, GX> xg;
+    xslice_convert(xg, xgr);
+    asm volatile("" : "+v"(lane));
+    for (int t = t_s; has_s && t < a.sh_tiles; t += NB * kFusedWaves) {
+        // shared-expert gate/up tiles t_s, t_s + 4 NB, ...: SwiGLU activations
+        const int row0 = t * lmg.rpw;
+        if (t != t_s) {
+            load_tile(stg, a.sh_gate, 0, lmg, row0, a.Is);
+            load_tile(stu, a.sh_up, 0, lmg, row0, a.Is);
+        }
+        float rg[1], ru[1];
+        dot_rows2(rg, ru, stg, stu, a.sh_gate, a.sh_up, xg, lmg);
+        const int row = row0 + lmg.q;
+        if (lmg.j == lmg.lpr - 1 && row < a.Is) put_pair(a.hsh_x + row, swiglu(rg[0], ru[0]), g);
+        SWQ_STAMP(11);
+    }
+    SWQ_STAMP(1);
+
+    // ---- routing (wave 0) ---------------------------------------------------
+    Rounds<M> rd;
+    asm volatile("" : "+v"(lane));
+    if (wave == 0) {
+        const uint64_t *rep = a.logit_x + (b % kReplicas) * a.rep_stride;
+        const uint64_t *pp[M];
+        bool live[M];
+#pragma unroll
+        for (int j = 0; j < M; ++j) {
+            const int e = lane * M + j;
+            live[j] = e < a.E;
+            pp[j] = rep + min(e, a.E - 1);
+        }
+        float v[M];
+        poll_words<M>(pp, live, g, v, a.err, 2u);
+        SWQ_STAMP(2);
+        rounds_init(rd, v, a.E, lane);
+        // the rounds up to this group's last owned slot; the rest after the
+        // routed work
+        const int own_last = a.K > grp ? grp + kGroups * ((a.K - 1 - grp) / kGroups) : -1;
+        rounds_run(rd, own_last + 1, lane, s_ids);
+        SWQ_STAMP(3);
+    }
+
+    // ---- routed slots of the group -------------------------------------------
+    asm volatile("" : "+v"(lane));
+    {
+        const LaneMap lmd = lane_map(a.down.lpr_log2, lane);
+        const int t0 = rank + NPG * wave;  // this wave's first tile of a slot
+        for (int s = grp; s < a.K; s += kGroups) {
+            const int64_t e = min(wait_lds_nonneg(&s_ids[s], a.err), a.E - 1);
+            // loads in the order they are needed: the first gate/up tile,
+            // then the first down tile (used only after the activations'
+            // round trip)
+            RowTile<GB, GC, 2, GRI> tg, tu;
+            RowTile<DB, 1, 2, DRI> dt0;
+            for (int t = t0; t < a.gu_tpe; t += NPG * kFusedWaves) {
+                const int row0 = t * GRI * lmg.rpw;
+                load_tile(tg, a.gate, e, lmg, row0, a.I);
+                load_tile(tu, a.up, e, lmg, row0, a.I);
+                float rg[GRI], ru[GRI];
+                dot_rows2(rg, ru, tg, tu, a.gate, a.up, xg, lmg);
+                if (lmg.j == lmg.lpr - 1) {
+#pragma unroll
+                    for (int i = 0; i < GRI; ++i) {
+                        const int row = row0 + i * lmg.rpw + lmg.q;
+                        if (row < a.I)
+                            put_pair_group(a.h_x + static_cast<int64_t>(s) * a.I + row, swiglu(rg[i], ru[i]), g,
+                                           a.local);
+                    }
+                }
+            }
+            SWQ_STAMP(4);
+            // the first down tile: its loads issued once the gate/up bytes,
+            // which the step waits for first, are in; used after the
+            // activations' round trip
+            if (t0 < a.dn_tpe) load_tile(dt0, a.down, e, lmd, t0 * DRI * lmd.rpw, a.H);
+            // Without this the compiler may sink the loads below the polls
+            // and the barrier that follow (allowed across an acquire), so they
+            // would start only once the activations are in.
+            asm volatile("" ::: "memory");
+            // the slot's activations: each wave polls a quarter into LDS
+            const int np = a.I / 2, q = (np + kFusedWaves - 1) / kFusedWaves;
+            fetch_acts<DB>(a.h_x + static_cast<int64_t>(s) * a.I, min(np, wave * q), min(np, (wave + 1) * q), g,
+                           s_hb, lane, a.err);
+            __syncthreads();
+            SWQ_STAMP(5);
+            for (int t = t0; t < a.dn_tpe; t += NPG * kFusedWaves) {
+                const int row0 = t * DRI * lmd.rpw;
+                if (t != t0) load_tile(dt0, a.down, e, lmd, row0, a.H);
+                float res[DRI];
+                down_dot<DB, DRI>(res, dt0, a.down, lmd, s_hb);
+                if (lmd.j == lmd.lpr - 1) {
+#pragma unroll
+                    for (int i = 0; i < DRI; ++i) {
+                        const int row = row0 + i * lmd.rpw + lmd.q;
+                        if (row < a.H) put_pair(a.part_x + static_cast<int64_t>(s) * a.H + row, res[i], g);
+                    }
+                }
+            }
+            SWQ_STAMP(6);
+            __syncthreads();  // s_hb is rewritten by the next slot
+        }
+    }
+    // ---- wave 0: the remaining picks, the weights, this workgroup's rows of
+    // every slot's down output; wave 1: the shared expert's down rows -------
+    asm volatile("" : "+v"(lane));
+    if (wave == 0) {
+        rounds_run(rd, a.K, lane, s_ids);
+        const float w = rounds_weight(rd, a.K, a.norm, lane);
+        if (lane < a.K) {
+            s_w[lane] = w;
+            if (b == 0) {
+                if (a.user_ids) a.user_ids[lane] = s_ids[lane];
+                if (a.user_w) a.user_w[lane] = w;
+            }
+        }
+        const int n = a.K * nr;
+        for (int j0 = 0; j0 < n; j0 += 2 * kWave) {
+            const uint64_t *pp[2];
+            bool live[2];
+            int jj[2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                jj[c] = j0 + c * kWave + lane;
+                live[c] = jj[c] < n;
+                const int jc = min(jj[c], n - 1), k = jc / nr;
+                pp[c] = a.part_x + static_cast<int64_t>(k) * a.H + r0 + (jc - k * nr);
+            }
+            float v[2];
+            poll_words<2>(pp, live, g, v, a.err, 8u);
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+                if (live[c]) s_cmb[jj[c]] = v[c];
+        }
+        SWQ_STAMP(8);
+    } else if (sh_rows) {
+        // a third of the shared activations -> LDS, then, once all three
+        // waves' thirds are in, this wave's passes of the shared down rows
+        const int np = a.Is / 2, q3 = (np + kFusedWaves - 2) / (kFusedWaves - 1);
+        fetch_acts<DB>(a.hsh_x, min(np, sp0 * q3), min(np, (sp0 + 1) * q3), g, s_hsh, lane, a.err);
+        SWQ_STAMP(12);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) __hip_atomic_fetch_add(&s_arrive, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        for (uint32_t it = 0; __hip_atomic_load(&s_arrive, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+                              kFusedWaves - 1;
+             ++it) {
+            if (it > kSpinLimit) {
+                if (lane == 0) record_stall(a.err, 16u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        for (int sp = sp0; sp < sh_passes; sp += kFusedWaves - 1) {
+            const int row0 = r0 + sp * lms.rpw;
+            if (sp != sp0) load_tile(sdt, a.sh_down, 0, lms, row0, r0 + nr);
+            float res[1];
+            down_dot<DB, 1>(res, sdt, a.sh_down, lms, s_hsh);
+            const int row = row0 + lms.q;
+            if (lms.j == lms.lpr - 1 && row < r0 + nr) s_shd[row - r0] = res[0];
+        }
+        SWQ_STAMP(7);
+    }
+    __syncthreads();  // s_w, s_cmb, s_shd, s_sg
+
+    // ---- combine ------------------------------------------------------------
+    if (wave == 0) {
+        const float gate = a.has_shared ? sigmoidf_ref(s_sg) : 0.f;
+        if (lane < nr) {
+            // out = sum_k w_k d_k in pick order, then + sigmoid(sg) * shared
+            // (QwenCPUModel.swift:549-566)
+            float acc = 0.f;
+            for (int k = 0; k < a.K; ++k) acc += s_w[k] * s_cmb[k * nr + lane];
+            if (a.has_shared) acc += gate * s_shd[lane];
+            const int row = r0 + lane;
+            if (a.odt == SWQ_BF16) {
+                static_cast<uint16_t *>(a.out)[row] = f32_to_bf16_rne(acc);
+            } else {
+                float *out = static_cast<float *>(a.out);
+                if constexpr (PN) {
+                    // the layer's residual stream: (h + r) + moe (QwenCPUModel.swift:276-279)
+                    float hv = a.h_in[row];
+                    if (a.res_in) hv += a.res_in[row];
+                    out[row] = hv + acc;
+                } else {
+                    out[row] = a.accumulate ? out[row] + acc : acc;
+                }
+            }
+        }
+        // the next call's epoch: every entry, whatever grid the next call uses
+        for (int i = b + NB * lane; i < kFusedMaxBlocks; i += NB * kWave)
+            __hip_atomic_store(a.gen + i, g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        SWQ_STAMP(9);
+    }
+}
+
+using FusedKernel = void (*)(FusedArgs);
+
+// Passes per tile, chosen so that a slot's gate/up and down rows at the
+// benchmark shapes are one tile per wave (I = 512 rows over the 128 waves of
+// a group: 4 rows per wave and matrix; H = 2048 down rows: 16 per wave).
+constexpr int gate_passes(int gb, int gc) { return gb == 4 && gc == 2 ? 2 : 4; }
+constexpr int down_passes(int db) { return db == 4 ? 4 : 8; }
+
+template <int XDT, int GB, int GC, int GX, int DB, int RC, bool PN>
+static FusedKernel fused_by_m(int M) {
+    constexpr int GRI = gate_passes(GB, GC), DRI = down_passes(DB);
+    switch (M) {
+        case 1: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 1, PN>;
+        case 2: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 2, PN>;
+        case 4: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 4, PN>;
+        case 8: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 8, PN>;
+        default: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 16, PN>;
+    }
+}
+
+
+// Gate/up formats of the single launch: 4-bit codes, 8-bit codes with two
+// chunks per lane, 8-bit codes with one.
+enum FusedGateFormat { kFusedQ4 = 0, kFusedQ8C2 = 1, kFusedQ8C1 = 2 };
+
+// The instantiation for (gate/up format, router chunks per lane 2 or 1,
+// logits per routing lane M), one per activation format; nullptr for none.
+FusedKernel fused_select_bf16(int gfmt, bool rc2, int M);
+FusedKernel fused_select_f32(int gfmt, bool rc2, int M);
+FusedKernel fused_select_pn(int gfmt, bool rc2, int M);
+
+}  // namespace swq

@@ -91,7 +91,6 @@ inline int check_layer(const swq_moe_layer *l, int B, int x_dtype) {
 // staged path's `base` bytes.  fused_decode launches it when the layer, the
 // batch and the device allow (*taken), else leaves the work to the caller.
 size_t fused_ws_bytes(const swq_moe_layer *l, size_t base);
-size_t fused_err_offset(const swq_moe_layer *l, size_t base);
 int fused_probe_device(hipStream_t stream);
 // The layer's post-attention norm folded into the single launch:
 // x = rmsnorm(h + residual) * weight, out = (h + residual) + moe(x).

@@ -154,50 +154,45 @@ __device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t m
     return r;
 }
 
+// The raw activation words of a lane's chunks: loads only.  A phase that
+// issues all its loads (weights, then these) before converting anything has
+// every load in flight at once; a conversion right after its loads would
+// make the compiler wait for them before the next load issues.
+template <int XDT, int BITS, int CPL>
+struct XRaw {
+    static constexpr int kCPC = codes_per_chunk<BITS>();
+    static constexpr int kN = XDT == 2 ? kCPC / 8 : kCPC / 4;  // 16-byte words per chunk
+    uint4 r[CPL][kN];
+};
+
+template <int XDT, int BITS, int CPL>
+__device__ __forceinline__ void load_xraw(XRaw<XDT, BITS, CPL> &xr, const QMat &m, const LaneMap &lm, const void *x,
+                                          int64_t x_base) {
+    constexpr int kCPC = codes_per_chunk<BITS>(), kN = XRaw<XDT, BITS, CPL>::kN;
+    constexpr int kES = XDT == 2 ? 2 : 4;
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) {
+        const int c = min(lm.j + t * lm.lpr, m.chunks - 1);
+        const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const uint8_t *>(x) +
+                                                         (x_base + static_cast<int64_t>(c) * kCPC) * kES);
+#pragma unroll
+        for (int k = 0; k < kN; ++k) xr.r[t][k] = p[k];
+    }
+}
+
+// The activation slice from its raw words (the same values and sums as
+// reading x directly).
 template <int XDT, int BITS, int CPL, int XF>
-__device__ __forceinline__ void load_xslice(XSlice<BITS, CPL, XF> &xs, const QMat &m, const LaneMap &lm,
-                                            const void *x, int64_t x_base) {
+__device__ __forceinline__ void xslice_convert(XSlice<BITS, CPL, XF> &xs, const XRaw<XDT, BITS, CPL> &xr) {
     constexpr int kCPC = codes_per_chunk<BITS>();
-    if constexpr (XF == kXF32) {
-#pragma unroll
-        for (int t = 0; t < CPL; ++t) {
-            const int c = min(lm.j + t * lm.lpr, m.chunks - 1);
-            load_x<XDT>(xs.v[t], x, x_base + static_cast<int64_t>(c) * kCPC);
-        }
-#pragma unroll
-        for (int t = 0; t < CPL; ++t) {
-            float s = 0.f;
-#pragma unroll
-            for (int i = 0; i < kCPC; ++i) s += xs.v[t][i];
-            xs.sum[t] = s;
-        }
-    } else if constexpr (XF == kXBF16X2) {
-        static_assert(XDT == 0 && BITS == 4, "split bf16 activations need fp32 x and 4-bit codes");
-        float v[CPL][32];
-#pragma unroll
-        for (int t = 0; t < CPL; ++t) {
-            const int c = min(lm.j + t * lm.lpr, m.chunks - 1);
-            load_x<XDT>(v[t], x, x_base + static_cast<int64_t>(c) * kCPC);
-        }
-#pragma unroll
-        for (int t = 0; t < CPL; ++t) pack_chunk_x2(v[t], xs.hi[t], xs.lo[t], xs.sum[t]);
-    } else {
+    if constexpr (XF == kXBF16) {
         static_assert(XDT == 2 && BITS == 4, "packed bf16 activations need bf16 x and 4-bit codes");
-        const uint16_t *xp = static_cast<const uint16_t *>(x) + x_base;
-        uint4 raw[CPL][4];
-#pragma unroll
-        for (int t = 0; t < CPL; ++t) {
-            const int c = min(lm.j + t * lm.lpr, m.chunks - 1);
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                raw[t][k] = *reinterpret_cast<const uint4 *>(xp + static_cast<int64_t>(c) * 32 + k * 8);
-        }
 #pragma unroll
         for (int t = 0; t < CPL; ++t) {
             float s[4] = {0.f, 0.f, 0.f, 0.f};  // independent chains
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const uint32_t d0 = raw[t][k].x, d1 = raw[t][k].y, d2 = raw[t][k].z, d3 = raw[t][k].w;
+                const uint32_t d0 = xr.r[t][k].x, d1 = xr.r[t][k].y, d2 = xr.r[t][k].z, d3 = xr.r[t][k].w;
                 xs.p[t][4 * k + 0] = (d0 & 0xFFFFu) | (d2 << 16);
                 xs.p[t][4 * k + 1] = (d0 >> 16) | (d2 & 0xFFFF0000u);
                 xs.p[t][4 * k + 2] = (d1 & 0xFFFFu) | (d3 << 16);
@@ -207,7 +202,50 @@ __device__ __forceinline__ void load_xslice(XSlice<BITS, CPL, XF> &xs, const QMa
             }
             xs.sum[t] = (s[0] + s[1]) + (s[2] + s[3]);
         }
+    } else {
+        float v[CPL][kCPC];
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) {
+#pragma unroll
+            for (int k = 0; k < XRaw<XDT, BITS, CPL>::kN; ++k) {
+                const uint32_t u[4] = {xr.r[t][k].x, xr.r[t][k].y, xr.r[t][k].z, xr.r[t][k].w};
+                if constexpr (XDT == 2) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        v[t][8 * k + 2 * i] = __uint_as_float(u[i] << 16);
+                        v[t][8 * k + 2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[t][4 * k + i] = __uint_as_float(u[i]);
+                }
+            }
+        }
+        if constexpr (XF == kXF32) {
+#pragma unroll
+            for (int t = 0; t < CPL; ++t) {
+                float s = 0.f;
+#pragma unroll
+                for (int i = 0; i < kCPC; ++i) {
+                    xs.v[t][i] = v[t][i];
+                    s += v[t][i];
+                }
+                xs.sum[t] = s;
+            }
+        } else {
+            static_assert(XDT == 0 && BITS == 4, "split bf16 activations need fp32 x and 4-bit codes");
+#pragma unroll
+            for (int t = 0; t < CPL; ++t) pack_chunk_x2(v[t], xs.hi[t], xs.lo[t], xs.sum[t]);
+        }
     }
+}
+
+template <int XDT, int BITS, int CPL, int XF>
+__device__ __forceinline__ void load_xslice(XSlice<BITS, CPL, XF> &xs, const QMat &m, const LaneMap &lm,
+                                            const void *x, int64_t x_base) {
+    XRaw<XDT, BITS, CPL> xr;
+    load_xraw<XDT>(xr, m, lm, x, x_base);
+    xslice_convert(xs, xr);
 }
 
 // sum_i (128 + q_i) * x_i over a chunk of 4-bit codes with packed bf16 pairs.
@@ -252,10 +290,11 @@ __device__ __forceinline__ float dot_chunk_q4_bf16x2(const uint4 w, const uint32
 // weights
 
 // Codes plus raw scale/bias bits of RI passes of rows (row0 + i*rpw + q).
-// ES is the byte size of a scale element: 2 (f16, bf16) or 4 (f32).
-template <int BITS, int CPL, int ES>
+// ES is the byte size of a scale element: 2 (f16, bf16) or 4 (f32).  RI
+// defaults to 4/CPL passes (four 16-byte code chunks per lane).
+template <int BITS, int CPL, int ES, int RI_ = 4 / CPL>
 struct RowTile {
-    static constexpr int kRI = 4 / CPL;
+    static constexpr int kRI = RI_;
     uint4 w[kRI][CPL];
     uint32_t s[kRI][CPL];
     uint32_t b[kRI][CPL];
@@ -278,10 +317,10 @@ __device__ __forceinline__ float scale_value(uint32_t raw, int stype) {
     }
 }
 
-template <int BITS, int CPL, int ES>
-__device__ __forceinline__ void load_tile(RowTile<BITS, CPL, ES> &rt, const QMat &m, int64_t expert,
+template <int BITS, int CPL, int ES, int RI_>
+__device__ __forceinline__ void load_tile(RowTile<BITS, CPL, ES, RI_> &rt, const QMat &m, int64_t expert,
                                           const LaneMap &lm, int row0, int row_end) {
-    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
+    constexpr int RI = RI_;
     const uint8_t *wbase = m.w + expert * m.stride_w;
     const uint8_t *sbase = m.s + expert * m.stride_sb;
     const uint8_t *bbase = m.b + expert * m.stride_sb;
@@ -312,10 +351,10 @@ __device__ __forceinline__ void load_tile(RowTile<BITS, CPL, ES> &rt, const QMat
 // loop: hoisted out of it, the unpacked codes of a tile would stay live
 // across the loop and spill.  They all come first, so the passes' arithmetic
 // that follows can interleave.
-template <int BITS, int CPL, int ES, int XF>
-__device__ __forceinline__ void dot_tile(float (&res)[4 / CPL], const RowTile<BITS, CPL, ES> &rt,
+template <int BITS, int CPL, int ES, int XF, int RI_>
+__device__ __forceinline__ void dot_tile(float (&res)[RI_], const RowTile<BITS, CPL, ES, RI_> &rt,
                                          const XSlice<BITS, CPL, XF> &xs, const QMat &m, const LaneMap &lm) {
-    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
+    constexpr int RI = RI_;
     uint4 wt[RI][CPL];
 #pragma unroll
     for (int i = 0; i < RI; ++i) {
@@ -352,6 +391,146 @@ __device__ __forceinline__ void dot_tile(float (&res)[4 / CPL], const RowTile<BI
     }
 #pragma unroll
     for (int i = 0; i < RI; ++i) res[i] = segment_reduce(res[i], lm.lpr_log2);
+}
+
+
+// ---------------------------------------------------------------------------
+// dot products of NT tiles (one activation slice) with the code words of all
+// their chunks interleaved: word k of every chunk before word k + 1 of any,
+// so the unpack -> dot chains of different chunks overlap.  A kernel with a
+// single wave per SIMD has no other wave to fill the issue slots a chain of
+// dependent instructions leaves; with 8-32 independent chains they fill
+// themselves.  Each chunk's own summation order is dot_chunk*'s, and the
+// per-row combination is dot_tile's, so results equal dot_tile's bit for bit.
+
+template <int BITS, int CPL, int XF, int N>
+__device__ __forceinline__ void chunk_dots(float (&d)[N], const uint4 (&w)[N], const XSlice<BITS, CPL, XF> &xs) {
+    if constexpr (XF == kXBF16) {
+        float a0[N], a1[N];
+#pragma unroll
+        for (int n = 0; n < N; ++n) a0[n] = a1[n] = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int n = 0; n < N; ++n) {
+                const uint32_t *xp = xs.p[n % CPL];
+                const uint32_t v = k == 0 ? w[n].x : k == 1 ? w[n].y : k == 2 ? w[n].z : w[n].w;
+                const uint32_t c0 = and_or(v, 0x000F000Fu, 0x43004300u);        // {q0, q4}
+                const uint32_t c1 = and_or(v >> 4, 0x000F000Fu, 0x43004300u);   // {q1, q5}
+                const uint32_t c2 = and_or(v >> 8, 0x000F000Fu, 0x43004300u);   // {q2, q6}
+                const uint32_t c3 = and_or(v >> 12, 0x000F000Fu, 0x43004300u);  // {q3, q7}
+                a0[n] = dot2_bf16(c0, xp[4 * k + 0], a0[n]);
+                a1[n] = dot2_bf16(c1, xp[4 * k + 1], a1[n]);
+                a0[n] = dot2_bf16(c2, xp[4 * k + 2], a0[n]);
+                a1[n] = dot2_bf16(c3, xp[4 * k + 3], a1[n]);
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < N; ++n) d[n] = a0[n] + a1[n];
+    } else if constexpr (XF == kXBF16X2) {
+        float a0[N], a1[N], b0[N], b1[N];
+#pragma unroll
+        for (int n = 0; n < N; ++n) a0[n] = a1[n] = b0[n] = b1[n] = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int n = 0; n < N; ++n) {
+                const uint32_t *hi = xs.hi[n % CPL], *lo = xs.lo[n % CPL];
+                const uint32_t v = k == 0 ? w[n].x : k == 1 ? w[n].y : k == 2 ? w[n].z : w[n].w;
+                const uint32_t c0 = and_or(v, 0x000F000Fu, 0x43004300u);
+                const uint32_t c1 = and_or(v >> 4, 0x000F000Fu, 0x43004300u);
+                const uint32_t c2 = and_or(v >> 8, 0x000F000Fu, 0x43004300u);
+                const uint32_t c3 = and_or(v >> 12, 0x000F000Fu, 0x43004300u);
+                a0[n] = dot2_bf16(c0, hi[4 * k + 0], a0[n]);
+                a1[n] = dot2_bf16(c1, hi[4 * k + 1], a1[n]);
+                b0[n] = dot2_bf16(c0, lo[4 * k + 0], b0[n]);
+                b1[n] = dot2_bf16(c1, lo[4 * k + 1], b1[n]);
+                a0[n] = dot2_bf16(c2, hi[4 * k + 2], a0[n]);
+                a1[n] = dot2_bf16(c3, hi[4 * k + 3], a1[n]);
+                b0[n] = dot2_bf16(c2, lo[4 * k + 2], b0[n]);
+                b1[n] = dot2_bf16(c3, lo[4 * k + 3], b1[n]);
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < N; ++n) d[n] = (a0[n] + a1[n]) + (b0[n] + b1[n]);
+    } else if constexpr (BITS == 8) {
+        // dot_chunk_q8: acc[k] over the bytes of word k in order
+        float acc[N][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int n = 0; n < N; ++n) {
+                const float *x = xs.v[n % CPL];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t v = k == 0 ? w[n].x : k == 1 ? w[n].y : k == 2 ? w[n].z : w[n].w;
+                    acc[n][k] = j == 0 ? ubyte(v, 0) * x[4 * k] : fmaf(ubyte(v, j), x[4 * k + j], acc[n][k]);
+                }
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < N; ++n) d[n] = (acc[n][0] + acc[n][1]) + (acc[n][2] + acc[n][3]);
+    } else {
+        // dot_chunk_q4: acc[k] over the nibbles of word k, low byte lane
+        // nibbles (0, 2, 4, 6) and high ones (1, 3, 5, 7) alternating
+        float acc[N][4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+#pragma unroll
+            for (int n = 0; n < N; ++n) {
+                const float *x = xs.v[n % CPL];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t v = k == 0 ? w[n].x : k == 1 ? w[n].y : k == 2 ? w[n].z : w[n].w;
+                    const uint32_t nib = (j & 1) ? (v >> 4) & 0x0F0F0F0Fu : v & 0x0F0F0F0Fu;
+                    const float q = ubyte(nib, j >> 1);
+                    acc[n][k] = j == 0 ? q * x[8 * k] : fmaf(q, x[8 * k + j], acc[n][k]);
+                }
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < N; ++n) d[n] = (acc[n][0] + acc[n][1]) + (acc[n][2] + acc[n][3]);
+    }
+}
+
+// res[u][i]: the full dot product of row (row0 + i*rpw + q) of tile u with
+// the activations, valid in the row segment's last lane (as dot_tile).
+template <int NT, int BITS, int CPL, int ES, int XF, int RI>
+__device__ __forceinline__ void dot_tiles(float (&res)[NT][RI], const RowTile<BITS, CPL, ES, RI> *const (&rt)[NT],
+                                          const QMat *const (&m)[NT], const XSlice<BITS, CPL, XF> &xs,
+                                          const LaneMap &lm) {
+    constexpr int N = NT * RI * CPL;  // chunk n = (u*RI + i)*CPL + t
+    uint4 w[N];
+#pragma unroll
+    for (int u = 0; u < NT; ++u)
+#pragma unroll
+        for (int i = 0; i < RI; ++i)
+#pragma unroll
+            for (int t = 0; t < CPL; ++t) w[(u * RI + i) * CPL + t] = rt[u]->w[i][t];
+    float d[N];
+    chunk_dots<BITS, CPL, XF, N>(d, w, xs);
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+#pragma unroll
+        for (int i = 0; i < RI; ++i) {
+            float acc = 0.f;
+#pragma unroll
+            for (int t = 0; t < CPL; ++t) {
+                const bool live = lm.j + t * lm.lpr < m[u]->chunks;
+                const float sc = live ? scale_value<ES>(rt[u]->s[i][t], m[u]->stype) : 0.f;
+                const float bi = live ? scale_value<ES>(rt[u]->b[i][t], m[u]->stype) : 0.f;
+                const float dd = d[(u * RI + i) * CPL + t];
+                if constexpr (XF == kXF32) {
+                    acc = fmaf(sc, dd, acc);
+                    acc = fmaf(bi, xs.sum[t], acc);
+                } else {
+                    acc = fmaf(sc, dd, acc);
+                    acc = fmaf(fmaf(-128.f, sc, bi), xs.sum[t], acc);
+                }
+            }
+            res[u][i] = segment_reduce(acc, lm.lpr_log2);
+        }
+    }
 }
 
 }  // namespace swq
