@@ -552,7 +552,7 @@ using namespace swq;
 
 extern "C" size_t swq_moe_decode_workspace_bytes(const swq_moe_layer *layer, int batch) {
     if (check_layer(layer, batch, SWQ_BF16) != SWQ_OK) return 0;
-    return fused_ws_bytes(layer, ws_layout(layer, batch).total);
+    return decode_ws_bytes(layer, batch, false);
 }
 
 extern "C" int swq_moe_workspace_init(void *ws, size_t ws_bytes, void *stream) {
@@ -589,7 +589,7 @@ extern "C" int swq_moe_workspace_status(void *ws, size_t ws_bytes, int clear, vo
 // cannot); 0 picks the single launch when possible, else the three stages.
 static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int batch, void *out,
                            int out_dtype, int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes,
-                           int flags, int stage_mask, void *stream) {
+                           int flags, int stage_mask, void *stream, bool max_layout = false) {
     if (x_dtype != SWQ_F32 && x_dtype != SWQ_BF16) return SWQ_ERR_UNSUPPORTED_DTYPE;
     int st = check_layer(layer, batch, x_dtype);
     if (st != SWQ_OK) return st;
@@ -601,7 +601,8 @@ static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtyp
     const int H = layer->hidden;
     const int xes = x_dtype == SWQ_F32 ? 4 : 2;
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || (static_cast<int64_t>(H) * xes) % 16 != 0) return SWQ_ERR_MISALIGNED;
-    const WsLayout wl = ws_layout(layer, batch);
+    const FusedLayout fl = fused_layout(layer, max_layout);
+    const WsLayout wl = ws_layout(layer, batch, fl.total);
     if (!ws || ws_bytes < wl.total) return SWQ_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(ws) % 256 != 0) return SWQ_ERR_MISALIGNED;
 
@@ -667,8 +668,8 @@ static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtyp
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (stage_mask == 0 || stage_mask == SWQ_STAGES_FUSED) {
         bool taken = false;
-        st = fused_decode(layer, x, x_dtype, batch, out, out_dtype, topk_ids, topk_weights, ws, ws_bytes, wl.total,
-                          accumulate, s, &taken);
+        st = fused_decode(layer, x, x_dtype, batch, out, out_dtype, topk_ids, topk_weights, ws, fl, accumulate, s,
+                          &taken);
         if (st != SWQ_OK || taken) return st;
         if (stage_mask == SWQ_STAGES_FUSED) return SWQ_ERR_LIMIT;
         stage_mask = 7;
@@ -711,12 +712,12 @@ extern "C" int swq_moe_decode_norm(const swq_moe_layer *layer, const float *h, c
         reinterpret_cast<uintptr_t>(out) % 4 != 0 ||
         reinterpret_cast<uintptr_t>(norm_weight) % (norm_dtype == SWQ_F32 ? 4 : 2) != 0)
         return SWQ_ERR_MISALIGNED;
-    const WsLayout wl = ws_layout(layer, 1);
-    if (!ws || ws_bytes < fused_ws_bytes(layer, wl.total)) return SWQ_ERR_WORKSPACE;
+    const FusedLayout fl = fused_layout(layer, false);
+    if (!ws || ws_bytes < decode_ws_bytes(layer, 1, false)) return SWQ_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(ws) % 256 != 0) return SWQ_ERR_MISALIGNED;
     const FusedPrenorm pn{h, residual, norm_weight, norm_dtype, norm_eps};
     bool taken = false;
-    st = fused_decode(layer, nullptr, SWQ_F32, 1, out, SWQ_F32, topk_ids, topk_weights, ws, ws_bytes, wl.total, false,
+    st = fused_decode(layer, nullptr, SWQ_F32, 1, out, SWQ_F32, topk_ids, topk_weights, ws, fl, false,
                       static_cast<hipStream_t>(stream), &taken, &pn);
     if (st != SWQ_OK) return st;
     return taken ? SWQ_OK : SWQ_ERR_LIMIT;

@@ -12,33 +12,6 @@ namespace swq {
 // ---------------------------------------------------------------------------
 // host side
 
-struct FusedLayout {
-    size_t gen, logit_x, hsh_x, h_x, part_x, total;
-    int rep_stride;
-};
-
-// Placed after the staged path's regions of the same workspace.
-inline FusedLayout fused_layout(const swq_moe_layer *l, size_t base) {
-    FusedLayout f{};
-    size_t off = align256(base);
-    auto take = [&](size_t n) {
-        const size_t o = off;
-        off = align256(off + n);
-        return o;
-    };
-    // replicas 4 KiB apart plus a 256-byte skew, so they sit in different
-    // memory channels
-    const size_t rep_bytes = ((static_cast<size_t>(l->num_experts) * 8 + 4095) & ~static_cast<size_t>(4095)) + 256;
-    f.rep_stride = static_cast<int>(rep_bytes / 8);
-    f.gen = take(kFusedMaxBlocks * 4);
-    f.logit_x = take(rep_bytes * kReplicas);
-    f.hsh_x = take(static_cast<size_t>(l->has_shared ? l->shared_intermediate : 1) * 8);
-    f.h_x = take(static_cast<size_t>(l->top_k) * l->moe_intermediate * 8);
-    f.part_x = take(static_cast<size_t>(l->top_k) * l->hidden * 8);
-    f.total = off;
-    return f;
-}
-
 // The instantiation for this layer's formats, or nullptr: routed and shared
 // gate/up rows in one format, 4- or 8-bit down rows, an 8-bit router and
 // shared-expert gate.  M = ceil(E / 64), as the staged path's routing wave.
@@ -153,6 +126,7 @@ static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch
     if (a.down.cpl != 1 || a.router.xf != 0) return nullptr;
     if (layer->moe_intermediate > kMaxInterFused || layer->moe_intermediate % 2 != 0) return nullptr;
     if (prenorm && layer->hidden > kPrenormMaxHidden) return nullptr;
+    if (layer->hidden > kFusedMaxHidden || layer->num_experts > kMaxExperts) return nullptr;
     FusedKernel kern = fused_kernel_for(a.router, a.gate, a.down, x_dtype, layer->num_experts, prenorm);
     if (!kern) return nullptr;
     const int blocks = fused_blocks(kern, dev);
@@ -180,18 +154,14 @@ static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch
     return kern;
 }
 
-size_t fused_ws_bytes(const swq_moe_layer *l, size_t base) { return fused_layout(l, base).total; }
-
 int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int batch, void *out, int out_dtype,
-                 int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes, size_t staged_bytes,
-                 bool accumulate, hipStream_t stream, bool *taken, const FusedPrenorm *pn) {
+                 int32_t *topk_ids, float *topk_weights, void *ws, const FusedLayout &fl, bool accumulate,
+                 hipStream_t stream, bool *taken, const FusedPrenorm *pn) {
     *taken = false;
     FusedArgs a;
     int nb = 0;
     FusedKernel k = fused_plan(layer, x_dtype, batch, pn != nullptr, &a, &nb);
     if (!k) return SWQ_OK;
-    const FusedLayout fl = fused_layout(layer, staged_bytes);
-    if (ws_bytes < fl.total) return SWQ_OK;
     uint8_t *wsb = static_cast<uint8_t *>(ws);
     a.x = x;
     a.out = out;
@@ -224,8 +194,10 @@ int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int bat
 // places every group's workgroups on one XCD (a launch of that grid reports
 // each workgroup's XCC_ID).  Blocking; runs on `stream`.  Thread-safe: the
 // first caller for a device runs the probe (std::call_once), later ones
-// wait for it; if it fails the device keeps the three-launch path.
-int fused_probe_device(hipStream_t stream) {
+// wait for it; if it fails the device keeps the three-launch path.  The
+// probe writes one word per workgroup into `given` when the caller passes
+// device memory of kFusedMaxBlocks words, else into a buffer it allocates.
+int fused_probe_device(hipStream_t stream, void *given) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return SWQ_ERR_HIP;
     FusedDevice &d = g_fused_dev[dev];
@@ -239,8 +211,8 @@ int fused_probe_device(hipStream_t stream) {
         const int n = min(cus, kFusedMaxBlocks) / kGroups * kGroups;
         int ok = 0;
         if (n >= kGroups) {
-            int32_t *buf = nullptr;
-            if (hipMalloc(&buf, n * sizeof(int32_t)) != hipSuccess) {
+            int32_t *buf = static_cast<int32_t *>(given);
+            if (!buf && hipMalloc(&buf, n * sizeof(int32_t)) != hipSuccess) {
                 status = SWQ_ERR_HIP;
                 return;
             }
@@ -249,7 +221,7 @@ int fused_probe_device(hipStream_t stream) {
             hipError_t e = hipGetLastError();
             if (e == hipSuccess) e = hipMemcpyAsync(h, buf, n * sizeof(int32_t), hipMemcpyDeviceToHost, stream);
             if (e == hipSuccess) e = hipStreamSynchronize(stream);
-            hipFree(buf);
+            if (!given) hipFree(buf);
             if (e != hipSuccess) {
                 status = SWQ_ERR_HIP;
                 return;

@@ -85,9 +85,8 @@ namespace swq {
 constexpr int kFusedWaves = 4;
 constexpr int kFusedThreads = kFusedWaves * kWave;
 constexpr int kGroups = 8;
-constexpr int kFusedMaxBlocks = 1024;      // gen[] entries kept in step
-constexpr int kReplicas = kGroups;         // logit replicas (one per XCD group)
-constexpr int kMaxInterFused = 2048;       // activations of one slot
+constexpr int kReplicas = kFusedReplicas;  // logit replicas (one per XCD group)
+constexpr int kMaxInterFused = kFusedMaxInter;  // activations of one slot
 constexpr int kMaxCombineRows = 16;        // output rows per workgroup
 constexpr int kPrenormMaxHidden = 4096;    // hidden size the folded-in norm holds in LDS
 constexpr uint32_t kSpinLimit = 1u << 20;  // polls of ~0.1-1 us each: about a second

@@ -18,16 +18,18 @@ struct WsLayout {
 
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
-inline WsLayout ws_layout(const swq_moe_layer *l, int B) {
+// The staged path's regions, from `base` (after the header and the single
+// launch's regions, so that neither depends on the batch).
+inline WsLayout ws_layout(const swq_moe_layer *l, int B, size_t base) {
     WsLayout w{};
-    size_t off = 0;
+    size_t off = align256(base);
     auto take = [&](size_t n) {
         const size_t o = off;
         off = align256(off + n);
         return o;
     };
     const size_t P = static_cast<size_t>(B) * l->top_k;
-    w.header = take(256);  // zeroed by swq_moe_workspace_init; word kWsErrByte/4: the stall record
+    w.header = 0;  // zeroed by swq_moe_workspace_init; word kWsErrByte/4: the stall record
     w.logits = take(static_cast<size_t>(B) * l->num_experts * 4);
     w.sg = take(static_cast<size_t>(B) * 4);
     w.h_sh = take(static_cast<size_t>(B) * (l->has_shared ? l->shared_intermediate : 1) * 4);
@@ -87,11 +89,63 @@ inline int check_layer(const swq_moe_layer *l, int B, int x_dtype) {
     return SWQ_OK;
 }
 
-// The single-launch path (moe_fused.hip): its workspace regions follow the
-// staged path's `base` bytes.  fused_decode launches it when the layer, the
-// batch and the device allow (*taken), else leaves the work to the caller.
-size_t fused_ws_bytes(const swq_moe_layer *l, size_t base);
-int fused_probe_device(hipStream_t stream);
+// Workspace of a decode call:
+//   [0, 256)          header (kWsErrByte: the stall record)
+//   [256, 4352)       the single launch's per-workgroup epoch counters
+//   [4352, ...)       its exchange words (logit replicas, activations,
+//                     partial outputs), sized for the layer, or for the
+//                     compiled maxima (kFusedMax*) in the scratch of the
+//                     no-allocation entry point, so that calls on any layer
+//                     and batch can share it
+//   then              the staged path's regions (ws_layout)
+// Epoch counters at a fixed place keep every call's epoch above those of the
+// words any earlier call left, whatever layer it ran.
+constexpr int kFusedMaxBlocks = 1024;   // epoch counters kept in step
+constexpr int kFusedReplicas = 8;       // logit replicas (one per XCD group)
+constexpr int kFusedMaxHidden = 8192;   // the compiled maxima of the scratch layout
+constexpr int kFusedMaxInter = 2048;
+struct FusedLayout {
+    size_t gen, logit_x, hsh_x, h_x, part_x, total;
+    int rep_stride;
+};
+
+inline FusedLayout fused_layout(const swq_moe_layer *l, bool max_shape) {
+    FusedLayout f{};
+    size_t off = 256;
+    auto take = [&](size_t n) {
+        const size_t o = off;
+        off = align256(off + n);
+        return o;
+    };
+    const size_t E = max_shape ? kMaxExperts : l->num_experts;
+    const size_t K = max_shape ? SWQ_MAX_TOPK : l->top_k;
+    const size_t I = max_shape ? kFusedMaxInter : l->moe_intermediate;
+    const size_t Is = max_shape ? kFusedMaxInter : (l->has_shared ? l->shared_intermediate : 1);
+    const size_t H = max_shape ? kFusedMaxHidden : l->hidden;
+    // replicas 4 KiB apart plus a 256-byte skew, so they sit in different
+    // memory channels
+    const size_t rep_bytes = ((E * 8 + 4095) & ~static_cast<size_t>(4095)) + 256;
+    f.rep_stride = static_cast<int>(rep_bytes / 8);
+    f.gen = take(kFusedMaxBlocks * 4);
+    f.logit_x = take(rep_bytes * kFusedReplicas);
+    f.hsh_x = take(Is * 8);
+    f.h_x = take(K * I * 8);
+    f.part_x = take(K * H * 8);
+    f.total = off;
+    return f;
+}
+
+// Bytes of the whole decode workspace for `batch` tokens.
+inline size_t decode_ws_bytes(const swq_moe_layer *l, int batch, bool max_shape) {
+    return ws_layout(l, batch, fused_layout(l, max_shape).total).total;
+}
+
+// The single-launch path (moe_fused.hip), in the regions `fl` places.
+// fused_decode launches it when the layer, the batch and the device allow
+// (*taken), else leaves the work to the caller.  fused_probe_device probes
+// the XCD placement once per device; `buf`, if given, is device memory of
+// at least kFusedMaxBlocks words it may use instead of allocating.
+int fused_probe_device(hipStream_t stream, void *buf = nullptr);
 // The layer's post-attention norm folded into the single launch:
 // x = rmsnorm(h + residual) * weight, out = (h + residual) + moe(x).
 struct FusedPrenorm {
@@ -101,7 +155,7 @@ struct FusedPrenorm {
     float eps;
 };
 int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int batch, void *out, int out_dtype,
-                 int32_t *topk_ids, float *topk_weights, void *ws, size_t ws_bytes, size_t staged_bytes,
-                 bool accumulate, hipStream_t stream, bool *taken, const FusedPrenorm *prenorm = nullptr);
+                 int32_t *topk_ids, float *topk_weights, void *ws, const FusedLayout &fl, bool accumulate,
+                 hipStream_t stream, bool *taken, const FusedPrenorm *prenorm = nullptr);
 
 }  // namespace swq

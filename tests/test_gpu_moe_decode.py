@@ -192,6 +192,26 @@ def test_fused_equals_staged_odd_shapes(E, K, I, Is, H, bits, norm):
     assert torch.equal(of, os_)
 
 
+def test_workspace_serves_every_batch():
+    """One workspace, sized for batch 4, serving batch 4, batch 1 (the single
+    launch) and batch 4 again: each call equals a call on a fresh workspace.
+    The single launch's exchange words sit before the staged regions, so a
+    staged call's raw values never land where epoch-tagged words are
+    polled."""
+    import torch
+    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    ws = gpu.new_workspace(4)
+    for i, batch in enumerate((4, 1, 4, 1)):
+        x = helpers.bf16_bits_to_torch(synth.activations_bf16(helpers.SEED + 60 + i, batch, shape.hidden))
+        o, ids, w = gpu.decode(x, ws=ws)
+        fo, fids, fw = gpu.decode(x, ws=gpu.new_workspace(batch))
+        torch.cuda.synchronize()
+        assert torch.equal(ids, fids) and torch.equal(w, fw) and torch.equal(o, fo), (i, batch)
+    from swiftlet_amd import _lib
+    assert gpu.workspace_status(ws) == _lib.SWQ_OK
+
+
 # a layer without a shared expert (has_shared = 0: checkpoints without
 # shared_expert weights load this way; QwenCPUModel.swift:559-566 runs the
 # shared expert only when present; MoEGPU's shared fields are optional,
