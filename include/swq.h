@@ -451,6 +451,27 @@ int swq_moe_decode(const swq_moe_layer *layer,
                    int32_t *topk_ids, float *topk_weights,
                    void *ws, size_t ws_bytes, int flags, void *stream);
 
+/* swq_moe_decode with no workspace argument and no allocation: for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It has no counterpart in the reference.
+ * The workspace is a static 4 MiB device array inside the library, one per
+ * GPU it runs on, held until the process ends; every call on a GPU shares
+ * that GPU's array, so calls that overlap in time on one GPU race (run them
+ * on one stream).  Layers whose workspace at `batch` does not fit it return
+ * SWQ_ERR_LIMIT (the limit covers the benchmark shapes at any batch up to
+ * SWQ_MAX_BATCH; use swq_moe_decode for larger ones).  The first call on a
+ * device sets the array up (its address, the single launch's XCD probe, a
+ * zero fill) and blocks until done: make it outside stream capture.  Calls
+ * on any layer and batch may follow one another.  A stall of the single
+ * launch (see swq_moe_workspace_status) is recorded in the array and has no
+ * query: this path assumes a device running nothing else.  Arguments and
+ * results are swq_moe_decode's. */
+int swq_moe_decode_noalloc(const swq_moe_layer *layer,
+                           const void *x, int x_dtype, int batch,
+                           void *out, int out_dtype,
+                           int32_t *topk_ids, float *topk_weights,
+                           int flags, void *stream);
+
 /* The MoE step of one token with the layer's residual add and post-attention
  * RMSNorm folded into the same launch:
  *     h1  = h + residual                      (residual may be NULL)

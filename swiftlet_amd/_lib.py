@@ -153,6 +153,7 @@ SIGNATURES = {
     "swq_moe_decode_workspace_bytes": (_SZ, [_c.POINTER(MoELayer), _I]),
     "swq_moe_workspace_init": (_I, [_P, _SZ, _P]),
     "swq_moe_workspace_status": (_I, [_P, _SZ, _I, _P]),
+    "swq_moe_decode_noalloc": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _I, _P]),
     "swq_moe_decode": (_I, [_c.POINTER(MoELayer), _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _I, _P]),
     "swq_moe_decode_norm": (_I, [_c.POINTER(MoELayer), _P, _P, _P, _I, _c.c_float, _P, _P, _P, _P, _SZ, _P]),
     "swq_synth_u32": (_I, [_P, _I64, _U64, _U64, _I64, _P]),

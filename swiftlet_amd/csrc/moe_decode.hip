@@ -21,6 +21,9 @@
 #include "route.hpp"
 #include "tile.hpp"
 
+#include <atomic>
+#include <mutex>
+
 namespace swq {
 
 constexpr int kThreads12 = 256;
@@ -736,4 +739,62 @@ extern "C" int swq_moe_decode(const swq_moe_layer *layer, const void *x, int x_d
                               int flags, void *stream) {
     return moe_decode_impl(layer, x, x_dtype, batch, out, out_dtype, topk_ids, topk_weights, ws, ws_bytes, flags, 0,
                            stream);
+}
+
+// ---------------------------------------------------------------------------
+// swq_moe_decode without a caller workspace: the workspace is `scratch`, a
+// static device array of kScratchBytes, one per GPU the library runs on,
+// held until the process ends.  Its layout places the single launch's
+// exchange regions at the compiled maxima, so calls on any layer and batch
+// share it: the epoch counters sit at a fixed place and every call's epoch
+// is above those of all words earlier calls left.  Calls that overlap in
+// time on one GPU race for it.
+
+constexpr size_t kScratchBytes = static_cast<size_t>(4) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+struct ScratchDevice {
+    std::once_flag once;
+    std::atomic<uint8_t *> ptr{nullptr};
+    std::atomic<int> status{SWQ_ERR_HIP};
+};
+ScratchDevice g_scratch_dev[64];
+}  // namespace
+
+// Once per device, with that device current: the array's device address
+// (in host code the array's name is only a stand-in, so it appears nowhere
+// but in HIP_SYMBOL here), the single launch's XCD probe (writing into the
+// array rather than into an allocation), then the whole array zero-filled by
+// a kernel.  Blocking (first call on a device only).
+static int scratch_for_device(hipStream_t stream, uint8_t **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return SWQ_ERR_HIP;
+    ScratchDevice &d = g_scratch_dev[dev];
+    std::call_once(d.once, [&]() {
+        void *p = nullptr;
+        int st = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess && p ? SWQ_OK : SWQ_ERR_HIP;
+        if (st == SWQ_OK) st = fused_probe_device(stream, p);
+        if (st == SWQ_OK) st = zero_fill(p, kScratchBytes, stream);
+        if (st == SWQ_OK && hipStreamSynchronize(stream) != hipSuccess) st = SWQ_ERR_HIP;
+        d.ptr.store(static_cast<uint8_t *>(p), std::memory_order_release);
+        d.status.store(st, std::memory_order_release);
+    });
+    const int st = d.status.load(std::memory_order_acquire);
+    if (st != SWQ_OK) return st;
+    *out = d.ptr.load(std::memory_order_acquire);
+    return SWQ_OK;
+}
+
+extern "C" int swq_moe_decode_noalloc(const swq_moe_layer *layer, const void *x, int x_dtype, int batch, void *out,
+                                      int out_dtype, int32_t *topk_ids, float *topk_weights, int flags,
+                                      void *stream) {
+    const int st0 = check_layer(layer, batch, SWQ_BF16);
+    if (st0 != SWQ_OK) return st0;
+    if (decode_ws_bytes(layer, batch, true) > kScratchBytes) return SWQ_ERR_LIMIT;
+    uint8_t *ws = nullptr;
+    const int st = scratch_for_device(static_cast<hipStream_t>(stream), &ws);
+    if (st != SWQ_OK) return st;
+    return moe_decode_impl(layer, x, x_dtype, batch, out, out_dtype, topk_ids, topk_weights, ws, kScratchBytes, flags,
+                           0, stream, true);
 }
