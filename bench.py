@@ -40,13 +40,14 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 
 # HBM bytes per launch from two rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE),
-# each scaled by what the counter reads for a 256 MiB device copy (FETCH x 2.0, WRITE x 1.0);
+# each scaled by what the counter reads for a 256 MiB device copy (FETCH x 2.0, WRITE x 1.0),
+# 48 distinct layers cycled;
 # the runs' commands and raw counts are kept with the kernel-trace summaries.  Keyed (workload, kernel).
 MEASURED_TRAFFIC = {
-    ("qwen3.6-35b-a3b-q4-b1", "moe_fused"): 18_163_424,
-    ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_692_148,
-    ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 14_590_849,
-    ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 5_743_112,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_fused"): 17_757_186,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_675_273,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 14_583_656,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 8_432_133,
     ("qwen3.6-35b-a3b-q4-prefill512", "gate_up"): 402_625_363,
     ("qwen3.6-35b-a3b-q4-prefill512", "down"): 209_861_891,
 }
