@@ -68,15 +68,30 @@ static __device__ unsigned long long g_swq_fused_trace[1024 * 4 * 16];
         }                                                                                               \
         return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_swq_fused_trace), bytes) == hipSuccess ? 0 : -1;  \
     }
-#define SWQ_STAMP(n)                                                                                  \
-    do {                                                                                              \
-        if ((threadIdx.x & 63) == 0)                                                                  \
-            g_swq_fused_trace[(blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + (n)] =                     \
-                __builtin_amdgcn_s_memrealtime();                                                     \
+// Stamps go to LDS as they are taken (a global store per stamp would join
+// the wave's vector-memory count, which every later load wait also drains)
+// and to the global array once, at the end of the kernel.
+#define SWQ_TRACE_DECL                                                                      \
+    __shared__ unsigned long long s_trace[4 * 16];                                          \
+    if ((threadIdx.x & 63) < 16) s_trace[(threadIdx.x >> 6) * 16 + (threadIdx.x & 63)] = 0
+#define SWQ_STAMP(n)                                                                        \
+    do {                                                                                    \
+        if ((threadIdx.x & 63) == 0) s_trace[(threadIdx.x >> 6) * 16 + (n)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#define SWQ_TRACE_FLUSH                                                                     \
+    do {                                                                                    \
+        __syncthreads();                                                                    \
+        if (threadIdx.x < 64) g_swq_fused_trace[blockIdx.x * 64 + threadIdx.x] = s_trace[threadIdx.x]; \
     } while (0)
 #else
+#define SWQ_TRACE_DECL \
+    do {               \
+    } while (0)
 #define SWQ_STAMP(n) \
     do {             \
+    } while (0)
+#define SWQ_TRACE_FLUSH \
+    do {                \
     } while (0)
 #endif
 
@@ -470,8 +485,8 @@ __device__ __forceinline__ float rounds_weight(const Rounds<M> &r, int K, int no
 // lane of the 8-bit router and shared-expert gate rows; M logits per lane
 // of the routing wave.
 
-template <int XDT, int GB, int GC, int GX, int GRI, int DB, int DRI, int RC, int M, bool PN>
-__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void moe_fused(FusedArgs a) {
+template <int XDT, int GB, int GC, int GX, int GRI, int DB, int DRI, int RC, int M, bool PN, int WPC>
+__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(WPC, WPC))) void moe_fused(FusedArgs a) {
     __shared__ int32_t s_ids[SWQ_MAX_TOPK];
     __shared__ float s_w[SWQ_MAX_TOPK];
     __shared__ __attribute__((aligned(16))) uint32_t s_hb[kMaxInterFused];   // a routed slot's activations
@@ -484,6 +499,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(1
     __shared__ float s_red[kFusedWaves];
 
     static_assert(sizeof(FusedArgs) <= 1024, "kernel arguments");
+    SWQ_TRACE_DECL;
     prefetch_kernargs();
     SWQ_STAMP(0);
     const int wave = threadIdx.x >> 6;
@@ -549,10 +565,13 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(1
     asm volatile("" : "+v"(lane));
     const LaneMap lmg = lane_map(a.gate.lpr_log2, lane);
     const LaneMap lmr = lane_map(a.router.lpr_log2, lane);
-    const int t_r = b + NB * wave;                            // first router tile of this wave
+    // the router and shared gate/up rows go to the first NF workgroups,
+    // which the hardware starts first
+    const int NF = NB / WPC;
+    const int t_r = b < NF ? b + NF * wave : a.E;                             // first router tile of this wave
     const bool has_r = t_r * lmr.rpw < a.E;
     const bool do_seg = a.has_shared && wave == 1;
-    const int t_s = b + NB * (kFusedWaves - 1 - wave);        // first shared gate/up tile
+    const int t_s = b < NF ? b + NF * (kFusedWaves - 1 - wave) : a.sh_tiles;  // first shared gate/up tile
     const bool has_s = a.has_shared && t_s < a.sh_tiles;
     RowTile<8, RC, 2, 1> rt;
     if (has_r) load_tile(rt, a.router, 0, lmr, t_r * lmr.rpw, a.E);
@@ -586,8 +605,8 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(1
     if (has_r || do_seg) {
         XSlice<8, RC, kXF32> xr;
         xslice_convert(xr, xrr);
-        for (int t = t_r; t * lmr.rpw < a.E; t += NB * kFusedWaves) {
-            // router tiles t_r, t_r + 4 NB, ...: one pass of rows each -> logits
+        for (int t = t_r; t * lmr.rpw < a.E; t += NF * kFusedWaves) {
+            // router tiles t_r, t_r + 4 NF, ...: one pass of rows each -> logits
             if (t != t_r) load_tile(rt, a.router, 0, lmr, t * lmr.rpw, a.E);
             float res[1];
             dot_rows(res, rt, a.router, xr, lmr);
@@ -611,8 +630,8 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(1
     XSlice<GB, GC, GX> xg;
     xslice_convert(xg, xgr);
     asm volatile("" : "+v"(lane));
-    for (int t = t_s; has_s && t < a.sh_tiles; t += NB * kFusedWaves) {
-        // shared-expert gate/up tiles t_s, t_s + 4 NB, ...: SwiGLU activations
+    for (int t = t_s; has_s && t < a.sh_tiles; t += NF * kFusedWaves) {
+        // shared-expert gate/up tiles t_s, t_s + 4 NF, ...: SwiGLU activations
         const int row0 = t * lmg.rpw;
         if (t != t_s) {
             load_tile(stg, a.sh_gate, 0, lmg, row0, a.Is);
@@ -800,37 +819,51 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(1
             __hip_atomic_store(a.gen + i, g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         SWQ_STAMP(9);
     }
+    SWQ_TRACE_FLUSH;
 }
 
 using FusedKernel = void (*)(FusedArgs);
 
-// Passes per tile, chosen so that a slot's gate/up and down rows at the
-// benchmark shapes are one tile per wave (I = 512 rows over the 128 waves of
-// a group: 4 rows per wave and matrix; H = 2048 down rows: 16 per wave).
-constexpr int gate_passes(int gb, int gc) { return gb == 4 && gc == 2 ? 2 : 4; }
-constexpr int down_passes(int db) { return db == 4 ? 4 : 8; }
+// Workgroups per CU: one, or two (two waves per SIMD) when a group's
+// routed bytes are large enough that the extra waves' dot products pay for
+// their start (measured: the 80B and 8-bit 35B steps gain, the 4-bit 35B
+// and single-expert steps lose).
+constexpr size_t kTwoPerCUBytes = static_cast<size_t>(5) << 19;  // 2.5 MiB per group
 
-template <int XDT, int GB, int GC, int GX, int DB, int RC, bool PN>
-static FusedKernel fused_by_m(int M) {
-    constexpr int GRI = gate_passes(GB, GC), DRI = down_passes(DB);
+// Passes per tile, chosen so that a slot's gate/up and down rows at the
+// benchmark shapes are one tile per wave (I = 512 rows over the 128 WPC
+// waves of a group: 4 / WPC rows per wave and matrix; H = 2048 down rows:
+// 16 / WPC per wave).
+constexpr int gate_passes(int gb, int gc, int wpc) { return (gb == 4 && gc == 2 ? 2 : 4) / wpc; }
+constexpr int down_passes(int db, int wpc) { return (db == 4 ? 4 : 8) / wpc; }
+
+template <int XDT, int GB, int GC, int GX, int DB, int RC, bool PN, int WPC>
+static FusedKernel fused_by_m_wpc(int M) {
+    constexpr int GRI = gate_passes(GB, GC, WPC), DRI = down_passes(DB, WPC);
     switch (M) {
-        case 1: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 1, PN>;
-        case 2: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 2, PN>;
-        case 4: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 4, PN>;
-        case 8: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 8, PN>;
-        default: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 16, PN>;
+        case 1: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 1, PN, WPC>;
+        case 2: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 2, PN, WPC>;
+        case 4: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 4, PN, WPC>;
+        case 8: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 8, PN, WPC>;
+        default: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 16, PN, WPC>;
     }
 }
 
+template <int XDT, int GB, int GC, int GX, int DB, int RC, bool PN>
+static FusedKernel fused_by_m(int M, int wpc) {
+    return wpc == 2 ? fused_by_m_wpc<XDT, GB, GC, GX, DB, RC, PN, 2>(M)
+                    : fused_by_m_wpc<XDT, GB, GC, GX, DB, RC, PN, 1>(M);
+}
 
 // Gate/up formats of the single launch: 4-bit codes, 8-bit codes with two
 // chunks per lane, 8-bit codes with one.
 enum FusedGateFormat { kFusedQ4 = 0, kFusedQ8C2 = 1, kFusedQ8C1 = 2 };
 
 // The instantiation for (gate/up format, router chunks per lane 2 or 1,
-// logits per routing lane M), one per activation format; nullptr for none.
-FusedKernel fused_select_bf16(int gfmt, bool rc2, int M);
-FusedKernel fused_select_f32(int gfmt, bool rc2, int M);
-FusedKernel fused_select_pn(int gfmt, bool rc2, int M);
+// logits per routing lane M, workgroups per CU), one per activation format;
+// nullptr for none.
+FusedKernel fused_select_bf16(int gfmt, bool rc2, int M, int wpc);
+FusedKernel fused_select_f32(int gfmt, bool rc2, int M, int wpc);
+FusedKernel fused_select_pn(int gfmt, bool rc2, int M, int wpc);
 
 }  // namespace swq
