@@ -24,11 +24,55 @@
 #include <atomic>
 #include <mutex>
 
+// Phase stamps of the staged kernels for timing studies (SWQ_FUSED_TRACE
+// builds only): s_memrealtime per (workgroup, wave, point) into LDS, copied
+// to a global array at the end of the kernel.
+#ifdef SWQ_FUSED_TRACE
+static __device__ unsigned long long g_swq_stage_trace[1024 * 8 * 16];
+extern "C" int swq_stage_trace(void *host, size_t bytes, int clear) {
+    if (clear) {
+        static unsigned long long z[1024 * 8 * 16];
+        return hipMemcpyToSymbol(HIP_SYMBOL(g_swq_stage_trace), z, sizeof(z)) == hipSuccess ? 0 : -1;
+    }
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_swq_stage_trace), bytes) == hipSuccess ? 0 : -1;
+}
+__device__ __forceinline__ unsigned long long *stage_trace_lds() {
+    __shared__ unsigned long long t[8 * 16];
+    return t;
+}
+#define STAGE_TRACE_DECL                                                                                \
+    if ((threadIdx.x & 63) < 16) stage_trace_lds()[(threadIdx.x >> 6) * 16 + (threadIdx.x & 63)] = 0
+#define STAGE_STAMP(n)                                                                                  \
+    do {                                                                                                \
+        if ((threadIdx.x & 63) == 0 && (n) < 16)                                                        \
+            stage_trace_lds()[(threadIdx.x >> 6) * 16 + (n)] = __builtin_amdgcn_s_memrealtime();       \
+    } while (0)
+#define STAGE_TRACE_FLUSH(base)                                                                         \
+    do {                                                                                                \
+        __syncthreads();                                                                                \
+        for (int i_ = threadIdx.x; i_ < 8 * 16; i_ += blockDim.x)                                       \
+            g_swq_stage_trace[((base) + blockIdx.x) * 128 + i_] =                                       \
+                i_ < static_cast<int>(blockDim.x >> 6) * 16 ? stage_trace_lds()[i_] : 0ull;             \
+    } while (0)
+#else
+#define STAGE_TRACE_DECL \
+    do {                 \
+    } while (0)
+#define STAGE_STAMP(n) \
+    do {               \
+    } while (0)
+#define STAGE_TRACE_FLUSH(base) \
+    do {                        \
+    } while (0)
+#endif
+
 namespace swq {
 
 constexpr int kThreads12 = 256;
 constexpr int kMaxPairs = SWQ_MAX_BATCH * SWQ_MAX_TOPK;
 constexpr int kRows3 = 16;  // stage-3 rows per workgroup (upper bound)
+constexpr int kStage2Blocks = 256;  // stage-2 workgroups at most: one per CU (one wave per SIMD)
+constexpr int kHeld3 = 2;           // stage-3 slots in flight per wave
 
 struct MoEArgs {
     QMat router, gate, up, down, sh_gate, sh_up, sh_down, seg;
@@ -89,104 +133,51 @@ struct MoEArgs {
     } while (0)
 
 // One tile of rows of one matrix against every token's x; the result of
-// (token b, row) goes to out[b*ld + row].
+// (token b, row) goes to out[b*ld + row].  Token b + 1's activations load
+// while token b's dot products run.
+template <int XDT, int BITS, int CPL, int ES, int XF>
+__device__ __forceinline__ void rows_token(const QMat &m, const LaneMap &lm, const RowTile<BITS, CPL, ES> &rt,
+                                           const XRaw<XDT, BITS, CPL> &xr, int row0, int row_end, float *out) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
+    XSlice<BITS, CPL, XF> xs;
+    xslice_convert(xs, xr);
+    float res[RI];
+    dot_tile(res, rt, xs, m, lm);
+    if (lm.j == lm.lpr - 1) {
+#pragma unroll
+        for (int i = 0; i < RI; ++i) {
+            const int row = row0 + i * lm.rpw + lm.q;
+            if (row < row_end) out[row] = res[i];
+        }
+    }
+}
+
 template <int XDT, int BITS, int CPL, int ES, int XF>
 __device__ __forceinline__ void gemv_rows_tokens(const QMat &m, int row0, int row_end, const void *x,
                                                  int H, int B, float *out, int ld, int lane) {
-    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
     const LaneMap lm = lane_map(m.lpr_log2, lane);
     RowTile<BITS, CPL, ES> rt;
     load_tile(rt, m, 0, lm, row0, row_end);
+    XRaw<XDT, BITS, CPL> xa, xb;
+    load_xraw<XDT>(xa, m, lm, x, 0);
 #pragma unroll 1
-    for (int b = 0; b < B; ++b) {
-        XSlice<BITS, CPL, XF> xs;
-        load_xslice<XDT>(xs, m, lm, x, static_cast<int64_t>(b) * H);
-        float res[RI];
-        dot_tile(res, rt, xs, m, lm);
-        if (lm.j == lm.lpr - 1) {
-#pragma unroll
-            for (int i = 0; i < RI; ++i) {
-                const int row = row0 + i * lm.rpw + lm.q;
-                if (row < row_end) out[b * ld + row] = res[i];
-            }
-        }
+    for (int b = 0; b < B; b += 2) {
+        if (b + 1 < B) load_xraw<XDT>(xb, m, lm, x, static_cast<int64_t>(b + 1) * H);
+        rows_token<XDT, BITS, CPL, ES, XF>(m, lm, rt, xa, row0, row_end, out + b * ld);
+        if (b + 1 >= B) break;
+        if (b + 2 < B) load_xraw<XDT>(xa, m, lm, x, static_cast<int64_t>(b + 2) * H);
+        rows_token<XDT, BITS, CPL, ES, XF>(m, lm, rt, xb, row0, row_end, out + (b + 1) * ld);
     }
 }
 
-// SwiGLU rows of one expert: h[p*ld + r] = silu(gate_r . x_b) * (up_r . x_b)
-// for each (token b, destination p) pair; pairs == nullptr means p = b.
+// SwiGLU rows of one tile for one token: h[r] = silu(gate_r . x) * (up_r . x).
 template <int XDT, int BITS, int CPL, int ES, int XF>
-__device__ __forceinline__ void gateup_rows(const QMat &g, const QMat &u, int64_t expert, int row0, int row_end,
-                                            const void *x, int H, const int32_t *pairs, int npairs, int K,
-                                            float *h, int ld, int lane) {
-    if (npairs <= 0) return;
+__device__ __forceinline__ void swiglu_token(const QMat &g, const QMat &u, const LaneMap &lm,
+                                             const RowTile<BITS, CPL, ES> &tg, const RowTile<BITS, CPL, ES> &tu,
+                                             const XRaw<XDT, BITS, CPL> &xr, int row0, int row_end, float *h) {
     constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
-    const LaneMap lm = lane_map(g.lpr_log2, lane);
-    RowTile<BITS, CPL, ES> tg, tu;
-    load_tile(tg, g, expert, lm, row0, row_end);
-    load_tile(tu, u, expert, lm, row0, row_end);
-#pragma unroll 1
-    for (int pi = 0; pi < npairs; ++pi) {
-        const int p = pairs ? pairs[pi] : pi;
-        const int b = pairs ? p / K : pi;
-        XSlice<BITS, CPL, XF> xs;
-        load_xslice<XDT>(xs, g, lm, x, static_cast<int64_t>(b) * H);
-        float rg[RI], ru[RI];
-        dot_tile(rg, tg, xs, g, lm);
-        dot_tile(ru, tu, xs, u, lm);
-        if (lm.j == lm.lpr - 1) {
-#pragma unroll
-            for (int i = 0; i < RI; ++i) {
-                const int row = row0 + i * lm.rpw + lm.q;
-                if (row < row_end) h[static_cast<int64_t>(p) * ld + row] = swiglu(rg[i], ru[i]);
-            }
-        }
-    }
-}
-
-// Down rows [row0, row0 + nrows) of one expert for each pair p: the dot of
-// the row with h[p] lands in part[part_base + p][row - row0].
-template <int XDT, int BITS, int CPL, int ES, int XF>
-__device__ __forceinline__ void down_rows(const QMat &m, int64_t expert, int row0, int nrows, int row_end,
-                                          const float *h, int ld, const int32_t *pairs, int npairs,
-                                          float (*part)[kRows3], int part_base, int lane) {
-    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
-    const LaneMap lm = lane_map(m.lpr_log2, lane);
-    const int end = min(row0 + nrows, row_end);
-#pragma unroll 1
-    for (int t0 = row0; t0 < end; t0 += RI * lm.rpw) {
-        RowTile<BITS, CPL, ES> rt;
-        load_tile(rt, m, expert, lm, t0, end);
-#pragma unroll 1
-        for (int pi = 0; pi < npairs; ++pi) {
-            const int p = pairs ? pairs[pi] : pi;
-            XSlice<BITS, CPL, XF> xs;
-            load_xslice<XDT>(xs, m, lm, h, static_cast<int64_t>(p) * ld);
-            float res[RI];
-            dot_tile(res, rt, xs, m, lm);
-            if (lm.j == lm.lpr - 1) {
-#pragma unroll
-                for (int i = 0; i < RI; ++i) {
-                    const int row = t0 + i * lm.rpw + lm.q;
-                    if (row < end) part[part_base + p][row - row0] = res[i];
-                }
-            }
-        }
-    }
-}
-
-
-// Batch-1 SwiGLU rows of expert e, the pick in slot `slot`.
-template <int XDT, int BITS, int CPL, int ES, int XF>
-__device__ __forceinline__ void gateup_rows_b1(const QMat &g, const QMat &u, int e, int slot, int row0,
-                                               int row_end, const void *x, float *h, int ld, int lane) {
-    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
-    const LaneMap lm = lane_map(g.lpr_log2, lane);
-    RowTile<BITS, CPL, ES> tg, tu;
-    load_tile(tg, g, e, lm, row0, row_end);
-    load_tile(tu, u, e, lm, row0, row_end);
     XSlice<BITS, CPL, XF> xs;
-    load_xslice<XDT>(xs, g, lm, x, 0);
+    xslice_convert(xs, xr);
     float rg[RI], ru[RI];
     dot_tile(rg, tg, xs, g, lm);
     dot_tile(ru, tu, xs, u, lm);
@@ -194,36 +185,131 @@ __device__ __forceinline__ void gateup_rows_b1(const QMat &g, const QMat &u, int
 #pragma unroll
         for (int i = 0; i < RI; ++i) {
             const int row = row0 + i * lm.rpw + lm.q;
-            if (row < row_end) h[static_cast<int64_t>(slot) * ld + row] = swiglu(rg[i], ru[i]);
+            if (row < row_end) h[row] = swiglu(rg[i], ru[i]);
         }
     }
 }
 
-// Batch-1 down rows [row0, row0 + nrows) of the expert in slot `slot` (or of
-// the shared expert when ids == nullptr) against activations hv.
+// SwiGLU rows of one expert for every token b: h[b*ld + r] = silu(gate_r .
+// x_b) * (up_r . x_b); token b + 1's activations load while token b's dot
+// products run.
 template <int XDT, int BITS, int CPL, int ES, int XF>
-__device__ __forceinline__ void down_rows_b1(const QMat &m, const int32_t *ids, int slot, int row0, int nrows,
-                                             int row_end, const float *hv, float (*part)[kRows3], int part_row,
-                                             int lane) {
-    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
-    const LaneMap lm = lane_map(m.lpr_log2, lane);
-    const int end = min(row0 + nrows, row_end);
-    XSlice<BITS, CPL, XF> xs;
-    load_xslice<XDT>(xs, m, lm, hv, 0);
-    const int64_t e = ids ? ids[slot] : 0;
+__device__ __forceinline__ void gateup_rows_tokens(const QMat &g, const QMat &u, int64_t expert, int row0,
+                                                   int row_end, const void *x, int H, int B, float *h, int ld,
+                                                   int lane) {
+    const LaneMap lm = lane_map(g.lpr_log2, lane);
+    RowTile<BITS, CPL, ES> tg, tu;
+    load_tile(tg, g, expert, lm, row0, row_end);
+    load_tile(tu, u, expert, lm, row0, row_end);
+    XRaw<XDT, BITS, CPL> xa, xb;
+    load_xraw<XDT>(xa, g, lm, x, 0);
 #pragma unroll 1
-    for (int t0 = row0; t0 < end; t0 += RI * lm.rpw) {
-        RowTile<BITS, CPL, ES> rt;
-        load_tile(rt, m, e, lm, t0, end);
-        float res[RI];
-        dot_tile(res, rt, xs, m, lm);
-        if (lm.j == lm.lpr - 1) {
+    for (int b = 0; b < B; b += 2) {
+        if (b + 1 < B) load_xraw<XDT>(xb, g, lm, x, static_cast<int64_t>(b + 1) * H);
+        swiglu_token<XDT, BITS, CPL, ES, XF>(g, u, lm, tg, tu, xa, row0, row_end, h + static_cast<int64_t>(b) * ld);
+        if (b + 1 >= B) break;
+        if (b + 2 < B) load_xraw<XDT>(xa, g, lm, x, static_cast<int64_t>(b + 2) * H);
+        swiglu_token<XDT, BITS, CPL, ES, XF>(g, u, lm, tg, tu, xb, row0, row_end,
+                                             h + static_cast<int64_t>(b + 1) * ld);
+    }
+}
+
+// One down tile against one activation row hv: the dot of each row with hv
+// lands in prow[row - r0].
+template <int BITS, int ES, int XF>
+__device__ __forceinline__ void down_tile_row(const QMat &m, const LaneMap &lm, const RowTile<BITS, 1, ES> &dt,
+                                              const XRaw<SWQ_F32, BITS, 1> &xr, int r0, int end, float *prow) {
+    constexpr int RI = RowTile<BITS, 1, ES>::kRI;
+    XSlice<BITS, 1, XF> xs;
+    xslice_convert(xs, xr);
+    float res[RI];
+    dot_tile(res, dt, xs, m, lm);
+    if (lm.j == lm.lpr - 1) {
 #pragma unroll
-            for (int i = 0; i < RI; ++i) {
-                const int row = t0 + i * lm.rpw + lm.q;
-                if (row < end) part[part_row][row - row0] = res[i];
+        for (int i = 0; i < RI; ++i) {
+            const int row = r0 + i * lm.rpw + lm.q;
+            if (row < end) prow[row - r0] = res[i];
+        }
+    }
+}
+
+// Stage 3's copy of the distinct slots (for batch 1, the picks) in LDS:
+// expert, pair count and pair list of each.
+struct Slots {
+    int32_t e[kMaxPairs];
+    int32_t np[kMaxPairs];
+    int16_t pairs[kMaxPairs * SWQ_MAX_BATCH];  // [slot][B]
+    int32_t n;
+};
+
+// Stage 3's routed slots for one wave: slots s = s0, s0 + ds, ... below nu,
+// each one down tile (rows [r0, r0 + rows3)) against every pair of the slot,
+// results to part[p][row - r0].  kHeld3 slots' tiles and first activation
+// rows are in flight at once.
+template <int XDT, int BITS, int CPL, int ES, int XF>
+__device__ __forceinline__ void down_slots(const MoEArgs &a, const Slots &sl, int s0, int ds, int nu, int r0,
+                                           float (*part)[kRows3], int lane) {
+    static_assert(XDT == SWQ_F32 && CPL == 1, "down rows read fp32 activations, one chunk per lane");
+    if (s0 >= nu) return;
+    const LaneMap lm = lane_map(a.down.lpr_log2, lane);
+    const int end = min(r0 + a.rows3, a.H);
+    using Tile = RowTile<BITS, 1, ES>;
+    using Raw = XRaw<SWQ_F32, BITS, 1>;
+    auto first_pair = [&](int s) { return static_cast<int>(sl.pairs[s * a.B]); };
+    auto issue = [&](Tile &t, Raw &xr, int s) __attribute__((always_inline)) {
+        load_tile(t, a.down, sl.e[s], lm, r0, end);
+        load_xraw<SWQ_F32>(xr, a.down, lm, a.h, static_cast<int64_t>(first_pair(s)) * a.I);
+    };
+    auto run = [&](const Tile &t, const Raw &xr, int s) __attribute__((always_inline)) {
+        down_tile_row<BITS, ES, XF>(a.down, lm, t, xr, r0, end, part[first_pair(s)]);
+        const int np = sl.np[s];
+        for (int pi = 1; pi < np; ++pi) {
+            const int p = sl.pairs[s * a.B + pi];
+            Raw xo;
+            load_xraw<SWQ_F32>(xo, a.down, lm, a.h, static_cast<int64_t>(p) * a.I);
+            down_tile_row<BITS, ES, XF>(a.down, lm, t, xo, r0, end, part[p]);
+        }
+    };
+    // a ring of kHeld3 slots in flight: slot j of each round reuses the
+    // buffers of slot j of the previous round
+    Tile t[kHeld3];
+    Raw x[kHeld3];
+#pragma unroll
+    for (int j = 0; j < kHeld3; ++j)
+        if (s0 + ds * j < nu) issue(t[j], x[j], s0 + ds * j);
+    int k = 2;
+    for (int base = 0; s0 + ds * base < nu; base += kHeld3) {
+#pragma unroll
+        for (int j = 0; j < kHeld3; ++j) {
+            const int sj = s0 + ds * (base + j);
+            if (sj < nu) {
+                run(t[j], x[j], sj);
+                STAGE_STAMP(k);
+                ++k;
+                if (sj + ds * kHeld3 < nu) issue(t[j], x[j], sj + ds * kHeld3);
             }
         }
+    }
+}
+
+// The shared expert's down tile for every token b: part[P + b][row - r0].
+template <int XDT, int BITS, int CPL, int ES, int XF>
+__device__ __forceinline__ void down_shared(const MoEArgs &a, int r0, float (*part)[kRows3], int lane) {
+    static_assert(XDT == SWQ_F32 && CPL == 1, "down rows read fp32 activations, one chunk per lane");
+    const LaneMap lm = lane_map(a.sh_down.lpr_log2, lane);
+    const int end = min(r0 + a.rows3, a.H);
+    RowTile<BITS, 1, ES> t;
+    load_tile(t, a.sh_down, 0, lm, r0, end);
+    XRaw<SWQ_F32, BITS, 1> xa, xb;
+    load_xraw<SWQ_F32>(xa, a.sh_down, lm, a.h_sh, 0);
+    const int P = a.B * a.K;
+#pragma unroll 1
+    for (int b = 0; b < a.B; b += 2) {
+        if (b + 1 < a.B) load_xraw<SWQ_F32>(xb, a.sh_down, lm, a.h_sh, static_cast<int64_t>(b + 1) * a.Is);
+        down_tile_row<BITS, ES, XF>(a.sh_down, lm, t, xa, r0, end, part[P + b]);
+        if (b + 1 >= a.B) break;
+        if (b + 2 < a.B) load_xraw<SWQ_F32>(xa, a.sh_down, lm, a.h_sh, static_cast<int64_t>(b + 2) * a.Is);
+        down_tile_row<BITS, ES, XF>(a.sh_down, lm, t, xb, r0, end, part[P + b + 1]);
     }
 }
 
@@ -308,16 +394,16 @@ struct Routing {
     int32_t slot[kMaxPairs];   // distinct slot of a leading pair
     int32_t uniq_e[kMaxPairs];
     int32_t uniq_np[kMaxPairs];
-    int32_t pairs[SWQ_MAX_BATCH];  // pairs of this block's slot
+    int16_t upairs[kMaxPairs * SWQ_MAX_BATCH];  // [slot][B]: each distinct slot's pairs, in pair order
     int32_t n_unique;
 };
 
 // Every token's top-k into r (one wave per token), then for batches the
 // distinct experts in order of first appearance, each with its pairs in pair
-// order (one thread per pair, two O(P) passes).  `my_slot` selects whose pair
-// list lands in r.pairs; with `publish` the block also writes the routing to
-// the workspace (and the caller's outputs) for stage 3.
-__device__ __forceinline__ void route(const MoEArgs &a, Routing &r, int my_slot, bool publish) {
+// order (one thread per pair, two O(P) passes) in r.upairs; with `publish`
+// the block also writes the routing to the workspace (and the caller's
+// outputs) for stage 3.
+__device__ __forceinline__ void route(const MoEArgs &a, Routing &r, bool publish) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int M = (a.E + kWave - 1) / kWave;
     for (int b = wave; b < a.B; b += kThreads12 / kWave) {
@@ -377,7 +463,7 @@ __device__ __forceinline__ void route(const MoEArgs &a, Routing &r, int my_slot,
     __syncthreads();
     if (p < P) {
         const int slot = r.slot[first];
-        if (slot == my_slot) r.pairs[pos] = p;
+        r.upairs[slot * a.B + pos] = static_cast<int16_t>(p);
         if (publish) a.uniq_pairs[slot * a.B + pos] = p;
     }
     __syncthreads();
@@ -407,6 +493,7 @@ __device__ __forceinline__ uint32_t touch_share(const QMat &m, int64_t expert, i
 
 __device__ __forceinline__ void keep(uint32_t v) { asm volatile("" ::"v"(v)); }
 
+
 template <int XDT>
 __global__ __launch_bounds__(kThreads12) void moe_stage1(MoEArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -426,78 +513,160 @@ __global__ __launch_bounds__(kThreads12) void moe_stage1(MoEArgs a) {
     if (st == 0) {
         SWQ_DISPATCH(XDT, a.seg, gemv_rows_tokens, a.seg, 0, 1, a.x, a.H, a.B, a.sg, 1, lane);
     } else if (st - 1 < a.shared_tasks) {
-        SWQ_DISPATCH(XDT, a.sh_gate, gateup_rows, a.sh_gate, a.sh_up, 0, (st - 1) * tile_rows(a.sh_gate), a.Is,
-                     a.x, a.H, nullptr, a.B, a.K, a.h_sh, a.Is, lane);
+        SWQ_DISPATCH(XDT, a.sh_gate, gateup_rows_tokens, a.sh_gate, a.sh_up, 0, (st - 1) * tile_rows(a.sh_gate),
+                     a.Is, a.x, a.H, a.B, a.h_sh, a.Is, lane);
     }
     keep(t);
 }
 
+// Stage 2's work for one wave: units u0, u0 + W, ... below nu, unit u the
+// gate/up row tile u % tps of distinct slot u / tps, for every token pair of
+// the slot: h[p][row] = silu(gate_row . x_b) * (up_row . x_b).  The next
+// unit's tiles and first activation slice load while the current unit's dot
+// products run.
+__device__ __forceinline__ int64_t unit_expert(const MoEArgs &a, const Routing &r, int s) {
+    return a.B == 1 ? r.ids[s] : r.uniq_e[s];
+}
+__device__ __forceinline__ int unit_pair(const MoEArgs &a, const Routing &r, int s, int pi) {
+    return a.B == 1 ? s : r.upairs[s * a.B + pi];
+}
+
+template <int XDT, int BITS, int CPL, int ES>
+__device__ __forceinline__ void gateup_issue(const MoEArgs &a, const Routing &r, const LaneMap &lm, int tps, int u,
+                                             RowTile<BITS, CPL, ES> &tg, RowTile<BITS, CPL, ES> &tu,
+                                             XRaw<XDT, BITS, CPL> &xr) {
+    const int s = u / tps, t = u - s * tps, rows = RowTile<BITS, CPL, ES>::kRI * lm.rpw;
+    const int64_t e = unit_expert(a, r, s);
+    load_tile(tg, a.gate, e, lm, t * rows, a.I);
+    load_tile(tu, a.up, e, lm, t * rows, a.I);
+    load_xraw<XDT>(xr, a.gate, lm, a.x, static_cast<int64_t>(unit_pair(a, r, s, 0) / a.K) * a.H);
+}
+
+template <int BITS, int CPL, int ES, int XF>
+__device__ __forceinline__ void gateup_pair(const MoEArgs &a, const LaneMap &lm, int row0, int p,
+                                            const RowTile<BITS, CPL, ES> &tg, const RowTile<BITS, CPL, ES> &tu,
+                                            const XSlice<BITS, CPL, XF> &xs) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
+    float rg[RI], ru[RI];
+    dot_tile(rg, tg, xs, a.gate, lm);
+    dot_tile(ru, tu, xs, a.up, lm);
+    if (lm.j == lm.lpr - 1) {
+#pragma unroll
+        for (int i = 0; i < RI; ++i) {
+            const int row = row0 + i * lm.rpw + lm.q;
+            if (row < a.I) a.h[static_cast<int64_t>(p) * a.I + row] = swiglu(rg[i], ru[i]);
+        }
+    }
+}
+
+template <int XDT, int BITS, int CPL, int ES, int XF>
+__device__ __forceinline__ void gateup_run(const MoEArgs &a, const Routing &r, const LaneMap &lm, int tps, int u,
+                                           const RowTile<BITS, CPL, ES> &tg, const RowTile<BITS, CPL, ES> &tu,
+                                           const XRaw<XDT, BITS, CPL> &xr) {
+    constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
+    const int s = u / tps, t = u - s * tps, row0 = t * RI * lm.rpw;
+    {
+        // the first pair from the prefetched activations; the rest (tokens
+        // sharing this expert) load theirs here.  Kept apart so the two
+        // sources are never one runtime-selected array.
+        XSlice<BITS, CPL, XF> xs;
+        xslice_convert(xs, xr);
+        gateup_pair(a, lm, row0, unit_pair(a, r, s, 0), tg, tu, xs);
+    }
+    const int np = a.B == 1 ? 1 : r.uniq_np[s];
+    for (int pi = 1; pi < np; ++pi) {
+        const int p = unit_pair(a, r, s, pi);
+        XSlice<BITS, CPL, XF> xs;
+        load_xslice<XDT>(xs, a.gate, lm, a.x, static_cast<int64_t>(p / a.K) * a.H);
+        gateup_pair(a, lm, row0, p, tg, tu, xs);
+    }
+}
+
+template <int XDT, int BITS, int CPL, int ES, int XF>
+__device__ __forceinline__ void gateup_units(const MoEArgs &a, const Routing &r, int u0, int W, int tps, int nu,
+                                             int lane) {
+    if (u0 >= nu) return;
+    const LaneMap lm = lane_map(a.gate.lpr_log2, lane);
+    RowTile<BITS, CPL, ES> tg0, tu0, tg1, tu1;
+    XRaw<XDT, BITS, CPL> xr0, xr1;
+    gateup_issue<XDT>(a, r, lm, tps, u0, tg0, tu0, xr0);
+    int k = 2;
+    for (int u = u0; u < nu; u += 2 * W) {
+        if (u + W < nu) gateup_issue<XDT>(a, r, lm, tps, u + W, tg1, tu1, xr1);
+        gateup_run<XDT, BITS, CPL, ES, XF>(a, r, lm, tps, u, tg0, tu0, xr0);
+        STAGE_STAMP(k);
+        ++k;
+        if (u + W >= nu) break;
+        if (u + 2 * W < nu) gateup_issue<XDT>(a, r, lm, tps, u + 2 * W, tg0, tu0, xr0);
+        gateup_run<XDT, BITS, CPL, ES, XF>(a, r, lm, tps, u + W, tg1, tu1, xr1);
+        STAGE_STAMP(k);
+        ++k;
+    }
+}
+
+// Every workgroup routes (softmax, top-k, distinct experts) from the logits
+// itself, then its waves take the (slot, row tile) units of the distinct
+// experts' gate/up rows grid-stride.
 template <int XDT>
 __global__ __launch_bounds__(kThreads12) void moe_stage2(MoEArgs a) {
     __shared__ Routing r;
-    const int slot = blockIdx.y;
+    STAGE_TRACE_DECL;
+    STAGE_STAMP(0);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    route(a, r, slot, blockIdx.x == 0 && blockIdx.y == 0);
-    if (slot >= r.n_unique) return;
-    const int e = a.B == 1 ? r.ids[slot] : r.uniq_e[slot];
-    const uint32_t t = touch_share(a.down, e, blockIdx.x, gridDim.x);
-    const int row0 = (blockIdx.x * (kThreads12 / kWave) + wave) * tile_rows(a.gate);
-    if (row0 < a.I) {
-        if (a.B == 1) {
-            SWQ_DISPATCH(XDT, a.gate, gateup_rows_b1, a.gate, a.up, e, slot, row0, a.I, a.x, a.h, a.I, lane);
-        } else {
-            SWQ_DISPATCH(XDT, a.gate, gateup_rows, a.gate, a.up, e, row0, a.I, a.x, a.H, r.pairs,
-                         r.uniq_np[slot], a.K, a.h, a.I, lane);
-        }
-    }
-    keep(t);
+    route(a, r, blockIdx.x == 0);
+    STAGE_STAMP(1);
+    const int rows = tile_rows(a.gate);
+    const int tps = (a.I + rows - 1) / rows;
+    const int nu = r.n_unique * tps;
+    const int W = gridDim.x * (kThreads12 / kWave);
+    SWQ_DISPATCH(XDT, a.gate, gateup_units, a, r, blockIdx.x * (kThreads12 / kWave) + wave, W, tps, nu, lane);
+    STAGE_STAMP(15);
+    STAGE_TRACE_FLUSH(0);
 }
 
-constexpr int kStage3MaxWaves = 12;
+constexpr int kStage3MaxWaves = 8;
 
 __global__ __launch_bounds__(kStage3MaxWaves * 64) void moe_stage3(MoEArgs a) {
     __shared__ float part[kMaxPairs + SWQ_MAX_BATCH][kRows3];
     __shared__ float s_w[kMaxPairs];
     __shared__ float s_gate[SWQ_MAX_BATCH];
+    __shared__ Slots sl;
+    STAGE_TRACE_DECL;
+    STAGE_STAMP(0);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nw = blockDim.x >> 6;
     const int r0 = blockIdx.x * a.rows3;
     const int P = a.B * a.K;
+    // the routing stage 2 published, into LDS in one round trip: every
+    // slot's expert and pairs (entries past the distinct count unused)
+    for (int t = threadIdx.x; t < P; t += blockDim.x) {
+        sl.e[t] = a.B == 1 ? a.ids[t] : a.uniq_e[t];
+        sl.np[t] = a.B == 1 ? 1 : a.uniq_np[t];
+    }
+    for (int t = threadIdx.x; t < P * a.B; t += blockDim.x)
+        sl.pairs[t] = static_cast<int16_t>(a.B == 1 ? t : a.uniq_pairs[t]);
+    if (threadIdx.x == 0) sl.n = a.B == 1 ? a.K : *a.n_unique;
     // combine weights and shared-gate logits: loaded into registers now,
     // staged in LDS only after the projections, so their latency overlaps.
-    float w_pre[4];  // P <= 4 * blockDim (the host sizes the block 64*min(12, slots))
+    float w_pre[4];  // P <= 4 * blockDim (the host sizes the block 64*min(8, slots))
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const unsigned t = threadIdx.x + i * blockDim.x;
         w_pre[i] = t < static_cast<unsigned>(P) ? a.wts[t] : 0.f;
     }
     const float sg_pre = (a.has_shared && threadIdx.x < static_cast<unsigned>(a.B)) ? a.sg[threadIdx.x] : 0.f;
-    if (a.B == 1) {
-        const int nslots = a.K + (a.has_shared ? 1 : 0);
-#pragma unroll 1
-        for (int s = wave; s < nslots; s += nw) {
-            if (s < a.K) {
-                SWQ_DISPATCH_DOWN(a.down, down_rows_b1, a.down, a.ids, s, r0, a.rows3, a.H,
-                                  a.h + static_cast<int64_t>(s) * a.I, part, s, lane);
-            } else {
-                SWQ_DISPATCH_DOWN(a.sh_down, down_rows_b1, a.sh_down, nullptr, 0, r0, a.rows3, a.H, a.h_sh,
-                                  part, P, lane);
-            }
-        }
-    } else {
-        const int nu = *a.n_unique;
-        const int nslots = nu + (a.has_shared ? 1 : 0);
-#pragma unroll 1
-        for (int s = wave; s < nslots; s += nw) {
-            if (s < nu) {
-                SWQ_DISPATCH_DOWN(a.down, down_rows, a.down, a.uniq_e[s], r0, a.rows3, a.H, a.h, a.I,
-                                  a.uniq_pairs + s * a.B, a.uniq_np[s], part, 0, lane);
-            } else {
-                SWQ_DISPATCH_DOWN(a.sh_down, down_rows, a.sh_down, 0, r0, a.rows3, a.H, a.h_sh, a.Is,
-                                  nullptr, a.B, part, P, lane);
-            }
-        }
+    // routed slots on every wave, the shared expert's on the wave with the
+    // fewest routed ones (first, so its loads start with the others')
+    __syncthreads();  // sl
+    STAGE_STAMP(1);
+    // the shared expert's tile on the wave with the fewest routed slots
+    // (first, so its loads start with the others'), then the routed slots
+    if (a.has_shared && wave == sl.n % nw) {
+        SWQ_DISPATCH_DOWN(a.sh_down, down_shared, a, r0, part, lane);
+        STAGE_STAMP(13);
     }
+    SWQ_DISPATCH_DOWN(a.down, down_slots, a, sl, wave, nw, sl.n, r0, part, lane);
+    STAGE_STAMP(14);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const unsigned t = threadIdx.x + i * blockDim.x;
@@ -522,6 +691,8 @@ __global__ __launch_bounds__(kStage3MaxWaves * 64) void moe_stage3(MoEArgs a) {
             out[o] = a.accumulate ? out[o] + acc : acc;
         }
     }
+    STAGE_STAMP(15);
+    STAGE_TRACE_FLUSH(512);
 }
 
 // Zero-fills n bytes (a fill kernel rather than hipMemsetAsync, so that a
@@ -685,8 +856,8 @@ static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtyp
 
     const int P = batch * a.K;
     const int max_slots = min(P, a.E);
-    const int rows2 = tile_rows(a.gate) * waves12;
-    const dim3 grid2((a.I + rows2 - 1) / rows2, max_slots);
+    const int tps2 = (a.I + tile_rows(a.gate) - 1) / tile_rows(a.gate);
+    const dim3 grid2(min(kStage2Blocks, (max_slots * tps2 + waves12 - 1) / waves12));
     if (stage_mask & 2) {
         if (x_dtype == SWQ_BF16) hipLaunchKernelGGL(moe_stage2<SWQ_BF16>, grid2, dim3(kThreads12), 0, s, a);
         else hipLaunchKernelGGL(moe_stage2<SWQ_F32>, grid2, dim3(kThreads12), 0, s, a);
