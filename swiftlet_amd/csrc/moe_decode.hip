@@ -1,10 +1,11 @@
 // MoE-layer decode step on gfx950: three launches per layer.
 //
-//   stage 1  router GEMV, shared-expert gate GEMV, shared gate/up SwiGLU.
-//   stage 2  every workgroup runs softmax, top-k and renormalisation on the
-//            router logits itself (and, for batches, the distinct-expert
-//            list), then the gate/up SwiGLU rows of its expert: one launch for
-//            all selected experts, indexed by device-resident ids.
+//   stage 1  router GEMV, shared-expert gate GEMV, shared gate/up SwiGLU;
+//            the last router workgroup to finish runs softmax, top-k and
+//            renormalisation for every token and (for batches) the
+//            distinct-expert list, and publishes them.
+//   stage 2  the gate/up SwiGLU rows of every selected expert: one launch
+//            for all of them, indexed by the device-resident tables.
 //   stage 3  down projections of the selected experts and of the shared
 //            expert, weighted combine in pick order, then the shared term.
 //
@@ -90,6 +91,7 @@ struct MoEArgs {
     int32_t *uniq_np;      // [P] pairs per distinct expert
     int32_t *uniq_pairs;   // [P][B] pair indices b*K + k
     float *h;              // [P][I] routed SwiGLU activations, by pair
+    int32_t *arrive;       // stage-1 router workgroups done (the last one routes)
     int32_t xdt, odt, accumulate;
     int32_t B, H, E, K, I, Is, norm, has_shared;
     int32_t nr_blocks;     // stage-1 workgroups holding router rows
@@ -97,6 +99,28 @@ struct MoEArgs {
     int32_t shared_tasks;  // waves with shared gate/up rows
     int32_t rows3;         // stage-3 rows per workgroup
 };
+
+// The routing stage 1 published (for batch 1, the picks; for batches, the
+// distinct experts), in LDS: expert, pair count and pair list of each slot.
+struct Slots {
+    int32_t e[kMaxPairs];
+    int32_t np[kMaxPairs];
+    int16_t pairs[kMaxPairs * SWQ_MAX_BATCH];  // [slot][B]
+    int32_t n;
+};
+
+// Loads the published routing into sl in one round trip (entries past the
+// slot count unused); the caller synchronises before reading it.
+__device__ __forceinline__ void load_slots(const MoEArgs &a, Slots &sl) {
+    const int P = a.B * a.K;
+    for (int t = threadIdx.x; t < P; t += blockDim.x) {
+        sl.e[t] = a.B == 1 ? a.ids[t] : a.uniq_e[t];
+        sl.np[t] = a.B == 1 ? 1 : a.uniq_np[t];
+    }
+    for (int t = threadIdx.x; t < P * a.B; t += blockDim.x)
+        sl.pairs[t] = static_cast<int16_t>(a.B == 1 ? t : a.uniq_pairs[t]);
+    if (threadIdx.x == 0) sl.n = a.B == 1 ? a.K : *a.n_unique;
+}
 
 // Wave-uniform dispatch over a matrix's plan (bits, chunks per lane,
 // activation format) and scale bytes.  FN<XDT, BITS, CPL, ES, XF>.
@@ -233,14 +257,6 @@ __device__ __forceinline__ void down_tile_row(const QMat &m, const LaneMap &lm, 
     }
 }
 
-// Stage 3's copy of the distinct slots (for batch 1, the picks) in LDS:
-// expert, pair count and pair list of each.
-struct Slots {
-    int32_t e[kMaxPairs];
-    int32_t np[kMaxPairs];
-    int16_t pairs[kMaxPairs * SWQ_MAX_BATCH];  // [slot][B]
-    int32_t n;
-};
 
 // Stage 3's routed slots for one wave: slots s = s0, s0 + ds, ... below nu,
 // each one down tile (rows [r0, r0 + rows3)) against every pair of the slot,
@@ -277,7 +293,7 @@ __device__ __forceinline__ void down_slots(const MoEArgs &a, const Slots &sl, in
 #pragma unroll
     for (int j = 0; j < kHeld3; ++j)
         if (s0 + ds * j < nu) issue(t[j], x[j], s0 + ds * j);
-    int k = 2;
+    [[maybe_unused]] int k = 2;
     for (int base = 0; s0 + ds * base < nu; base += kHeld3) {
 #pragma unroll
         for (int j = 0; j < kHeld3; ++j) {
@@ -316,80 +332,26 @@ __device__ __forceinline__ void down_shared(const MoEArgs &a, int r0, float (*pa
 // ---------------------------------------------------------------------------
 // top-k (one wave per token)
 
-// Top-k of one token's router logits, one wave.  Selection by logit with
-// ties to the lower expert id equals the reference's selection by softmax
-// probability (QwenCPUModel.swift:508-522; softmax is monotonic) up to fp32
-// ties of exp().  Lane l holds experts l*M .. l*M+M-1 as 64-bit keys
-// (orderable logit, inverted id), sorted descending; each of the K rounds
-// takes the wave-wide maximum head.  Then p_k = exp(l_k - max) / sum_e
-// exp(l_e - max) (:65-71) and w_k = p_k / sum_j p_j when norm (:546-550).
-// Writes ids[k], w[k] (LDS); sel_l is LDS scratch of K floats.
+// Top-k of one token's router logits on one wave (the rounds of route.hpp):
+// picks to ids[k] in pick order, combine weights to w[k].  The same picks,
+// weights and summation order as the single launch's routing wave.
 template <int M>
 __device__ __forceinline__ void topk_token(const float *lrow, int E, int K, int norm, int lane, int32_t *ids,
-                                           float *w, float *sel_l) {
-    float lg[M];
+                                           float *w) {
+    float v[M];
 #pragma unroll
-    for (int j = 0; j < M; ++j) lg[j] = lrow[min(lane * M + j, E - 1)];  // every load issued first
-    uint64_t key[M];
-#pragma unroll
-    for (int j = 0; j < M; ++j) {
-        const int e = lane * M + j;
-        const bool valid = e < E;
-        key[j] = valid ? (static_cast<uint64_t>(orderable(lg[j])) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(e))
-                       : 0;
-        if (!valid) lg[j] = -INFINITY;
-    }
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-#pragma unroll
-        for (int j = 0; j + 1 < M - i; ++j) {
-            if (key[j] < key[j + 1]) {
-                const uint64_t t = key[j];
-                key[j] = key[j + 1];
-                key[j + 1] = t;
-            }
-        }
-    }
-    float top = 0.f;
-    for (int k = 0; k < K; ++k) {
-        const uint32_t hi = static_cast<uint32_t>(key[0] >> 32);
-        const uint32_t lo = static_cast<uint32_t>(key[0]);
-        const uint32_t mhi = wave_max_u32(hi);
-        const uint64_t cand = __ballot(hi == mhi);
-        int winner;
-        if (__popcll(cand) == 1) {
-            winner = __ffsll(static_cast<long long>(cand)) - 1;
-        } else {
-            const uint32_t mlo = wave_max_u32(hi == mhi ? lo : 0u);
-            winner = __ffsll(static_cast<long long>(__ballot(hi == mhi && lo == mlo))) - 1;
-        }
-        const uint32_t wlo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo), winner));
-        const float l = from_orderable(mhi);
-        if (k == 0) top = l;
-        if (lane == 0) {
-            ids[k] = static_cast<int32_t>(0xFFFFFFFFu - wlo);
-            sel_l[k] = l;
-        }
-        if (lane == winner) {
-#pragma unroll
-            for (int j = 0; j + 1 < M; ++j) key[j] = key[j + 1];
-            key[M - 1] = 0;
-        }
-    }
-    float part = 0.f;
-#pragma unroll
-    for (int j = 0; j < M; ++j) part += expf(lg[j] - top);  // -inf padding adds 0
-    const float denom = wave_sum_all(part);
-    const float pk = lane < K ? expf(sel_l[lane] - top) / denom : 0.f;
-    const float total = wave_sum_all(pk);
-    if (lane < K) w[lane] = norm ? pk / total : pk;
+    for (int j = 0; j < M; ++j) v[j] = lrow[min(lane * M + j, E - 1)];  // every load issued first
+    Rounds<M> rd;
+    rounds_init(rd, v, E, lane);
+    rounds_run(rd, K, lane, ids);
+    const float wk = rounds_weight(rd, K, norm, lane);
+    if (lane < K) w[lane] = wk;
 }
 
 // The block's routing, in LDS.
 struct Routing {
     int32_t ids[kMaxPairs];    // [B][K] picks, pair p = b*K + k
     float w[kMaxPairs];        // combine weights
-    float sel_l[kThreads12 / kWave][SWQ_MAX_TOPK];
     int32_t lead[kMaxPairs];   // pair leads its expert's list
     int32_t slot[kMaxPairs];   // distinct slot of a leading pair
     int32_t uniq_e[kMaxPairs];
@@ -410,11 +372,11 @@ __device__ __forceinline__ void route(const MoEArgs &a, Routing &r, bool publish
         const float *lrow = a.logits + static_cast<int64_t>(b) * a.E;
         int32_t *ids = r.ids + b * a.K;
         float *w = r.w + b * a.K;
-        if (M <= 1) topk_token<1>(lrow, a.E, a.K, a.norm, lane, ids, w, r.sel_l[wave]);
-        else if (M <= 2) topk_token<2>(lrow, a.E, a.K, a.norm, lane, ids, w, r.sel_l[wave]);
-        else if (M <= 4) topk_token<4>(lrow, a.E, a.K, a.norm, lane, ids, w, r.sel_l[wave]);
-        else if (M <= 8) topk_token<8>(lrow, a.E, a.K, a.norm, lane, ids, w, r.sel_l[wave]);
-        else topk_token<16>(lrow, a.E, a.K, a.norm, lane, ids, w, r.sel_l[wave]);
+        if (M <= 1) topk_token<1>(lrow, a.E, a.K, a.norm, lane, ids, w);
+        else if (M <= 2) topk_token<2>(lrow, a.E, a.K, a.norm, lane, ids, w);
+        else if (M <= 4) topk_token<4>(lrow, a.E, a.K, a.norm, lane, ids, w);
+        else if (M <= 8) topk_token<8>(lrow, a.E, a.K, a.norm, lane, ids, w);
+        else topk_token<16>(lrow, a.E, a.K, a.norm, lane, ids, w);
     }
     __syncthreads();
     const int P = a.B * a.K;
@@ -496,12 +458,31 @@ __device__ __forceinline__ void keep(uint32_t v) { asm volatile("" ::"v"(v)); }
 
 template <int XDT>
 __global__ __launch_bounds__(kThreads12) void moe_stage1(MoEArgs a) {
+    __shared__ Routing r;
+    __shared__ int32_t s_last;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int task = blockIdx.x * (kThreads12 / kWave) + wave;
     if (static_cast<int>(blockIdx.x) < a.nr_blocks) {
         if (task < a.router_tasks)
             SWQ_DISPATCH(XDT, a.router, gemv_rows_tokens, a.router, task * tile_rows(a.router), a.E, a.x,
                          a.H, a.B, a.logits, a.E, lane);
+        // The last router workgroup to finish routes every token (softmax,
+        // top-k, the distinct experts) and publishes the tables stage 2 and 3
+        // read, while the shared-expert workgroups still run.  Release: this
+        // workgroup's logits reach memory before its arrival counts; acquire:
+        // the last one sees every workgroup's logits.
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __threadfence();
+            const int32_t old = __hip_atomic_fetch_add(a.arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = old == a.nr_blocks - 1 ? 1 : 0;
+        }
+        __syncthreads();
+        if (s_last) {
+            __threadfence();
+            route(a, r, true);
+            if (threadIdx.x == 0) __hip_atomic_store(a.arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         return;
     }
     // shared-expert workgroups; the shared down projection is pulled toward
@@ -524,15 +505,13 @@ __global__ __launch_bounds__(kThreads12) void moe_stage1(MoEArgs a) {
 // the slot: h[p][row] = silu(gate_row . x_b) * (up_row . x_b).  The next
 // unit's tiles and first activation slice load while the current unit's dot
 // products run.
-__device__ __forceinline__ int64_t unit_expert(const MoEArgs &a, const Routing &r, int s) {
-    return a.B == 1 ? r.ids[s] : r.uniq_e[s];
-}
-__device__ __forceinline__ int unit_pair(const MoEArgs &a, const Routing &r, int s, int pi) {
-    return a.B == 1 ? s : r.upairs[s * a.B + pi];
+__device__ __forceinline__ int64_t unit_expert(const MoEArgs &, const Slots &r, int s) { return r.e[s]; }
+__device__ __forceinline__ int unit_pair(const MoEArgs &a, const Slots &r, int s, int pi) {
+    return r.pairs[s * a.B + pi];
 }
 
 template <int XDT, int BITS, int CPL, int ES>
-__device__ __forceinline__ void gateup_issue(const MoEArgs &a, const Routing &r, const LaneMap &lm, int tps, int u,
+__device__ __forceinline__ void gateup_issue(const MoEArgs &a, const Slots &r, const LaneMap &lm, int tps, int u,
                                              RowTile<BITS, CPL, ES> &tg, RowTile<BITS, CPL, ES> &tu,
                                              XRaw<XDT, BITS, CPL> &xr) {
     const int s = u / tps, t = u - s * tps, rows = RowTile<BITS, CPL, ES>::kRI * lm.rpw;
@@ -560,7 +539,7 @@ __device__ __forceinline__ void gateup_pair(const MoEArgs &a, const LaneMap &lm,
 }
 
 template <int XDT, int BITS, int CPL, int ES, int XF>
-__device__ __forceinline__ void gateup_run(const MoEArgs &a, const Routing &r, const LaneMap &lm, int tps, int u,
+__device__ __forceinline__ void gateup_run(const MoEArgs &a, const Slots &r, const LaneMap &lm, int tps, int u,
                                            const RowTile<BITS, CPL, ES> &tg, const RowTile<BITS, CPL, ES> &tu,
                                            const XRaw<XDT, BITS, CPL> &xr) {
     constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
@@ -573,7 +552,7 @@ __device__ __forceinline__ void gateup_run(const MoEArgs &a, const Routing &r, c
         xslice_convert(xs, xr);
         gateup_pair(a, lm, row0, unit_pair(a, r, s, 0), tg, tu, xs);
     }
-    const int np = a.B == 1 ? 1 : r.uniq_np[s];
+    const int np = r.np[s];
     for (int pi = 1; pi < np; ++pi) {
         const int p = unit_pair(a, r, s, pi);
         XSlice<BITS, CPL, XF> xs;
@@ -583,14 +562,14 @@ __device__ __forceinline__ void gateup_run(const MoEArgs &a, const Routing &r, c
 }
 
 template <int XDT, int BITS, int CPL, int ES, int XF>
-__device__ __forceinline__ void gateup_units(const MoEArgs &a, const Routing &r, int u0, int W, int tps, int nu,
+__device__ __forceinline__ void gateup_units(const MoEArgs &a, const Slots &r, int u0, int W, int tps, int nu,
                                              int lane) {
     if (u0 >= nu) return;
     const LaneMap lm = lane_map(a.gate.lpr_log2, lane);
     RowTile<BITS, CPL, ES> tg0, tu0, tg1, tu1;
     XRaw<XDT, BITS, CPL> xr0, xr1;
     gateup_issue<XDT>(a, r, lm, tps, u0, tg0, tu0, xr0);
-    int k = 2;
+    [[maybe_unused]] int k = 2;
     for (int u = u0; u < nu; u += 2 * W) {
         if (u + W < nu) gateup_issue<XDT>(a, r, lm, tps, u + W, tg1, tu1, xr1);
         gateup_run<XDT, BITS, CPL, ES, XF>(a, r, lm, tps, u, tg0, tu0, xr0);
@@ -604,22 +583,22 @@ __device__ __forceinline__ void gateup_units(const MoEArgs &a, const Routing &r,
     }
 }
 
-// Every workgroup routes (softmax, top-k, distinct experts) from the logits
-// itself, then its waves take the (slot, row tile) units of the distinct
-// experts' gate/up rows grid-stride.
+// The routing stage 1 published into LDS, then the waves take the (slot,
+// row tile) units of the distinct experts' gate/up rows grid-stride.
 template <int XDT>
 __global__ __launch_bounds__(kThreads12) void moe_stage2(MoEArgs a) {
-    __shared__ Routing r;
+    __shared__ Slots sl;
     STAGE_TRACE_DECL;
     STAGE_STAMP(0);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    route(a, r, blockIdx.x == 0);
+    load_slots(a, sl);
+    __syncthreads();
     STAGE_STAMP(1);
     const int rows = tile_rows(a.gate);
     const int tps = (a.I + rows - 1) / rows;
-    const int nu = r.n_unique * tps;
+    const int nu = sl.n * tps;
     const int W = gridDim.x * (kThreads12 / kWave);
-    SWQ_DISPATCH(XDT, a.gate, gateup_units, a, r, blockIdx.x * (kThreads12 / kWave) + wave, W, tps, nu, lane);
+    SWQ_DISPATCH(XDT, a.gate, gateup_units, a, sl, blockIdx.x * (kThreads12 / kWave) + wave, W, tps, nu, lane);
     STAGE_STAMP(15);
     STAGE_TRACE_FLUSH(0);
 }
@@ -637,15 +616,7 @@ __global__ __launch_bounds__(kStage3MaxWaves * 64) void moe_stage3(MoEArgs a) {
     const int nw = blockDim.x >> 6;
     const int r0 = blockIdx.x * a.rows3;
     const int P = a.B * a.K;
-    // the routing stage 2 published, into LDS in one round trip: every
-    // slot's expert and pairs (entries past the distinct count unused)
-    for (int t = threadIdx.x; t < P; t += blockDim.x) {
-        sl.e[t] = a.B == 1 ? a.ids[t] : a.uniq_e[t];
-        sl.np[t] = a.B == 1 ? 1 : a.uniq_np[t];
-    }
-    for (int t = threadIdx.x; t < P * a.B; t += blockDim.x)
-        sl.pairs[t] = static_cast<int16_t>(a.B == 1 ? t : a.uniq_pairs[t]);
-    if (threadIdx.x == 0) sl.n = a.B == 1 ? a.K : *a.n_unique;
+    load_slots(a, sl);
     // combine weights and shared-gate logits: loaded into registers now,
     // staged in LDS only after the projections, so their latency overlaps.
     float w_pre[4];  // P <= 4 * blockDim (the host sizes the block 64*min(8, slots))
@@ -814,6 +785,7 @@ static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtyp
     a.uniq_np = reinterpret_cast<int32_t *>(wsb + wl.uniq_np);
     a.uniq_pairs = reinterpret_cast<int32_t *>(wsb + wl.uniq_pairs);
     a.h = reinterpret_cast<float *>(wsb + wl.h);
+    a.arrive = reinterpret_cast<int32_t *>(wsb + kWsArriveByte);
     a.xdt = x_dtype;
     a.odt = out_dtype;
     a.accumulate = accumulate ? 1 : 0;

@@ -377,106 +377,6 @@ __device__ __forceinline__ void down_dot(float (&res)[DRI], const RowTile<DB, 1,
     }
 }
 
-// ---------------------------------------------------------------------------
-// routing: the top-k rounds on one wave with the keys in registers
-//
-// Lane l holds experts l*M .. l*M+M-1, sorted by (logit desc, id asc) with a
-// stable odd-even transposition sort.  Each round takes the wave-wide
-// maximum head; the lowest lane holding it wins (lower lanes hold lower
-// ids) and pops its head.  Selection by logit with ties to the lower id
-// equals the reference's selection by probability (QwenCPUModel.swift:
-// 508-522) except where two distinct logits give the same fp32 probability.
-
-template <int M>
-struct Rounds {
-    uint32_t key[M];
-    int32_t jj[M];
-    float lg[M];        // the lane's logits in expert order (-inf past E)
-    uint32_t my_key;    // lane k: the key of pick k
-    uint32_t top_key;   // the largest key
-    int done;           // rounds finished
-};
-
-template <int CTRL, int RM>
-__device__ __forceinline__ uint32_t dpp_max_step(uint32_t v) {
-    return max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, RM, 0xF, false)));
-}
-
-// The maximum over the wave, read from lane 63.
-__device__ __forceinline__ uint32_t wave_max_bcast(uint32_t v) {
-    v = dpp_max_step<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-    v = dpp_max_step<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-    v = dpp_max_step<0x141, 0xF>(v);  // row_half_mirror
-    v = dpp_max_step<0x140, 0xF>(v);  // row_mirror
-    v = dpp_max_step<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
-    v = dpp_max_step<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
-    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
-}
-
-template <int M>
-__device__ __forceinline__ void rounds_init(Rounds<M> &r, const float (&v)[M], int E, int lane) {
-#pragma unroll
-    for (int j = 0; j < M; ++j) {
-        const bool valid = lane * M + j < E;
-        r.lg[j] = valid ? v[j] : -INFINITY;
-        r.key[j] = valid ? orderable(v[j]) : 0u;
-        r.jj[j] = j;
-    }
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-#pragma unroll
-        for (int j = i & 1; j + 1 < M; j += 2) {
-            const bool sw = r.key[j] < r.key[j + 1];
-            const uint32_t k0 = r.key[j], k1 = r.key[j + 1];
-            const int32_t i0 = r.jj[j], i1 = r.jj[j + 1];
-            r.key[j] = sw ? k1 : k0;
-            r.key[j + 1] = sw ? k0 : k1;
-            r.jj[j] = sw ? i1 : i0;
-            r.jj[j + 1] = sw ? i0 : i1;
-        }
-    }
-    r.my_key = 0;
-    r.top_key = 0;
-    r.done = 0;
-}
-
-// Rounds up to (not including) `upto`; pick k goes to s_ids[k] the moment
-// its round ends.
-template <int M>
-__device__ __forceinline__ void rounds_run(Rounds<M> &r, int upto, int lane, int32_t *s_ids) {
-    for (int k = r.done; k < upto; ++k) {
-        const uint32_t gmax = wave_max_bcast(r.key[0]);
-        const uint64_t cand = __ballot(r.key[0] == gmax);
-        const int wl = static_cast<int>(__builtin_ctzll(cand));
-        const int32_t e = wl * M + __builtin_amdgcn_readlane(r.jj[0], wl);
-        if (lane == 0) __hip_atomic_store(&s_ids[k], e, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (k == 0) r.top_key = gmax;
-        r.my_key = lane == k ? gmax : r.my_key;
-        const bool pop = lane == wl;
-#pragma unroll
-        for (int j = 0; j + 1 < M; ++j) {
-            r.key[j] = pop ? r.key[j + 1] : r.key[j];
-            r.jj[j] = pop ? r.jj[j + 1] : r.jj[j];
-        }
-        r.key[M - 1] = pop ? 0u : r.key[M - 1];
-    }
-    r.done = max(r.done, upto);
-}
-
-// Combine weights: p_k = exp(l_k - max) / sum_e exp(l_e - max) (:65-71),
-// w_k = p_k / sum_j p_j when norm (:546-550); the staged path's sums in the
-// same order.
-template <int M>
-__device__ __forceinline__ float rounds_weight(const Rounds<M> &r, int K, int norm, int lane) {
-    const float top = from_orderable(r.top_key);
-    float part = 0.f;
-#pragma unroll
-    for (int j = 0; j < M; ++j) part += expf(r.lg[j] - top);  // -inf padding adds 0
-    const float denom = wave_sum_all(part);
-    const float pk = lane < K ? expf(from_orderable(r.my_key) - top) / denom : 0.f;
-    const float total = wave_sum_all(pk);
-    return norm ? pk / total : pk;
-}
 
 // ---------------------------------------------------------------------------
 // the kernel.  XDT activation dtype; GB/GC/GX/GRI the gate/up format (bits,

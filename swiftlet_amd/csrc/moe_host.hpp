@@ -10,6 +10,7 @@ constexpr int kMaxExperts = 1024;
 // Byte offset, in the 256-byte workspace header, of the word the
 // single-launch path sets when one of its bounded waits runs out.
 constexpr size_t kWsErrByte = 64;
+constexpr size_t kWsArriveByte = 128;  // the staged path's stage-1 arrival counter (zero between calls)
 int zero_fill(void *p, size_t n, hipStream_t stream);
 
 struct WsLayout {
@@ -90,7 +91,8 @@ inline int check_layer(const swq_moe_layer *l, int B, int x_dtype) {
 }
 
 // Workspace of a decode call:
-//   [0, 256)          header (kWsErrByte: the stall record)
+//   [0, 256)          header (kWsErrByte: the stall record; kWsArriveByte:
+//                     the staged path's stage-1 arrival counter)
 //   [256, 4352)       the single launch's per-workgroup epoch counters
 //   [4352, ...)       its exchange words (logit replicas, activations,
 //                     partial outputs), sized for the layer, or for the
