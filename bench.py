@@ -45,9 +45,12 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 # the runs' commands and raw counts are kept with the kernel-trace summaries.  Keyed (workload, kernel).
 MEASURED_TRAFFIC = {
     ("qwen3.6-35b-a3b-q4-b1", "moe_fused"): 17_757_186,
-    ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_675_273,
-    ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 14_583_656,
-    ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 8_432_133,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_747_356,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 9_726_124,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 5_825_844,
+    ("qwen3.6-35b-a3b-q8-b4", "moe_stage1"): 4_461_998,
+    ("qwen3.6-35b-a3b-q8-b4", "moe_stage2"): 69_598_251,
+    ("qwen3.6-35b-a3b-q8-b4", "moe_stage3"): 36_610_935,
     ("qwen3.6-35b-a3b-q4-prefill512", "gate_up"): 402_625_363,
     ("qwen3.6-35b-a3b-q4-prefill512", "down"): 209_861_891,
 }

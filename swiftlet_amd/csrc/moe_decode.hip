@@ -619,12 +619,10 @@ __global__ __launch_bounds__(kStage3MaxWaves * 64) void moe_stage3(MoEArgs a) {
     load_slots(a, sl);
     // combine weights and shared-gate logits: loaded into registers now,
     // staged in LDS only after the projections, so their latency overlaps.
-    float w_pre[4];  // P <= 4 * blockDim (the host sizes the block 64*min(8, slots))
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const unsigned t = threadIdx.x + i * blockDim.x;
-        w_pre[i] = t < static_cast<unsigned>(P) ? a.wts[t] : 0.f;
-    }
+    // one weight per lane: the host sizes the block 64 * min(8, min(P, E) +
+    // shared) lanes, which is 512 >= P = B*K <= 256, or >= 64 * P, or
+    // >= 64 * E >= 16 * K >= P (and checks P <= blockDim)
+    const float w_pre = threadIdx.x < static_cast<unsigned>(P) ? a.wts[threadIdx.x] : 0.f;
     const float sg_pre = (a.has_shared && threadIdx.x < static_cast<unsigned>(a.B)) ? a.sg[threadIdx.x] : 0.f;
     // routed slots on every wave, the shared expert's on the wave with the
     // fewest routed ones (first, so its loads start with the others')
@@ -638,11 +636,7 @@ __global__ __launch_bounds__(kStage3MaxWaves * 64) void moe_stage3(MoEArgs a) {
     }
     SWQ_DISPATCH_DOWN(a.down, down_slots, a, sl, wave, nw, sl.n, r0, part, lane);
     STAGE_STAMP(14);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const unsigned t = threadIdx.x + i * blockDim.x;
-        if (t < static_cast<unsigned>(P)) s_w[t] = w_pre[i];
-    }
+    if (threadIdx.x < static_cast<unsigned>(P)) s_w[threadIdx.x] = w_pre;
     if (a.has_shared && threadIdx.x < static_cast<unsigned>(a.B)) s_gate[threadIdx.x] = sigmoidf_ref(sg_pre);
     __syncthreads();
     for (int t = threadIdx.x; t < a.B * a.rows3; t += blockDim.x) {
@@ -837,6 +831,7 @@ static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtyp
     }
     if (stage_mask & 4) {
         const int nw3 = min(kStage3MaxWaves, max_slots + a.has_shared);
+        if (P > nw3 * kWave) return SWQ_ERR_LIMIT;  // one combine weight per lane
         hipLaunchKernelGGL(moe_stage3, dim3((H + a.rows3 - 1) / a.rows3), dim3(nw3 * kWave), 0, s, a);
         if ((st = launch_status()) != SWQ_OK) return st;
     }
