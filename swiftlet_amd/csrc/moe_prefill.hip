@@ -341,6 +341,27 @@ __device__ __forceinline__ void bias_term_bs(f32x4_t (&acc)[MT][2], const BiasBS
     }
 }
 
+// The 2-byte scales of group g (g < NG <= 32) for this lane's columns of
+// both operands, from the words load_bias_bs preloaded: lane (n, kg) holds
+// groups 8 kg .. 8 kg + 7, so they come from lane (n, g / 8), both operands'
+// halves packed into one ds_bpermute.  g is wave-uniform; the word index is
+// picked by selects (no register indexing).
+template <int ST>
+__device__ __forceinline__ void scales_from_bs(const BiasBS<ST> &bi, int g, int n, float (&sc)[2]) {
+    static_assert(ST != SWQ_F32, "2-byte scales");
+    auto pick4 = [](uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int i) {
+        return (i & 2) ? ((i & 1) ? w3 : w2) : ((i & 1) ? w1 : w0);
+    };
+    const int i = (g & 7) >> 1;
+    const uint32_t w0 = pick4(bi.s[0][0], bi.s[0][1], bi.s[0][2], bi.s[0][3], i);
+    const uint32_t w1 = pick4(bi.s[1][0], bi.s[1][1], bi.s[1][2], bi.s[1][3], i);
+    // {operand 0, operand 1} halves of group g: bytes 0-1 or 2-3 of each word
+    const uint32_t both = __builtin_amdgcn_perm(w1, w0, (g & 1) ? 0x07060302u : 0x05040100u);
+    const uint32_t r = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(((g >> 3) * 16 + n) * 4, static_cast<int>(both)));
+    sc[0] = scale_of<ST>(r & 0xFFFFu);
+    sc[1] = scale_of<ST>(r >> 16);
+}
+
 // Position of column c in a row stored in nibble_order (within each 8).
 __device__ __forceinline__ int nibble_pos(int c) {
     const int i = c & 7;
@@ -687,8 +708,10 @@ __device__ __forceinline__ void ring_wait() {
 // The grouped quantised GEMM of pf_gemm (same tile, lanes and arithmetic) fed
 // by an LDS ring D groups deep: per group, each wave's DMA brings in its
 // share of the 64 activation rows (NPL bf16 planes, already in the order the
-// codes need), its 2 x 16 code rows and their scale pairs; a group is used
-// D - 1 groups after its loads were issued.  Activation rows are 128 B; row r
+// codes need) and its 2 x 16 code rows (f32 scales: and their scales); a
+// group is used D - 1 groups after its loads were issued.  2-byte scales come
+// from registers: the bias term's scale preload holds every group's, handed
+// between lanes per group.  Activation rows are 128 B; row r
 // keeps its 16 B chunk c in slot c ^ (r & 7) so the matrix-core reads of 16
 // rows at one chunk hit distinct banks.
 template <int BITS, int ST, int NPL, int EPI, int DA, int DB, int WAVES>
@@ -700,9 +723,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
     constexpr int AW = 8 / WAVES;                    // 8-row slabs each wave brings in per plane
     constexpr int A_SLOT = NPL * ROWS * 128;         // activation rows of one group
     constexpr int B_WAVE = BITS == 4 ? 1024 : 2048;  // code bytes per wave per group
-    constexpr int B_SLOT = WAVES * (B_WAVE + 256);   // codes + scale pairs of one group
-    // DMA instructions per wave per group: activations, codes, scales
-    constexpr int LA = AW * NPL, LB = B_WAVE / 1024, LSC = 1, L = LA + LB + LSC;
+    constexpr bool kScaleDma = ST == SWQ_F32;        // f32 scales ride the ring
+    constexpr int B_SLOT = WAVES * (B_WAVE + (kScaleDma ? 256 : 0));  // codes (+ scales) of one group
+    // DMA instructions per wave per group: activations, codes (+ scales)
+    constexpr int LA = AW * NPL, LB = B_WAVE / 1024 + (kScaleDma ? 1 : 0), L = LA + LB;
     __shared__ __attribute__((aligned(16))) uint8_t s_ring_a[DA * A_SLOT];
     __shared__ __attribute__((aligned(16))) uint8_t s_ring_b[DB * B_SLOT];
     __shared__ __attribute__((aligned(16))) uint8_t s_xs[ROWS * 128];  // group sums of the rows
@@ -781,13 +805,18 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
             bsrc[j] = wbase[j] + static_cast<int64_t>(r) * row_bytes + 16 * (lane & 3);
         }
     }
-    const uint8_t *ssrc;
-    {
+    const uint8_t *ssrc = nullptr;
+    if constexpr (kScaleDma) {
         const int j = lane >> 5, r = min(wcol + j * a.col_op + (lane & 15), N - 1);
-        ssrc = (j ? sbase[1] : sbase[0]) + static_cast<int64_t>(r) * gpr * (ST == SWQ_F32 ? 4 : 2);
+        ssrc = (j ? sbase[1] : sbase[0]) + static_cast<int64_t>(r) * gpr * 4;
     }
     const uint32_t ring_a = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_ring_a));
     const uint32_t ring_b = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_ring_b));
+
+    // the bias term's biases and scales (the K loop takes its scales from
+    // them), issued before every ring load
+    BiasBS<ST> bi;
+    load_bias_bs<ST>(bi, sbase, bbase, srow, NG, kg);
 
     // group g's activation rows into A slot sa (LA instructions per wave)
     auto issue_a = [&](int sa, int g) {
@@ -802,7 +831,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
                 if (afetch[i]) dma16(asrc[p][i] + kGroupK * 2 * g, d);
             }
     };
-    // group g's code rows and scale pairs into B slot sb (LB + LSC instructions per wave)
+    // group g's code rows (and f32 scales) into B slot sb (LB instructions per wave)
     auto issue_b = [&](int sb, int g) {
         const uint32_t base = ring_b + sb * B_SLOT;
         if constexpr (BITS == 4) {
@@ -811,9 +840,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
             dma16(bsrc[0] + 64 * g, base + wave * B_WAVE);
             dma16(bsrc[1] + 64 * g, base + wave * B_WAVE + 1024);
         }
-        // 2-byte scales: the aligned pair holding group g (rows hold an even
-        // number of groups); f32: the scale itself
-        dma4(ssrc + (ST == SWQ_F32 ? 4 * g : 4 * (g >> 1)), base + WAVES * B_WAVE + wave * 256);
+        if constexpr (kScaleDma) dma4(ssrc + 4 * g, base + WAVES * B_WAVE + wave * 256);
     };
 
     f32x4_t acc[MT][2];
@@ -838,10 +865,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
                 bq[j][0] = codes_q8(w.x, w.y);
                 bq[j][1] = codes_q8(w.z, w.w);
             }
-            const uint32_t raw = *reinterpret_cast<const uint32_t *>(bl + WAVES * B_WAVE + wave * 256 + (j * 32 + n) * 4);
-            if constexpr (ST == SWQ_F32) sc[j] = __uint_as_float(raw);
-            else sc[j] = scale_of<ST>((g & 1) ? raw >> 16 : raw & 0xFFFFu);
+            if constexpr (kScaleDma)
+                sc[j] = __uint_as_float(*reinterpret_cast<const uint32_t *>(bl + WAVES * B_WAVE + wave * 256 + (j * 32 + n) * 4));
         }
+        if constexpr (!kScaleDma) scales_from_bs<ST>(bi, g, n, sc);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             if (16 * mt >= rows) break;
@@ -873,8 +900,6 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
     // sums by DMA into LDS), issued before the ring so that they are older
     // than every ring load (ring_wait's counts stay exact) and arrive during
     // the loop
-    BiasBS<ST> bi;
-    load_bias_bs<ST>(bi, sbase, bbase, srow, NG, kg);
     {
         const uint32_t xb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_xs));
 #pragma unroll
@@ -884,7 +909,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
         }
     }
 
-    // ---- the rings: codes and scales DB-1 groups ahead, activation rows
+    // ---- the rings: codes DB-1 groups ahead, activation rows
     // (mostly L2 hits) DA-1 groups ahead.  Before the loop: B groups 0..DB-2,
     // then A groups 0..DA-2.  At group g: wait until A(g) has landed (B(g)
     // is older), then refill the slots group g-1 used with A(g+DA-1) and
@@ -910,7 +935,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
         int sa = (DA - 1) % DA, sb = (DA - 1) % DB;
 #pragma unroll 1
         for (int g = DA - 1; g < NG; ++g) {
-            ring_wait<LB + LSC + (DA - 2) * L>();
+            ring_wait<LB + (DA - 2) * L>();
             step(g, sa, sb);
             sa = sa + 1 == DA ? 0 : sa + 1;
             sb = sb + 1 == DB ? 0 : sb + 1;
