@@ -46,7 +46,7 @@ constexpr int kPfThreads = 256;  // 4 waves
 constexpr int kGroupK = 64;      // the quantisation group: one MFMA pair of k = 32
 constexpr int kLdsPitch = 72;    // bf16 per staged row: 64 + 8 (144 B rows, conflict-free b128 reads)
 constexpr int kMaxGroups = 64;   // inputs per row <= 4096
-constexpr int kXsPitch = kMaxGroups + 4;
+constexpr int kXsPitch = kMaxGroups + 36;  // a K slice's bias term reads up to 31 groups past its first
 constexpr int kTileRows = 64;    // rows of a routed / shared tile
 constexpr int kRouterRows = 16;  // rows of a router tile
 constexpr int kRouteWaves = 4;   // tokens per route workgroup
@@ -97,6 +97,10 @@ struct GemmArgs {
     int32_t xs_ld, xs_ld_out;
     int32_t o_perm;           // SwiGLU output in nibble_order within each 8 columns (4-bit down)
     int32_t max_tiles;        // entries of the tile table
+    // pf_gemm: K split over blockIdx.y into kslices slices of kgroups groups
+    // (the last may be shorter); rows outputs of slice s at o0 + s * o_slice
+    int32_t kslices, kgroups;
+    int64_t o_slice;
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -209,7 +213,7 @@ struct BSlot {
 };
 
 // Eight consecutive group sums of one activation row, zeros past NG (the
-// row holds at least g + 8 entries: rows are padded to whole 32-group blocks).
+// row holds at least g + 8 entries; g is a multiple of 4).
 __device__ __forceinline__ void load_sums8(const float *row, int g, int NG, float (&v)[8]) {
     const float4 x0 = *reinterpret_cast<const float4 *>(row + g);
     const float4 x1 = *reinterpret_cast<const float4 *>(row + g + 4);
@@ -218,55 +222,48 @@ __device__ __forceinline__ void load_sums8(const float *row, int g, int NG, floa
     for (int i = 0; i < 8; ++i) v[i] = g + i < NG ? t[i] : 0.f;
 }
 
-// The bias term sum_g b'[n,g] X_g[m] on the group axis, added to acc.  b' is
-// exact as bf16 hi + lo (an fp16 bias less 16 fp16 scales); X_g as hi + mid +
-// lo; the five products above 2^-24 relative are accumulated.  xrow[mt]: the
-// group sums of this lane's A row (16 mt + n), rows padded to 32-group blocks.
+// Raw biases (and 4-bit: scales) of one 32-group block of the bias term:
+// this lane's groups g0 + 8 kg .. +7 of both operands.
+template <int ST>
+struct BiasRaw {
+    uint32_t b[2][8], s[2][8];
+};
+
+// The bias term sum_g b'[n,g] X_g[m] over the block's groups below ge, on the
+// group axis, added to acc.  b' is exact as bf16 hi + lo (an fp16 bias less
+// 16 fp16 scales); X_g as hi + mid + lo; the five products above 2^-24
+// relative are accumulated.  xrow[mt]: the group sums of this lane's A row
+// (16 mt + n); entries up to g0 + 31 are readable.
 template <int BITS, int ST, int MT>
-__device__ __forceinline__ void bias_term(f32x4_t (&acc)[MT][2], const float *const (&xrow)[MT],
-                                          const uint8_t *const (&sbase)[2], const uint8_t *const (&bbase)[2],
-                                          const int64_t (&srow)[2], int NG, int rows, int kg) {
-#pragma unroll 1
-    for (int g0 = 0; g0 < NG; g0 += 32) {
-        // every load first (clamped indices), then the selects: a load under
-        // a branch would be waited for on its own
-        uint32_t braw[2][8], sraw[2][8];
+__device__ __forceinline__ void bias_apply(f32x4_t (&acc)[MT][2], const BiasRaw<ST> &r,
+                                           const float *const (&xrow)[MT], int g0, int ge, int rows, int kg) {
+    float xv[MT][8];
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+    for (int mt = 0; mt < MT; ++mt) load_sums8(xrow[mt], g0 + 8 * kg, ge, xv[mt]);
+    u32x4_t bh[2], bl[2];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int gi = min(g0 + 8 * kg + i, NG - 1);
-                braw[j][i] = scale_raw<ST>(bbase[j], srow[j] + gi);
-                if constexpr (BITS == 4) sraw[j][i] = scale_raw<ST>(sbase[j], srow[j] + gi);
-            }
-        float xv[MT][8];
+    for (int j = 0; j < 2; ++j) {
+        float v[8];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) load_sums8(xrow[mt], g0 + 8 * kg, NG, xv[mt]);
-        u32x4_t bh[2], bl[2];
+        for (int i = 0; i < 8; ++i) {
+            float bp = scale_of<ST>(r.b[j][i]);
+            if constexpr (BITS == 4) bp = fmaf(-16.f, scale_of<ST>(r.s[j][i]), bp);
+            v[i] = g0 + 8 * kg + i < ge ? bp : 0.f;
+        }
+        split8(v, bh[j], bl[j]);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        if (16 * mt >= rows) break;
+        u32x4_t xh, xm, xl;
+        split8x3(xv[mt], xh, xm, xl);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float bp = scale_of<ST>(braw[j][i]);
-                if constexpr (BITS == 4) bp = fmaf(-16.f, scale_of<ST>(sraw[j][i]), bp);
-                v[i] = g0 + 8 * kg + i < NG ? bp : 0.f;
-            }
-            split8(v, bh[j], bl[j]);
-        }
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            if (16 * mt >= rows) break;
-            u32x4_t xh, xm, xl;
-            split8x3(xv[mt], xh, xm, xl);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                acc[mt][j] = mfma(xl, bh[j], acc[mt][j]);
-                acc[mt][j] = mfma(xm, bl[j], acc[mt][j]);
-                acc[mt][j] = mfma(xm, bh[j], acc[mt][j]);
-                acc[mt][j] = mfma(xh, bl[j], acc[mt][j]);
-                acc[mt][j] = mfma(xh, bh[j], acc[mt][j]);
-            }
+            acc[mt][j] = mfma(xl, bh[j], acc[mt][j]);
+            acc[mt][j] = mfma(xm, bl[j], acc[mt][j]);
+            acc[mt][j] = mfma(xm, bh[j], acc[mt][j]);
+            acc[mt][j] = mfma(xh, bl[j], acc[mt][j]);
+            acc[mt][j] = mfma(xh, bh[j], acc[mt][j]);
         }
     }
 }
@@ -374,7 +371,7 @@ __device__ __forceinline__ int nibble_pos(int c) {
 // projection's input).  Every thread of the workgroup calls it.
 template <int EPI, int MT, int WAVES = 4>
 __device__ __forceinline__ void epilogue(const f32x4_t (&acc)[MT][2], const GemmArgs &a, const int (&col)[2], int N,
-                                         bool active, int row0, int rows, int nb, float *s_red) {
+                                         bool active, int row0, int rows, int nb, float *s_red, int64_t obase = 0) {
     constexpr int ROWS = 16 * MT;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 15, kg = lane >> 4;
     if constexpr (EPI == kEpiSwiGLU) {
@@ -416,7 +413,7 @@ __device__ __forceinline__ void epilogue(const f32x4_t (&acc)[MT][2], const Gemm
             for (int r = 0; r < 4; ++r) {
                 const int row = 16 * mt + 4 * kg + r;
                 if (row >= rows) continue;
-                const int64_t o = static_cast<int64_t>(row0 + row) * a.o_ld;
+                const int64_t o = obase + static_cast<int64_t>(row0 + row) * a.o_ld;
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     if (col[j] < N) static_cast<float *>(a.o0)[o + col[j]] = acc[mt][j][r];
@@ -424,6 +421,8 @@ __device__ __forceinline__ void epilogue(const f32x4_t (&acc)[MT][2], const Gemm
         }
     }
 }
+
+constexpr int kBlockG = 4;  // pf_gemm: K groups staged per round trip
 
 // The grouped quantised GEMM: one workgroup computes a tile of up to 16*MT
 // activation rows against 4 waves x 2 operands x 16 matrix rows (output
@@ -436,9 +435,13 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
     constexpr int NPL = SRC == kSrcBF16 ? 1 : 2;
     constexpr int PIECES = ROWS * 8;
     constexpr int PPT = (PIECES + kPfThreads - 1) / kPfThreads;
-    __shared__ __attribute__((aligned(16))) uint16_t s_a[2][NPL][ROWS * kLdsPitch];
+    __shared__ __attribute__((aligned(16))) uint16_t s_a[kBlockG][NPL][ROWS * kLdsPitch];
     __shared__ __attribute__((aligned(16))) float s_xs[SUM == kSumStage ? ROWS * kXsPitch : 1];
     __shared__ float s_red[EPI == kEpiSwiGLU ? 4 * ROWS : 1];
+    // raw scales and biases of the slice's groups for the workgroup's
+    // columns: [operand][scales, biases][wave * 16 + n][group - gb], one
+    // u32 per element (f32) or a u16 pair per word
+    __shared__ uint32_t s_tab[2 * 2 * 64 * kBlockG];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -469,6 +472,10 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
     const int K = shared ? a.Ksh : a.K;
     const int N = shared ? a.Nsh : a.N;
     const int NG = K / kGroupK;
+    // this workgroup's K slice (blockIdx.y of kslices): groups [gb, ge), an
+    // even count of at most kBlockG
+    const int gb = static_cast<int>(blockIdx.y) * a.kgroups, ge = min(gb + a.kgroups, NG);
+    if (gb >= ge) return;
     const int wcol = nb * a.col_block + wave * a.col_wave;
     const bool active = wcol < N;
 
@@ -505,8 +512,35 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
                 sl.w[j][2] = v.z;
                 sl.w[j][3] = v.w;
             }
-            sl.s[j] = scale_raw<ST>(sbase[j], srow[j] + g);
         }
+    };
+
+    // ---- the slice's scales and biases into s_tab, every load at once
+    // (rows of 4-byte aligned words: an even group count per row)
+    {
+        constexpr int ES = ST == SWQ_F32 ? 4 : 2;
+        constexpr int WPE = kBlockG * ES / 4;  // words per (operand, array, column)
+        constexpr int WORDS = 2 * 2 * 64 * WPE;
+        constexpr int PER = WORDS / kPfThreads;
+        const int valid = (ge - gb) * ES / 4;  // words holding the slice's groups
+        uint32_t v[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int w = tid + u * kPfThreads;
+            const int q = w % WPE, lc = (w / WPE) % 64, arr = (w / (WPE * 64)) % 2, j = w / (WPE * 128);
+            const int c = min(nb * a.col_block + (lc >> 4) * a.col_wave + j * a.col_op + (lc & 15), N - 1);
+            const uint8_t *base = arr ? (j ? bbase[1] : bbase[0]) : (j ? sbase[1] : sbase[0]);
+            const int64_t byte = (static_cast<int64_t>(c) * (K / kGroupK) + gb) * ES + 4 * min(q, valid - 1);
+            v[u] = *reinterpret_cast<const uint32_t *>(base + byte);
+        }
+#pragma unroll
+        for (int u = 0; u < PER; ++u) s_tab[tid + u * kPfThreads] = v[u];
+    }
+    // raw scale (arr 0) or bias (arr 1) of operand j, this lane's column, group g
+    auto tab = [&](int j, int arr, int g) -> uint32_t {
+        const int e = ((j * 2 + arr) * 64 + wave * 16 + n) * kBlockG + (g - gb);
+        if constexpr (ST == SWQ_F32) return s_tab[e];
+        else return reinterpret_cast<const uint16_t *>(s_tab)[e];
     };
 
     // ---- A staging (rows past the tile stage row 0)
@@ -568,7 +602,7 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
                 const float sum = segment_reduce((t[0] + t[1]) + (t[2] + t[3]), 3);  // 8 lanes of (row, group)
                 // the last column is a sink for the redundant groups the
                 // loop's tail stages (the bias term reads columns < 64)
-                if (c8 == 0) s_xs[r * kXsPitch + (g < NG ? g : kXsPitch - 1)] = sum;
+                if (c8 == 0) s_xs[r * kXsPitch + (g < ge ? g : kXsPitch - 1)] = sum;
             }
             if constexpr (BITS == 4) {
                 hi = nibble_order(hi);
@@ -585,7 +619,7 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](const BSlot<BITS> &sl, int buf) {
+    auto compute = [&](const BSlot<BITS> &sl, int buf, int g) {
         u32x4_t bq[2][2];
         float sc[2];
 #pragma unroll
@@ -597,7 +631,7 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
                 bq[j][0] = codes_q8(sl.w[j][0], sl.w[j][1]);
                 bq[j][1] = codes_q8(sl.w[j][2], sl.w[j][3]);
             }
-            sc[j] = scale_of<ST>(sl.s[j]);
+            sc[j] = scale_of<ST>(tab(j, 0, g));
         }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
@@ -625,39 +659,37 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
         }
     };
 
-    // ---- the K loop: A two groups ahead (registers, then LDS), B two groups
-    // ahead (registers); NG is even.  Straight-line: every load is issued
-    // unconditionally (the tail re-loads group NG-1 and stages it into the
-    // buffer no later iteration reads), and waves whose columns lie past N
-    // compute on clamped rows and store nothing.
-    AStage<SRC, PPT> sx, sy;
-    BSlot<BITS> b0, b1;
-    load_a(sx, 0);
-    load_b(b0, 0);
-    load_a(sy, 1);
-    load_b(b1, 1);
-    store_a(sx, 0, 0);
-    __syncthreads();
+    // ---- the K loop over the slice, kBlockG groups at a time: every load
+    // of a block is issued at once (A into registers, then LDS; B into
+    // registers), so a slice of up to kBlockG groups costs one round trip.
+    // Loads past the slice repeat group ge-1 (staged into the sink column,
+    // never computed).  Waves whose columns lie past N compute on clamped
+    // rows and store nothing.
 #pragma unroll 1
-    for (int g = 0; g < NG; g += 2) {
-        const int g2 = min(g + 2, NG - 1), g3 = min(g + 3, NG - 1);
-        load_a(sx, g2);
-        compute(b0, 0);
-        load_b(b0, g2);
-        store_a(sy, 1, g + 1);
+    for (int g0 = gb; g0 < ge; g0 += kBlockG) {
+        AStage<SRC, PPT> st[kBlockG];
+        BSlot<BITS> bs[kBlockG];
+#pragma unroll
+        for (int u = 0; u < kBlockG; ++u) {
+            const int g = min(g0 + u, ge - 1);
+            load_a(st[u], g);
+            load_b(bs[u], g);
+        }
+#pragma unroll
+        for (int u = 0; u < kBlockG; ++u) store_a(st[u], u, g0 + u);
         __syncthreads();
-        load_a(sy, g3);
-        compute(b1, 1);
-        load_b(b1, g3);
-        store_a(sx, 0, g + 2);
-        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kBlockG; ++u)
+            if (g0 + u < ge) compute(bs[u], u, g0 + u);
+        __syncthreads();  // the buffers are restaged by the next block
     }
 
     // the router hands the group sums of x to gate/up (one column block does)
     if constexpr (SUM == kSumStage) {
         if (a.xs_out && nb == 0) {
-            for (int i = tid; i < rows * NG; i += kPfThreads) {
-                const int r = i / NG, g = i - r * NG;
+            const int gs = ge - gb;
+            for (int i = tid; i < rows * gs; i += kPfThreads) {
+                const int r = i / gs, g = gb + (i - r * gs);
                 a.xs_out[static_cast<int64_t>(row0 + r) * a.xs_ld_out + g] = s_xs[r * kXsPitch + g];
             }
         }
@@ -675,9 +707,21 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
                 xrow[mt] = &s_xs[(16 * mt + n) * kXsPitch];
             }
         }
-        bias_term<BITS, ST, MT>(acc, xrow, sbase, bbase, srow, NG, rows, kg);
+        // the slice's biases (and 4-bit scales) from s_tab: lane kg holds
+        // groups gb + 8 kg .. (only kg = 0 has any: a slice has at most
+        // kBlockG groups)
+        BiasRaw<ST> braw;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int g = min(gb + 8 * kg + i, ge - 1);
+                braw.b[j][i] = tab(j, 1, g);
+                braw.s[j][i] = tab(j, 0, g);
+            }
+        bias_apply<BITS, ST, MT>(acc, braw, xrow, gb, ge, rows, kg);
     }
-    epilogue<EPI, MT>(acc, a, col, N, active, row0, rows, nb, s_red);
+    epilogue<EPI, MT>(acc, a, col, N, active, row0, rows, nb, s_red, static_cast<int64_t>(blockIdx.y) * a.o_slice);
 }
 
 // ---------------------------------------------------------------------------
@@ -1004,10 +1048,12 @@ __global__ __launch_bounds__(kPfThreads) void pf_prep(const PrepArgs a) {
 // ---------------------------------------------------------------------------
 // routing and grouping
 
+constexpr int kMaxLogitSlices = 16;  // router K slices (partial logit rows per token): H <= 4096
+
 struct RouteArgs {
     QMat seg;                 // shared_expert_gate [1, H]
     const void *x;
-    const float *logits;      // [T, E]
+    const float *logits;      // [lslices][T, E] partial logits, summed in slice order
     const float *bias;        // [E] added to the logits, or null
     int32_t *ids;             // [T, K]
     float *wts;               // [T, K]
@@ -1020,51 +1066,82 @@ struct RouteArgs {
     Tile *tiles;
     int32_t *n_tiles;
     int32_t T, E, K, H, norm, has_shared;
+    int32_t lslices;
+    int64_t lslice;           // elements between slices
 };
 
 // <w_sg, x_t> over one row of any vector-path format (QwenCPUModel.swift:559).
-template <int XDT>
+// Lane l sums chunks l, l + 64, ... in that order; two chunks' loads go out
+// before either is used.
+template <int XDT, int BITS>
 __device__ float row_dot(const QMat &m, const void *x, int64_t x0, int lane) {
+    constexpr int CPC = 128 / BITS;  // codes per 16-byte chunk
     float acc = 0.f;
-    const int cpc = 128 / m.bits;
-    for (int c = lane; c < m.chunks; c += kWave) {
-        const uint4 w = *reinterpret_cast<const uint4 *>(m.w + 16 * static_cast<int64_t>(c));
-        const int g = (c * cpc) / m.group;
-        const float s = load_scale(m.s, g, m.stype), b = load_scale(m.b, g, m.stype);
-        float d, xs = 0.f;
-        if (m.bits == 4) {
-            float xv[32];
-            load_x<XDT, 32>(xv, x, x0 + static_cast<int64_t>(c) * 32);
+    for (int c0 = lane; c0 < m.chunks; c0 += 2 * kWave) {
+        const bool has1 = c0 + kWave < m.chunks;
+        const int c1 = has1 ? c0 + kWave : c0;
+        const uint4 w0 = *reinterpret_cast<const uint4 *>(m.w + 16 * static_cast<int64_t>(c0));
+        const uint4 w1 = *reinterpret_cast<const uint4 *>(m.w + 16 * static_cast<int64_t>(c1));
+        const int g0 = (c0 * CPC) / m.group, g1 = (c1 * CPC) / m.group;
+        const float s0 = load_scale(m.s, g0, m.stype), b0 = load_scale(m.b, g0, m.stype);
+        const float s1 = load_scale(m.s, g1, m.stype), b1 = load_scale(m.b, g1, m.stype);
+        float xv0[CPC], xv1[CPC];
+        load_x<XDT, CPC>(xv0, x, x0 + static_cast<int64_t>(c0) * CPC);
+        load_x<XDT, CPC>(xv1, x, x0 + static_cast<int64_t>(c1) * CPC);
+        float xs0 = 0.f, xs1 = 0.f;
 #pragma unroll
-            for (int i = 0; i < 32; ++i) xs += xv[i];
-            d = dot_chunk_q4(w, xv);
-        } else {
-            float xv[16];
-            load_x<XDT, 16>(xv, x, x0 + static_cast<int64_t>(c) * 16);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) xs += xv[i];
-            d = dot_chunk_q8(w, xv);
+        for (int i = 0; i < CPC; ++i) {
+            xs0 += xv0[i];
+            xs1 += xv1[i];
         }
-        acc += s * d + b * xs;
+        float d0, d1;
+        if constexpr (BITS == 4) {
+            d0 = dot_chunk_q4(w0, xv0);
+            d1 = dot_chunk_q4(w1, xv1);
+        } else {
+            d0 = dot_chunk_q8(w0, xv0);
+            d1 = dot_chunk_q8(w1, xv1);
+        }
+        acc += s0 * d0 + b0 * xs0;
+        if (has1) acc += s1 * d1 + b1 * xs1;
     }
     return wave_sum(acc);
+}
+
+// Inclusive prefix sum over the lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int u = __shfl_up(v, d, kWave);
+        if (lane >= d) v += u;
+    }
+    return v;
 }
 
 // The last workgroup: per-expert pair counts (LDS atomics over the ids),
 // exclusive scans of the pair counts and of the tile counts, the tile table
 // (by decreasing row count), and the sorted pair order (a second pass hands
 // out the slots; the order of pairs within an expert does not matter, every
-// row is computed on its own).
+// row is computed on its own).  The first kHeldIds * 256 ids are loaded at
+// once and kept in registers for the second pass.
 __device__ void group_pairs(const RouteArgs &a) {
     __shared__ int32_t s_cnt[kMaxExperts];  // counts, then the next free slot
-    __shared__ int32_t s_part[2][kPfThreads];
+    __shared__ int32_t s_wsum[2][kPfThreads / kWave];
     __shared__ int32_t s_rows[kTileRows + 1];  // tiles of each row count, then their next slot
-    const int tid = threadIdx.x;
+    constexpr int kHeldIds = 16;
+    constexpr int kBatch = 8;  // ids per thread per pass past the held ones, all in flight at once
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int P = a.T * a.K;
-    constexpr int kBatch = 8;  // ids per thread per pass, all in flight at once
+    int held[kHeldIds];
+#pragma unroll
+    for (int u = 0; u < kHeldIds; ++u) held[u] = a.ids[min(tid + u * kPfThreads, P - 1)];
     for (int e = tid; e < a.E; e += kPfThreads) s_cnt[e] = 0;
+    for (int r = tid; r <= kTileRows; r += kPfThreads) s_rows[r] = 0;
     __syncthreads();
-    for (int p0 = tid; p0 < P; p0 += kBatch * kPfThreads) {
+#pragma unroll
+    for (int u = 0; u < kHeldIds; ++u)
+        if (tid + u * kPfThreads < P) atomicAdd(&s_cnt[held[u]], 1);
+    for (int p0 = tid + kHeldIds * kPfThreads; p0 < P; p0 += kBatch * kPfThreads) {
         int e[kBatch];
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) e[u] = a.ids[min(p0 + u * kPfThreads, P - 1)];
@@ -1084,26 +1161,17 @@ __device__ void group_pairs(const RouteArgs &a) {
         csum += cnt[i];
         tsum += tl[i];
     }
-    s_part[0][tid] = csum;
-    s_part[1][tid] = tsum;
-    __syncthreads();
-    // inclusive scan over the 256 partials (Hillis-Steele in LDS)
-    for (int d = 1; d < kPfThreads; d <<= 1) {
-        const int c = tid >= d ? s_part[0][tid - d] : 0;
-        const int t = tid >= d ? s_part[1][tid - d] : 0;
-        __syncthreads();
-        s_part[0][tid] += c;
-        s_part[1][tid] += t;
-        __syncthreads();
+    // exclusive scans over the threads' pair and tile counts: wave scans,
+    // then the wave totals
+    const int cinc = wave_incl_scan(csum, lane), tinc = wave_incl_scan(tsum, lane);
+    if (lane == kWave - 1) {
+        s_wsum[0][wave] = cinc;
+        s_wsum[1][wave] = tinc;
     }
-    int c0 = s_part[0][tid] - csum;
-    const int routed_tiles = s_part[1][kPfThreads - 1];
-    const int sh_tiles = a.has_shared ? (a.T + kTileRows - 1) / kTileRows : 0;
     // The tile table in decreasing row count (the GEMMs start the heaviest
     // tiles first, so the light ones fill in at the end): tiles per row
     // count, their first slots, then each tile into the next slot of its count.
-    for (int r = tid; r <= kTileRows; r += kPfThreads) s_rows[r] = 0;
-    __syncthreads();
+    const int sh_tiles = a.has_shared ? (a.T + kTileRows - 1) / kTileRows : 0;
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
         if (tid * EPT + i < a.E && cnt[i] > 0) {
@@ -1116,13 +1184,18 @@ __device__ void group_pairs(const RouteArgs &a) {
         if (a.T % kTileRows) atomicAdd(&s_rows[a.T % kTileRows], 1);
     }
     __syncthreads();
-    if (tid == 0) {
-        int next = 0;
-        for (int r = kTileRows; r >= 1; --r) {
-            const int n = s_rows[r];
-            s_rows[r] = next;
-            next += n;
-        }
+    int c0 = cinc - csum, routed_tiles = 0;
+#pragma unroll
+    for (int w = 0; w < kPfThreads / kWave; ++w) {
+        if (w < wave) c0 += s_wsum[0][w];
+        routed_tiles += s_wsum[1][w];
+    }
+    static_assert(kTileRows == kWave, "one lane per tile row count");
+    if (wave == 0) {
+        // first slot of each row count, counts 64 .. 1 in that order (lane l: 64 - l)
+        const int r = kTileRows - lane;
+        const int n = s_rows[r];
+        s_rows[r] = wave_incl_scan(n, lane) - n;
     }
     __syncthreads();
 #pragma unroll
@@ -1146,7 +1219,16 @@ __device__ void group_pairs(const RouteArgs &a) {
         *a.done = 0u;
     }
     __syncthreads();
-    for (int p0 = tid; p0 < P; p0 += kBatch * kPfThreads) {
+#pragma unroll
+    for (int u = 0; u < kHeldIds; ++u) {
+        const int p = tid + u * kPfThreads;
+        if (p < P) {
+            const int q = atomicAdd(&s_cnt[held[u]], 1);
+            a.pos[p] = q;
+            a.tok[q] = p / a.K;
+        }
+    }
+    for (int p0 = tid + kHeldIds * kPfThreads; p0 < P; p0 += kBatch * kPfThreads) {
         int e[kBatch];
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) e[u] = a.ids[min(p0 + u * kPfThreads, P - 1)];
@@ -1163,31 +1245,99 @@ __device__ void group_pairs(const RouteArgs &a) {
         for (int t = tid; t < a.T; t += kPfThreads) a.tok[P + t] = t;
 }
 
+// One token's routing on one wave: the logits of the lane's experts
+// l*M .. l*M+M-1, summed over the router's K slices in slice order (every
+// slice's load in flight at once) plus the bias; top-k by the rounds of
+// route.hpp; the shared-expert gate logit, whose loads go out with the
+// logits'.
+// The lane's M consecutive entries l*M .. of a row of E floats (vector loads
+// when E is a multiple of M, so that the row and lane offsets are aligned;
+// entries past E repeat the last).
+template <int M>
+__device__ __forceinline__ void load_lane_m(const float *row, int E, int lane, bool vec, float (&v)[M]) {
+    if (vec && M >= 4) {
+#pragma unroll
+        for (int q = 0; q < M / 4; ++q) {
+            const float4 f = *reinterpret_cast<const float4 *>(row + lane * M + 4 * q);
+            v[4 * q] = f.x;
+            v[4 * q + 1] = f.y;
+            v[4 * q + 2] = f.z;
+            v[4 * q + 3] = f.w;
+        }
+    } else if (vec && M == 2) {
+        const float2 f = *reinterpret_cast<const float2 *>(row + lane * M);
+        v[0] = f.x;
+        v[1 % M] = f.y;
+    } else {
+#pragma unroll
+        for (int j = 0; j < M; ++j) v[j] = row[min(lane * M + j, E - 1)];
+    }
+}
+
+// One token's routing on one wave: the logits of the lane's experts
+// l*M .. l*M+M-1, summed over the router's K slices in slice order (eight
+// slices' loads in flight at once) plus the bias; top-k by the rounds of
+// route.hpp; the shared-expert gate logit, whose loads go out with the
+// logits'.
+template <int XDT, int M>
+__device__ __forceinline__ void route_token(const RouteArgs &a, int t, int lane, int32_t *s_pick) {
+    constexpr int kBatch = 8;
+    const float *lg = a.logits + static_cast<int64_t>(t) * a.E;
+    // lanes past E (M * 64 > E) read in bounds when E is a multiple of M
+    const bool vec = a.E % M == 0 && lane * M < a.E;
+    float v[M];
+    float sg = 0.f;
+    for (int k0 = 0; k0 < a.lslices; k0 += kBatch) {
+        float part[kBatch][M];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) load_lane_m<M>(lg + min(k0 + k, a.lslices - 1) * a.lslice, a.E, lane, vec, part[k]);
+        if (k0 == 0 && a.has_shared) {
+            if (a.seg.bits == 4) sg = row_dot<XDT, 4>(a.seg, a.x, static_cast<int64_t>(t) * a.H, lane);
+            else sg = row_dot<XDT, 8>(a.seg, a.x, static_cast<int64_t>(t) * a.H, lane);
+        }
+#pragma unroll
+        for (int j = 0; j < M; ++j) {
+            float acc = k0 == 0 ? part[0][j] : v[j] + part[0][j];
+#pragma unroll
+            for (int k = 1; k < kBatch; ++k)
+                if (k0 + k < a.lslices) acc += part[k][j];
+            v[j] = acc;
+        }
+    }
+    if (a.bias) {
+#pragma unroll
+        for (int j = 0; j < M; ++j) v[j] += a.bias[min(lane * M + j, a.E - 1)];
+    }
+    Rounds<M> rd;
+    rounds_init(rd, v, a.E, lane);
+    rounds_run(rd, a.K, lane, s_pick);
+    const float w = rounds_weight(rd, a.K, a.norm, lane);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < a.K) {
+        const int32_t id = s_pick[lane];
+        const int64_t p = static_cast<int64_t>(t) * a.K + lane;
+        a.ids[p] = id;
+        a.wts[p] = w;
+        if (a.user_ids) a.user_ids[p] = id;
+        if (a.user_w) a.user_w[p] = w;
+    }
+    if (a.has_shared && lane == 0) a.sg[t] = sg;
+}
+
 template <int XDT>
 __global__ __launch_bounds__(kPfThreads) void pf_route(const RouteArgs a) {
-    __shared__ float s_lg[kRouteWaves][kMaxExperts];
+    __shared__ int32_t s_pick[kRouteWaves][SWQ_MAX_TOPK];
     __shared__ int s_last;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t = blockIdx.x * kRouteWaves + wave;
     if (t < a.T) {
-        const float *lg = a.logits + static_cast<int64_t>(t) * a.E;
-        for (int e = lane; e < a.E; e += kWave) s_lg[wave][e] = a.bias ? lg[e] + a.bias[e] : lg[e];
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        int32_t my_id;
-        float my_w;
-        topk_wave(s_lg[wave], a.E, a.K, a.norm, lane, my_id, my_w);
-        if (lane < a.K) {
-            const int64_t p = static_cast<int64_t>(t) * a.K + lane;
-            a.ids[p] = my_id;
-            a.wts[p] = my_w;
-            if (a.user_ids) a.user_ids[p] = my_id;
-            if (a.user_w) a.user_w[p] = my_w;
-        }
-        if (a.has_shared) {
-            const float v = row_dot<XDT>(a.seg, a.x, static_cast<int64_t>(t) * a.H, lane);
-            if (lane == 0) a.sg[t] = v;
-        }
+        const int M = (a.E + kWave - 1) / kWave;
+        if (M <= 1) route_token<XDT, 1>(a, t, lane, s_pick[wave]);
+        else if (M <= 2) route_token<XDT, 2>(a, t, lane, s_pick[wave]);
+        else if (M <= 4) route_token<XDT, 4>(a, t, lane, s_pick[wave]);
+        else if (M <= 8) route_token<XDT, 8>(a, t, lane, s_pick[wave]);
+        else route_token<XDT, 16>(a, t, lane, s_pick[wave]);
     }
     // the last workgroup to arrive groups the pairs: the barrier orders this
     // workgroup's stores before thread 0's release, the release before its
@@ -1259,9 +1409,14 @@ __global__ __launch_bounds__(kPfThreads) void pf_combine(const CombineArgs a) {
 // ---------------------------------------------------------------------------
 // host side
 
+// K slices of the router GEMM: kBlockG groups each (the last one 2 when the
+// group count is not a multiple of 4), so that 16-token tiles x 128-column
+// blocks x slices fill the device and a slice's loads are one round trip.
+int router_kslices(int H) { return (H / kGroupK + kBlockG - 1) / kBlockG; }
+
 struct PfLayout {
     size_t header, logits, sg, ids, wts, pos, tok, tiles, xs_x, xs_h, xa0, xa1, h_hi, h_lo, y, total;
-    int max_tiles, Ih, xs_ld_x, xs_ld_h;
+    int max_tiles, Ih, xs_ld_x, xs_ld_h, kslices;
 };
 
 PfLayout pf_layout(const swq_moe_layer *l, int T) {
@@ -1279,7 +1434,8 @@ PfLayout pf_layout(const swq_moe_layer *l, int T) {
                   (l->has_shared ? (T + kTileRows - 1) / kTileRows : 0);
     w.Ih = std::max(l->moe_intermediate, l->has_shared ? l->shared_intermediate : 0);
     w.header = take(256);  // [0] finished route workgroups, [1] tile count
-    w.logits = take(static_cast<size_t>(T) * l->num_experts * 4);
+    w.kslices = router_kslices(l->hidden);
+    w.logits = take(static_cast<size_t>(w.kslices) * T * l->num_experts * 4);  // [slice][T][E] partial logits
     w.sg = take(static_cast<size_t>(T) * 4);
     w.ids = take(P * 4);
     w.wts = take(P * 4);
@@ -1329,6 +1485,10 @@ int check_prefill_layer(const swq_moe_layer *l, int T) {
     const int H = l->hidden, E = l->num_experts, I = l->moe_intermediate;
     int st;
     if ((st = check_mfma(&l->router, E, H, false, E, false)) != SWQ_OK) return st;
+    // the router GEMM stages its scales and biases as aligned 4-byte words
+    if (((reinterpret_cast<uintptr_t>(l->router.scales) + l->router.s_off) % 4 != 0) ||
+        ((reinterpret_cast<uintptr_t>(l->router.biases) + l->router.b_off) % 4 != 0))
+        return SWQ_ERR_MISALIGNED;
     if ((st = check_mfma(&l->gate, I, H, true, E)) != SWQ_OK) return st;
     if ((st = check_mfma(&l->up, I, H, true, E)) != SWQ_OK) return st;
     if ((st = check_mfma(&l->down, H, I, true, E)) != SWQ_OK) return st;
@@ -1359,17 +1519,24 @@ int check_prefill_layer(const swq_moe_layer *l, int T) {
 
 template <int BITS, int SRC, int MT, int EPI, int SUM>
 void launch_gemm_st(int stype, const GemmArgs &a, int blocks, hipStream_t s) {
+    const dim3 grid(blocks, a.kslices);
     if (stype == SWQ_F16)
-        hipLaunchKernelGGL((pf_gemm<BITS, SWQ_F16, SRC, MT, EPI, SUM>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm<BITS, SWQ_F16, SRC, MT, EPI, SUM>), grid, dim3(kPfThreads), 0, s, a);
     else if (stype == SWQ_BF16)
-        hipLaunchKernelGGL((pf_gemm<BITS, SWQ_BF16, SRC, MT, EPI, SUM>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm<BITS, SWQ_BF16, SRC, MT, EPI, SUM>), grid, dim3(kPfThreads), 0, s, a);
     else
-        hipLaunchKernelGGL((pf_gemm<BITS, SWQ_F32, SRC, MT, EPI, SUM>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm<BITS, SWQ_F32, SRC, MT, EPI, SUM>), grid, dim3(kPfThreads), 0, s, a);
 }
 
 template <int SRC, int MT, int EPI, int SUM>
 int launch_gemm(const swq_qlinear &lin, const GemmArgs &a, int blocks, hipStream_t s) {
     if (blocks <= 0) return SWQ_OK;
+    // slices of kBlockG groups cover the rows' groups (an even count), the
+    // scale table covers the column block; tiled rows hold one slice
+    const int NG = a.K / kGroupK;
+    if (a.kgroups != std::min(kBlockG, NG) || a.kslices != (NG + kBlockG - 1) / kBlockG || a.col_block > 128 ||
+        a.col_wave != 32 || a.col_op != 16 || (a.kslices > 1 && (a.tiles || EPI != kEpiRows)))
+        return SWQ_ERR_INVALID_ARGUMENT;
     if (lin.bits == 4) launch_gemm_st<4, SRC, MT, EPI, SUM>(lin.scales_type, a, blocks, s);
     else launch_gemm_st<8, SRC, MT, EPI, SUM>(lin.scales_type, a, blocks, s);
     return launch_status();
@@ -1481,6 +1648,9 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         g.col_wave = 32;
         g.col_op = 16;
         g.nblk = (E + 127) / 128;
+        g.kslices = wl.kslices;
+        g.kgroups = std::min(kBlockG, H / kGroupK);
+        g.o_slice = static_cast<int64_t>(T) * E;
         const int blocks = gemm_blocks((T + kRouterRows - 1) / kRouterRows, g.nblk);
         st = bf16x ? launch_gemm<kSrcBF16, 1, kEpiRows, kSumStage>(layer->router, g, blocks, s)
                    : launch_gemm<kSrcF32, 1, kEpiRows, kSumStage>(layer->router, g, blocks, s);
@@ -1492,6 +1662,8 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         if (layer->has_shared) r.seg = make_qmat(&layer->shared_expert_gate);
         r.x = x;
         r.logits = logits;
+        r.lslices = wl.kslices;
+        r.lslice = static_cast<int64_t>(T) * E;
         r.bias = logit_bias;
         r.ids = reinterpret_cast<int32_t *>(wsb + wl.ids);
         r.wts = wts;
