@@ -749,6 +749,17 @@ __device__ __forceinline__ void ring_wait() {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(N) : "memory");
 }
 
+// ring_wait<Cn>() for the wave's count n of live activation copies per
+// group (wave-uniform, 0..4): one branch per count, each with its immediate.
+template <int C0, int C1, int C2, int C3, int C4>
+__device__ __forceinline__ void ring_wait_sel(int n) {
+    if (n <= 0) ring_wait<C0>();
+    else if (n == 1) ring_wait<C1>();
+    else if (n == 2) ring_wait<C2>();
+    else if (n == 3) ring_wait<C3>();
+    else ring_wait<C4>();
+}
+
 // The grouped quantised GEMM of pf_gemm (same tile, lanes and arithmetic) fed
 // by an LDS ring D groups deep: per group, each wave's DMA brings in its
 // share of the 64 activation rows (NPL bf16 planes, already in the order the
@@ -823,8 +834,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
     const uint8_t *asrc[NPL][AW];
     const uint8_t *xsrc[AW];
     // rows past the tile are not fetched (their LDS rows hold stale values,
-    // which stay in those rows of the matrix-core results, never stored);
-    // lane 0 always fetches so that no copy is empty
+    // which stay in those rows of the matrix-core results, never stored):
+    // a wave issues the copies of its slabs that hold tile rows (`live`, the
+    // same count every group; the ring waits use it), and within a partial
+    // slab lane 0 always fetches so that no copy is empty
+    const int live = min(AW, max(0, (rows + 7) / 8 - AW * wave));
     bool afetch[AW];
 #pragma unroll
     for (int i = 0; i < AW; ++i) {
@@ -869,11 +883,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
         for (int p = 0; p < NPL; ++p)
 #pragma unroll
             for (int i = 0; i < AW; ++i)
-            {
-                // the LDS address in a scalar register before the branch
-                const uint32_t d = __builtin_amdgcn_readfirstlane(base + p * ROWS * 128 + 8 * (AW * wave + i) * 128);
-                if (afetch[i]) dma16(asrc[p][i] + kGroupK * 2 * g, d);
-            }
+                if (i < live) {
+                    // the LDS address in a scalar register before the branch
+                    const uint32_t d = __builtin_amdgcn_readfirstlane(base + p * ROWS * 128 + 8 * (AW * wave + i) * 128);
+                    if (afetch[i]) dma16(asrc[p][i] + kGroupK * 2 * g, d);
+                }
     };
     // group g's code rows (and f32 scales) into B slot sb (LB instructions per wave)
     auto issue_b = [&](int sb, int g) {
@@ -961,7 +975,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
     // Loads return in order, so "at most N of this wave's loads in flight"
     // with N = the loads issued after A(g) means A(g) and everything before
     // it have landed; N is the same for every group from DA-1 on, and the
-    // first DA-1 groups are peeled with their own counts.
+    // first DA-1 groups are peeled with their own counts.  The counts depend
+    // on the wave's live copies n = NPL * live per group: with none, the same
+    // formula counts the loads after B(g) (issued one step before A(g)
+    // would be, DB = DA + 1) exactly in the loop and too few in the peeled
+    // groups (a stricter wait).
 #pragma unroll
     for (int s = 0; s < DB - 1; ++s) issue_b(s, min(s, NG - 1));
 #pragma unroll
@@ -971,15 +989,33 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
         issue_b(sb == 0 ? DB - 1 : sb - 1, min(g + DB - 1, NG - 1));
         compute(sa, sb, g);
     };
-    static_assert(DA <= 4, "peeled prologue");
-    if (0 < NG) { ring_wait<(DA - 2) * LA>(); step(0, 0, 0); }
-    if constexpr (DA >= 3) if (1 < NG) { ring_wait<(DA - 3) * LA + 1 * L>(); step(1, 1, 1); }
-    if constexpr (DA >= 4) if (2 < NG) { ring_wait<(DA - 4) * LA + 2 * L>(); step(2, 2, 2); }
+    static_assert(DA <= 4 && DB == DA + 1 && LA <= 4, "peeled prologue, wait counts");
+    const int nl = NPL * live;
+    // the wait counts for n live copies per group (n <= LA)
+    constexpr auto w0 = [](int n) constexpr { return (DA - 2) * n; };
+    constexpr auto w1 = [](int n) constexpr { return (DA - 3) * n + (n + LB); };
+    constexpr auto w2 = [](int n) constexpr { return (DA - 4) * n + 2 * (n + LB); };
+    constexpr auto wl = [](int n) constexpr { return LB + (DA - 2) * (n + LB); };
+    constexpr auto cl = [](int n) constexpr { return n < LA ? n : LA; };
+    if (0 < NG) {
+        ring_wait_sel<w0(0), w0(cl(1)), w0(cl(2)), w0(cl(3)), w0(cl(4))>(nl);
+        step(0, 0, 0);
+    }
+    if constexpr (DA >= 3)
+        if (1 < NG) {
+            ring_wait_sel<w1(0), w1(cl(1)), w1(cl(2)), w1(cl(3)), w1(cl(4))>(nl);
+            step(1, 1, 1);
+        }
+    if constexpr (DA >= 4)
+        if (2 < NG) {
+            ring_wait_sel<w2(0), w2(cl(1)), w2(cl(2)), w2(cl(3)), w2(cl(4))>(nl);
+            step(2, 2, 2);
+        }
     {
         int sa = (DA - 1) % DA, sb = (DA - 1) % DB;
 #pragma unroll 1
         for (int g = DA - 1; g < NG; ++g) {
-            ring_wait<LB + (DA - 2) * L>();
+            ring_wait_sel<wl(0), wl(cl(1)), wl(cl(2)), wl(cl(3)), wl(cl(4))>(nl);
             step(g, sa, sb);
             sa = sa + 1 == DA ? 0 : sa + 1;
             sb = sb + 1 == DB ? 0 : sb + 1;
