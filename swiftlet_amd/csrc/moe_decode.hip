@@ -526,14 +526,17 @@ __device__ __forceinline__ void gateup_pair(const MoEArgs &a, const LaneMap &lm,
                                             const RowTile<BITS, CPL, ES> &tg, const RowTile<BITS, CPL, ES> &tu,
                                             const XSlice<BITS, CPL, XF> &xs) {
     constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
-    float rg[RI], ru[RI];
-    dot_tile(rg, tg, xs, a.gate, lm);
-    dot_tile(ru, tu, xs, a.up, lm);
+    // both tiles' chunks interleaved (independent chains for a wave that has
+    // its SIMD to itself); the same results as a dot_tile per tile
+    const RowTile<BITS, CPL, ES> *tiles[2] = {&tg, &tu};
+    const QMat *mats[2] = {&a.gate, &a.up};
+    float r[2][RI];
+    dot_tiles<2>(r, tiles, mats, xs, lm);
     if (lm.j == lm.lpr - 1) {
 #pragma unroll
         for (int i = 0; i < RI; ++i) {
             const int row = row0 + i * lm.rpw + lm.q;
-            if (row < a.I) a.h[static_cast<int64_t>(p) * a.I + row] = swiglu(rg[i], ru[i]);
+            if (row < a.I) a.h[static_cast<int64_t>(p) * a.I + row] = swiglu(r[0][i], r[1][i]);
         }
     }
 }
