@@ -61,7 +61,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
 PREFILL_CONFIGS = {
     "qwen3.6-35b-a3b-q4-prefill512": ("qwen3.6-35b-a3b-q4", 512, 2024),
 }
-PREFILL_STAGES = [("prep", 1), ("router", 2), ("route", 4), ("gate_up", 8), ("down", 16), ("combine", 32)]
+PREFILL_STAGES = [("router", 2), ("route", 4), ("gate_up", 8), ("down", 16), ("combine", 32)]
 
 CONFIGS = {
     # name: (shape key, batch)
@@ -1001,7 +1001,6 @@ def prefill_measure(args, torch, lib, name):
     xb = T * H * 2
     P = T * K
     kbytes = {
-        "prep": xb,
         "router": mb(E, H, rb) + xb,
         "route": mb(1, H, rb) + xb,
         "gate_up": touched * 2 * mb(I, H, eb) + 2 * mb(Is, H, eb) + xb,

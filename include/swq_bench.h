@@ -62,8 +62,10 @@ int swq_moe_prefill_biased(const swq_moe_layer *layer, const void *x, int x_dtyp
                            void *ws, size_t ws_bytes, int flags, void *stream);
 
 /* swq_moe_prefill_biased (logit_bias may be NULL: none) running only the
- * launches whose bits are set in stage_mask: 1 activation prep, 2 router
- * GEMM, 4 routing and grouping, 8 gate/up + SwiGLU, 16 down, 32 combine.  A
+ * launches whose bits are set in stage_mask: 2 router GEMM (with the
+ * activation planes and group sums of x gate/up reads), 4 routing and
+ * grouping, 8 gate/up + SwiGLU, 16 down, 32 combine (bit 1, which named a
+ * separate activation prep, launches nothing).  A
  * launch reads what the earlier ones left in the workspace (a full call on
  * the same inputs leaves everything each one needs). */
 enum { SWQ_PREFILL_ALL = 63 };

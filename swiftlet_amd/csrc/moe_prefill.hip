@@ -7,7 +7,9 @@
 // path, which loops the same per-token computation (QwenCPUModel.swift:544-567).
 //
 // Launches, all on the caller's stream:
-//   1. router GEMM: logits[T, E], 16-token tiles;
+//   1. router GEMM: partial logits [slice][T, E], 16-token tiles x K slices
+//      of 4 groups; its first column block also writes x in the layout
+//      gate/up reads (bf16 planes) and the group sums of x;
 //   2. route: softmax, top-k (ties to the lower id), renormalisation and
 //      the shared-expert gate logit per token; the last workgroup to finish
 //      counts the pairs per expert and builds the sorted pair order and the
@@ -101,6 +103,11 @@ struct GemmArgs {
     // (the last may be shorter); rows outputs of slice s at o0 + s * o_slice
     int32_t kslices, kgroups;
     int64_t o_slice;
+    // pf_gemm (the router, first column block): x as the bf16 planes gate/up
+    // reads ([rows][a_ld]: hi, and lo for f32 x; in nibble_order within each
+    // 8 for 4-bit gate/up codes), or null
+    uint16_t *pl0, *pl1;
+    int32_t pl_perm;
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -604,6 +611,12 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
                 // loop's tail stages (the bias term reads columns < 64)
                 if (c8 == 0) s_xs[r * kXsPitch + (g < ge ? g : kXsPitch - 1)] = sum;
             }
+            // the activation planes of gate/up (one column block writes them)
+            if (a.pl0 && nb == 0 && g < ge && r < rows) {
+                const int64_t e = static_cast<int64_t>(row0 + r) * a.a_ld + kGroupK * g + 8 * c8;
+                *reinterpret_cast<u32x4_t *>(a.pl0 + e) = a.pl_perm ? nibble_order(hi) : hi;
+                if (a.pl1) *reinterpret_cast<u32x4_t *>(a.pl1 + e) = a.pl_perm ? nibble_order(lo) : lo;
+            }
             if constexpr (BITS == 4) {
                 hi = nibble_order(hi);
                 if constexpr (NPL == 2) lo = nibble_order(lo);
@@ -1036,49 +1049,6 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
         bias_term_bs<BITS, ST, MT>(acc, bi, xv, NG, rows, kg);
     }
     epilogue<EPI, MT, WAVES>(acc, a, col, N, active, row0, rows, nb, s_red);
-}
-
-// ---------------------------------------------------------------------------
-// activation prep: x as the bf16 planes gate/up reads (hi, and lo for fp32 x;
-// in nibble_order for 4-bit gate/up codes) and its group sums
-
-struct PrepArgs {
-    const void *x;
-    uint16_t *p0, *p1;   // planes [T, H] (null p0: x itself is read, only the sums are made)
-    float *xs;           // group sums [T, xs_ld]
-    int32_t T, H, xdt, perm, xs_ld;
-};
-
-__global__ __launch_bounds__(kPfThreads) void pf_prep(const PrepArgs a) {
-    const int64_t pc = static_cast<int64_t>(blockIdx.x) * kPfThreads + threadIdx.x;  // 8-element piece
-    const int per_row = a.H / 8;
-    const bool ok = pc < static_cast<int64_t>(a.T) * per_row;  // whole 8-lane groups (per_row % 8 == 0)
-    const int64_t e = (ok ? pc : 0) * 8;
-    u32x4_t hi, lo = {0u, 0u, 0u, 0u};
-    if (a.xdt == SWQ_BF16) {
-        hi = *reinterpret_cast<const u32x4_t *>(static_cast<const uint16_t *>(a.x) + e);
-    } else {
-        const float4 x0 = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + e);
-        const float4 x1 = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) + e + 4);
-        const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        split8(v, hi, lo);
-    }
-    float t[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) t[q] = (bf16_lo(hi[q]) + bf16_lo(lo[q])) + (bf16_hi(hi[q]) + bf16_hi(lo[q]));
-    const float sum = segment_reduce((t[0] + t[1]) + (t[2] + t[3]), 3);
-    if (!ok) return;
-    const int64_t row = pc / per_row;
-    const int c8 = static_cast<int>(pc - row * per_row);
-    if ((c8 & 7) == 0) a.xs[row * a.xs_ld + c8 / 8] = sum;
-    if (a.p0) {
-        if (a.perm) {
-            hi = nibble_order(hi);
-            lo = nibble_order(lo);
-        }
-        *reinterpret_cast<u32x4_t *>(a.p0 + e) = hi;
-        if (a.p1) *reinterpret_cast<u32x4_t *>(a.p1 + e) = lo;
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1645,28 +1615,12 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool bf16x = x_dtype == SWQ_BF16;
 
-    // 0. x planes for gate/up (nibble_order for 4-bit codes, hi/lo for fp32 x)
-    //    and the group sums of x
+    // x planes for gate/up (nibble_order for 4-bit codes, hi/lo for fp32 x)
+    // and the group sums of x: written by the router GEMM as it stages x
     const bool perm_x = layer->gate.bits == 4;
     const bool planes = perm_x || !bf16x;
     uint16_t *xa0 = reinterpret_cast<uint16_t *>(wsb + wl.xa0);
     uint16_t *xa1 = reinterpret_cast<uint16_t *>(wsb + wl.xa1);
-    if (stage_mask & 1) {
-        PrepArgs pa{};
-        pa.x = x;
-        pa.p0 = planes ? xa0 : nullptr;
-        pa.p1 = planes && !bf16x ? xa1 : nullptr;
-        pa.xs = xs_x;
-        pa.T = T;
-        pa.H = H;
-        pa.xdt = x_dtype;
-        pa.perm = perm_x ? 1 : 0;
-        pa.xs_ld = wl.xs_ld_x;
-        const int64_t pieces = static_cast<int64_t>(T) * H / 8;
-        hipLaunchKernelGGL(pf_prep, dim3(static_cast<unsigned>((pieces + kPfThreads - 1) / kPfThreads)),
-                           dim3(kPfThreads), 0, s, pa);
-        if ((st = launch_status()) != SWQ_OK) return st;
-    }
     // 1. router logits
     if (stage_mask & 2) {
         GemmArgs g{};
@@ -1687,6 +1641,11 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         g.kslices = wl.kslices;
         g.kgroups = std::min(kBlockG, H / kGroupK);
         g.o_slice = static_cast<int64_t>(T) * E;
+        g.xs_out = xs_x;
+        g.xs_ld_out = wl.xs_ld_x;
+        g.pl0 = planes ? xa0 : nullptr;
+        g.pl1 = planes && !bf16x ? xa1 : nullptr;
+        g.pl_perm = perm_x ? 1 : 0;
         const int blocks = gemm_blocks((T + kRouterRows - 1) / kRouterRows, g.nblk);
         st = bf16x ? launch_gemm<kSrcBF16, 1, kEpiRows, kSumStage>(layer->router, g, blocks, s)
                    : launch_gemm<kSrcF32, 1, kEpiRows, kSumStage>(layer->router, g, blocks, s);
