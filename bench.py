@@ -51,8 +51,8 @@ MEASURED_TRAFFIC = {
     ("qwen3.6-35b-a3b-q8-b4", "moe_stage1"): 4_461_998,
     ("qwen3.6-35b-a3b-q8-b4", "moe_stage2"): 69_598_251,
     ("qwen3.6-35b-a3b-q8-b4", "moe_stage3"): 36_610_935,
-    ("qwen3.6-35b-a3b-q4-prefill512", "gate_up"): 347_655_510,
-    ("qwen3.6-35b-a3b-q4-prefill512", "down"): 209_624_345,
+    ("qwen3.6-35b-a3b-q4-prefill512", "gate_up"): 347_003_996,
+    ("qwen3.6-35b-a3b-q4-prefill512", "down"): 209_619_225,
 }
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
