@@ -418,7 +418,7 @@ int swq_moe_workspace_init(void *ws, size_t ws_bytes, void *stream);
 /* Whether every swq_moe_decode / swq_moe_decode_norm call on this workspace
  * since the last cleared check completed normally: SWQ_OK, or
  * SWQ_ERR_STALLED when one ran out of a bounded wait.  The single-launch
- * (batch 1) kernel has one or two workgroups per CU and hands data between them
+ * (batch 1) kernel has one workgroup per CU and hands data between them
  * through the workspace; it assumes the whole grid is resident at once,
  * which holds on a device running nothing else.  If other work occupies
  * CUs, a wait can last about a second and then give up, and that call's

@@ -16,7 +16,7 @@ namespace swq {
 // gate/up rows in one format, 4- or 8-bit down rows, an 8-bit router and
 // shared-expert gate.  M = ceil(E / 64), as the staged path's routing wave.
 static FusedKernel fused_kernel_for(const QMat &router, const QMat &gate, const QMat &down, int x_dtype, int E,
-                                    bool prenorm, int wpc) {
+                                    bool prenorm) {
     if (router.bits != 8) return nullptr;
     const int m = (E + kWave - 1) / kWave;
     const int M = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
@@ -31,13 +31,13 @@ static FusedKernel fused_kernel_for(const QMat &router, const QMat &gate, const 
         gfmt = gate.cpl == 2 ? kFusedQ8C2 : kFusedQ8C1;
     }
     if (gfmt < 0) return nullptr;
-    if (prenorm) return x_dtype == SWQ_F32 ? fused_select_pn(gfmt, rc2, M, wpc) : nullptr;
-    return x_dtype == SWQ_BF16 ? fused_select_bf16(gfmt, rc2, M, wpc) : fused_select_f32(gfmt, rc2, M, wpc);
+    if (prenorm) return x_dtype == SWQ_F32 ? fused_select_pn(gfmt, rc2, M) : nullptr;
+    return x_dtype == SWQ_BF16 ? fused_select_bf16(gfmt, rc2, M) : fused_select_f32(gfmt, rc2, M);
 }
 
 // Per device, set once by fused_probe_device (under std::call_once, then
 // read with acquire loads): the CU count and whether the workgroups of each
-// group (b mod kGroups) of a grid of two workgroups per CU (so also of one)
+// group (b mod kGroups) of a grid of one workgroup per CU
 // run on one XCD.  The kernels whose occupancy has been checked sit in a
 // small list under a mutex.
 struct FusedDevice {
@@ -57,11 +57,11 @@ __global__ __launch_bounds__(kFusedThreads) void xcd_probe_kernel(int32_t *out) 
     }
 }
 
-// Workgroups of the fused launch on device `dev`: wpc per CU, rounded down
-// to whole groups, provided the kernel fits wpc workgroups per CU (so the
+// Workgroups of the fused launch on device `dev`: one per CU, rounded down
+// to whole groups, provided the kernel fits one workgroup per CU (so the
 // grid is resident at once on an idle device); 0 if not, or before the
 // device's probe.
-static int fused_blocks(FusedKernel k, int dev, int wpc) {
+static int fused_blocks(FusedKernel k, int dev) {
     FusedDevice &d = g_fused_dev[dev];
     const int cus = d.cus.load(std::memory_order_acquire);
     if (cus <= 0) return 0;
@@ -74,13 +74,13 @@ static int fused_blocks(FusedKernel k, int dev, int wpc) {
             int per_cu = 0;
             fits = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(k),
                                                                 kFusedThreads, 0) == hipSuccess &&
-                           per_cu >= wpc
+                           per_cu >= 1
                        ? 1
                        : 0;
             d.fits.emplace_back(k, fits);
         }
     }
-    return fits ? min(cus * wpc, kFusedMaxBlocks) / kGroups * kGroups : 0;
+    return fits ? min(cus, kFusedMaxBlocks) / kGroups * kGroups : 0;
 }
 
 // The fused launch's arguments for this layer, or no kernel when the layer,
@@ -127,19 +127,9 @@ static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch
     if (layer->moe_intermediate > kMaxInterFused || layer->moe_intermediate % 2 != 0) return nullptr;
     if (prenorm && layer->hidden > kPrenormMaxHidden) return nullptr;
     if (layer->hidden > kFusedMaxHidden || layer->num_experts > kMaxExperts) return nullptr;
-    // two workgroups per CU when a group's routed bytes (its slots' gate, up
-    // and down matrices) exceed kTwoPerCUBytes
-    auto mat_bytes = [](const swq_qlinear &m) {
-        const size_t es = m.scales_type == SWQ_F32 ? 4 : 2;
-        return static_cast<size_t>(m.out_dim) * m.in_dim * m.bits / 8 +
-               static_cast<size_t>(m.out_dim) * (m.in_dim / m.group_size) * 2 * es;
-    };
-    const size_t group_bytes = static_cast<size_t>((layer->top_k + kGroups - 1) / kGroups) *
-                               (mat_bytes(layer->gate) + mat_bytes(layer->up) + mat_bytes(layer->down));
-    const int wpc = group_bytes > kTwoPerCUBytes ? 2 : 1;
-    FusedKernel kern = fused_kernel_for(a.router, a.gate, a.down, x_dtype, layer->num_experts, prenorm, wpc);
+    FusedKernel kern = fused_kernel_for(a.router, a.gate, a.down, x_dtype, layer->num_experts, prenorm);
     if (!kern) return nullptr;
-    const int blocks = fused_blocks(kern, dev, wpc);
+    const int blocks = fused_blocks(kern, dev);
     if (blocks <= 0) return nullptr;
     const int H = layer->hidden;
     a.nb = blocks;
@@ -154,9 +144,9 @@ static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch
     a.has_shared = layer->has_shared ? 1 : 0;
     const int gate_rpw = kWave >> a.gate.lpr_log2;
     a.sh_tiles = a.has_shared ? (a.Is + gate_rpw - 1) / gate_rpw : 0;
-    const int gate_rows = gate_passes(a.gate.bits, a.gate.cpl, wpc) * gate_rpw;
+    const int gate_rows = gate_passes(a.gate.bits, a.gate.cpl) * gate_rpw;
     a.gu_tpe = (a.I + gate_rows - 1) / gate_rows;
-    const int down_rows = down_passes(a.down.bits, wpc) * (kWave >> a.down.lpr_log2);
+    const int down_rows = down_passes(a.down.bits) * (kWave >> a.down.lpr_log2);
     a.dn_tpe = (H + down_rows - 1) / down_rows;
     a.local = g_fused_dev[dev].local.load(std::memory_order_acquire);
     *fa = a;
@@ -200,7 +190,7 @@ int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int bat
     return SWQ_OK;
 }
 
-// Once per device: the CU count and whether a grid of two workgroups per CU
+// Once per device: the CU count and whether a grid of one workgroup per CU
 // places every group's workgroups on one XCD (a launch of that grid reports
 // each workgroup's XCC_ID).  Blocking; runs on `stream`.  Thread-safe: the
 // first caller for a device runs the probe (std::call_once), later ones
@@ -218,7 +208,7 @@ int fused_probe_device(hipStream_t stream, void *given) {
             status = SWQ_ERR_HIP;
             return;
         }
-        const int n = min(cus * 2, kFusedMaxBlocks) / kGroups * kGroups;  // the larger grid
+        const int n = min(cus, kFusedMaxBlocks) / kGroups * kGroups;  // the fused grid
         int ok = 0;
         if (n >= kGroups) {
             int32_t *buf = static_cast<int32_t *>(given);

@@ -1,10 +1,12 @@
 // MoE-layer decode step for one token in a single launch on gfx950.
 //
-// One workgroup of four waves (one wave per SIMD) per CU, launched as an
+// One workgroup of eight waves (two per SIMD) per CU, launched as an
 // ordinary kernel: on a device with no other work the whole grid is resident
-// at once, and a grid of four-wave workgroups, one per CU, has every wave
-// running within ~0.7 us of the launch (eight-wave workgroups take ~2.4 us
-// to start on MI355X, measured).  The stages hand data to each other through
+// at once.  Eight waves halve each wave's rows of every dot product (at one
+// wave per SIMD a dependency chain leaves most issue slots empty); against
+// four-wave workgroups, measured: the 80B, 8-bit and folded-norm steps
+// 0.6-0.8 us faster, the 4-bit 35B step unchanged, the single-expert step
+// 0.2 us slower.  The stages hand data to each other through
 // the workspace instead of kernel boundaries: every value crossing
 // workgroups is one 8-byte word (fp32 value, call epoch), written and polled
 // with relaxed device-scope atomics, so a consumer polls the data itself and
@@ -30,8 +32,8 @@
 //            them.  The rounds of picks the workgroup does not own, and the
 //            combine weights, finish after its routed work.
 //   routed   per owned slot: gate/up rows (+ SwiGLU) -> activations in the
-//            XCD's L2; the slot's activations -> LDS (each wave polls a
-//            quarter); down rows (their loads issued with the gate/up
+//            XCD's L2; the slot's activations -> LDS (each wave polls an
+//            eighth); down rows (their loads issued with the gate/up
 //            loads) -> partial outputs, one word per (slot, output row).
 //   combine  the workgroup's output rows: routed partials in pick order,
 //            then the gated shared expert (+ the residual stream).
@@ -58,12 +60,13 @@
 // Phase stamps for timing studies: SWQ_FUSED_TRACE builds record
 // s_memrealtime per (workgroup, wave, point); product builds compile them out.
 #ifdef SWQ_FUSED_TRACE
-static __device__ unsigned long long g_swq_fused_trace[1024 * 4 * 16];
+// 16 stamps per (workgroup, wave), 8 waves per workgroup
+static __device__ unsigned long long g_swq_fused_trace[1024 * 8 * 16];
 // host access to one translation unit's stamps (the array is per code object)
 #define SWQ_TRACE_ACCESSOR(name)                                                                        \
     extern "C" int name(void *host, size_t bytes, int clear) {                                          \
         if (clear) {                                                                                    \
-            static unsigned long long z[1024 * 4 * 16];                                                 \
+            static unsigned long long z[1024 * 8 * 16];                                                 \
             return hipMemcpyToSymbol(HIP_SYMBOL(g_swq_fused_trace), z, sizeof(z)) == hipSuccess ? 0 : -1; \
         }                                                                                               \
         return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_swq_fused_trace), bytes) == hipSuccess ? 0 : -1;  \
@@ -72,7 +75,7 @@ static __device__ unsigned long long g_swq_fused_trace[1024 * 4 * 16];
 // the wave's vector-memory count, which every later load wait also drains)
 // and to the global array once, at the end of the kernel.
 #define SWQ_TRACE_DECL                                                                      \
-    __shared__ unsigned long long s_trace[4 * 16];                                          \
+    __shared__ unsigned long long s_trace[8 * 16];                                          \
     if ((threadIdx.x & 63) < 16) s_trace[(threadIdx.x >> 6) * 16 + (threadIdx.x & 63)] = 0
 #define SWQ_STAMP(n)                                                                        \
     do {                                                                                    \
@@ -81,7 +84,7 @@ static __device__ unsigned long long g_swq_fused_trace[1024 * 4 * 16];
 #define SWQ_TRACE_FLUSH                                                                     \
     do {                                                                                    \
         __syncthreads();                                                                    \
-        if (threadIdx.x < 64) g_swq_fused_trace[blockIdx.x * 64 + threadIdx.x] = s_trace[threadIdx.x]; \
+        if (threadIdx.x < 128) g_swq_fused_trace[blockIdx.x * 128 + threadIdx.x] = s_trace[threadIdx.x]; \
     } while (0)
 #else
 #define SWQ_TRACE_DECL \
@@ -97,7 +100,7 @@ static __device__ unsigned long long g_swq_fused_trace[1024 * 4 * 16];
 
 namespace swq {
 
-constexpr int kFusedWaves = 4;
+constexpr int kFusedWaves = 8;  // two per SIMD: one workgroup per CU
 constexpr int kFusedThreads = kFusedWaves * kWave;
 constexpr int kGroups = 8;
 constexpr int kReplicas = kFusedReplicas;  // logit replicas (one per XCD group)
@@ -385,8 +388,8 @@ __device__ __forceinline__ void down_dot(float (&res)[DRI], const RowTile<DB, 1,
 // lane of the 8-bit router and shared-expert gate rows; M logits per lane
 // of the routing wave.
 
-template <int XDT, int GB, int GC, int GX, int GRI, int DB, int DRI, int RC, int M, bool PN, int WPC>
-__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(WPC, WPC))) void moe_fused(FusedArgs a) {
+template <int XDT, int GB, int GC, int GX, int GRI, int DB, int DRI, int RC, int M, bool PN>
+__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(kFusedWaves / 4, kFusedWaves / 4))) void moe_fused(FusedArgs a) {
     __shared__ int32_t s_ids[SWQ_MAX_TOPK];
     __shared__ float s_w[SWQ_MAX_TOPK];
     __shared__ __attribute__((aligned(16))) uint32_t s_hb[kMaxInterFused];   // a routed slot's activations
@@ -394,7 +397,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(W
     __shared__ float s_cmb[SWQ_MAX_TOPK * kMaxCombineRows];
     __shared__ float s_shd[kMaxCombineRows];  // shared-expert down rows of the combine rows
     __shared__ float s_sg;                    // shared-expert gate logit
-    __shared__ int32_t s_arrive;              // waves with their third of the shared activations in
+    __shared__ int32_t s_arrive;              // waves with their share of the shared activations in
     __shared__ __attribute__((aligned(16))) float s_x[PN ? kPrenormMaxHidden : 4];  // the normalised input
     __shared__ float s_red[kFusedWaves];
 
@@ -465,13 +468,11 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(W
     asm volatile("" : "+v"(lane));
     const LaneMap lmg = lane_map(a.gate.lpr_log2, lane);
     const LaneMap lmr = lane_map(a.router.lpr_log2, lane);
-    // the router and shared gate/up rows go to the first NF workgroups,
-    // which the hardware starts first
-    const int NF = NB / WPC;
-    const int t_r = b < NF ? b + NF * wave : a.E;                             // first router tile of this wave
+    // router and shared gate/up tiles: tile b + NB * w on wave w of workgroup b
+    const int t_r = b + NB * wave;  // first router tile of this wave
     const bool has_r = t_r * lmr.rpw < a.E;
     const bool do_seg = a.has_shared && wave == 1;
-    const int t_s = b < NF ? b + NF * (kFusedWaves - 1 - wave) : a.sh_tiles;  // first shared gate/up tile
+    const int t_s = b + NB * (kFusedWaves - 1 - wave);  // first shared gate/up tile
     const bool has_s = a.has_shared && t_s < a.sh_tiles;
     RowTile<8, RC, 2, 1> rt;
     if (has_r) load_tile(rt, a.router, 0, lmr, t_r * lmr.rpw, a.E);
@@ -481,10 +482,8 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(W
         load_tile(stg, a.sh_gate, 0, lmg, t_s * lmg.rpw, a.Is);
         load_tile(stu, a.sh_up, 0, lmg, t_s * lmg.rpw, a.Is);
     }
-    // the shared expert's down tile of this workgroup's output rows (wave 1),
-    // held until the shared activations are in
     // the shared expert's down rows of this workgroup's output rows: one
-    // pass of rows each for waves 1-3, loaded now, used once the shared
+    // pass of rows each for waves 1.., loaded now, used once the shared
     // activations are in
     const LaneMap lms = lane_map(a.sh_down.lpr_log2, lane);
     const bool sh_rows = a.has_shared && nr > 0;
@@ -505,8 +504,8 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(W
     if (has_r || do_seg) {
         XSlice<8, RC, kXF32> xr;
         xslice_convert(xr, xrr);
-        for (int t = t_r; t * lmr.rpw < a.E; t += NF * kFusedWaves) {
-            // router tiles t_r, t_r + 4 NF, ...: one pass of rows each -> logits
+        for (int t = t_r; t * lmr.rpw < a.E; t += NB * kFusedWaves) {
+            // router tiles t_r, t_r + 8 NB, ...: one pass of rows each -> logits
             if (t != t_r) load_tile(rt, a.router, 0, lmr, t * lmr.rpw, a.E);
             float res[1];
             dot_rows(res, rt, a.router, xr, lmr);
@@ -530,8 +529,8 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(W
     XSlice<GB, GC, GX> xg;
     xslice_convert(xg, xgr);
     asm volatile("" : "+v"(lane));
-    for (int t = t_s; has_s && t < a.sh_tiles; t += NF * kFusedWaves) {
-        // shared-expert gate/up tiles t_s, t_s + 4 NF, ...: SwiGLU activations
+    for (int t = t_s; has_s && t < a.sh_tiles; t += NB * kFusedWaves) {
+        // shared-expert gate/up tiles t_s, t_s + 8 NB, ...: SwiGLU activations
         const int row0 = t * lmg.rpw;
         if (t != t_s) {
             load_tile(stg, a.sh_gate, 0, lmg, row0, a.Is);
@@ -606,7 +605,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(W
             // and the barrier that follow (allowed across an acquire), so they
             // would start only once the activations are in.
             asm volatile("" ::: "memory");
-            // the slot's activations: each wave polls a quarter into LDS
+            // the slot's activations: each wave polls an eighth into LDS
             const int np = a.I / 2, q = (np + kFusedWaves - 1) / kFusedWaves;
             fetch_acts<DB>(a.h_x + static_cast<int64_t>(s) * a.I, min(np, wave * q), min(np, (wave + 1) * q), g,
                            s_hb, lane, a.err);
@@ -630,7 +629,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(W
         }
     }
     // ---- wave 0: the remaining picks, the weights, this workgroup's rows of
-    // every slot's down output; wave 1: the shared expert's down rows -------
+    // every slot's down output; waves 1..: the shared expert's down rows ---
     asm volatile("" : "+v"(lane));
     if (wave == 0) {
         rounds_run(rd, a.K, lane, s_ids);
@@ -662,8 +661,8 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(W
         }
         SWQ_STAMP(8);
     } else if (sh_rows) {
-        // a third of the shared activations -> LDS, then, once all three
-        // waves' thirds are in, this wave's passes of the shared down rows
+        // a share of the shared activations -> LDS, then, once every
+        // wave's share is in, this wave's passes of the shared down rows
         const int np = a.Is / 2, q3 = (np + kFusedWaves - 2) / (kFusedWaves - 1);
         fetch_acts<DB>(a.hsh_x, min(np, sp0 * q3), min(np, (sp0 + 1) * q3), g, s_hsh, lane, a.err);
         SWQ_STAMP(12);
@@ -724,35 +723,22 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(W
 
 using FusedKernel = void (*)(FusedArgs);
 
-// Workgroups per CU: one, or two (two waves per SIMD) when a group's
-// routed bytes are large enough that the extra waves' dot products pay for
-// their start (measured: the 80B and 8-bit 35B steps gain, the 4-bit 35B
-// and single-expert steps lose).
-constexpr size_t kTwoPerCUBytes = static_cast<size_t>(5) << 19;  // 2.5 MiB per group
-
 // Passes per tile, chosen so that a slot's gate/up and down rows at the
-// benchmark shapes are one tile per wave (I = 512 rows over the 128 WPC
-// waves of a group: 4 / WPC rows per wave and matrix; H = 2048 down rows:
-// 16 / WPC per wave).
-constexpr int gate_passes(int gb, int gc, int wpc) { return (gb == 4 && gc == 2 ? 2 : 4) / wpc; }
-constexpr int down_passes(int db, int wpc) { return (db == 4 ? 4 : 8) / wpc; }
-
-template <int XDT, int GB, int GC, int GX, int DB, int RC, bool PN, int WPC>
-static FusedKernel fused_by_m_wpc(int M) {
-    constexpr int GRI = gate_passes(GB, GC, WPC), DRI = down_passes(DB, WPC);
-    switch (M) {
-        case 1: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 1, PN, WPC>;
-        case 2: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 2, PN, WPC>;
-        case 4: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 4, PN, WPC>;
-        case 8: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 8, PN, WPC>;
-        default: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 16, PN, WPC>;
-    }
-}
+// benchmark shapes are one tile per wave (I = 512 rows over the 256 waves of
+// a group: 2 rows per wave and matrix; H = 2048 down rows: 8 per wave).
+constexpr int gate_passes(int gb, int gc) { return gb == 4 && gc == 2 ? 1 : 2; }
+constexpr int down_passes(int db) { return db == 4 ? 2 : 4; }
 
 template <int XDT, int GB, int GC, int GX, int DB, int RC, bool PN>
-static FusedKernel fused_by_m(int M, int wpc) {
-    return wpc == 2 ? fused_by_m_wpc<XDT, GB, GC, GX, DB, RC, PN, 2>(M)
-                    : fused_by_m_wpc<XDT, GB, GC, GX, DB, RC, PN, 1>(M);
+static FusedKernel fused_by_m(int M) {
+    constexpr int GRI = gate_passes(GB, GC), DRI = down_passes(DB);
+    switch (M) {
+        case 1: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 1, PN>;
+        case 2: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 2, PN>;
+        case 4: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 4, PN>;
+        case 8: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 8, PN>;
+        default: return moe_fused<XDT, GB, GC, GX, GRI, DB, DRI, RC, 16, PN>;
+    }
 }
 
 // Gate/up formats of the single launch: 4-bit codes, 8-bit codes with two
@@ -760,10 +746,9 @@ static FusedKernel fused_by_m(int M, int wpc) {
 enum FusedGateFormat { kFusedQ4 = 0, kFusedQ8C2 = 1, kFusedQ8C1 = 2 };
 
 // The instantiation for (gate/up format, router chunks per lane 2 or 1,
-// logits per routing lane M, workgroups per CU), one per activation format;
-// nullptr for none.
-FusedKernel fused_select_bf16(int gfmt, bool rc2, int M, int wpc);
-FusedKernel fused_select_f32(int gfmt, bool rc2, int M, int wpc);
-FusedKernel fused_select_pn(int gfmt, bool rc2, int M, int wpc);
+// logits per routing lane M), one per activation format; nullptr for none.
+FusedKernel fused_select_bf16(int gfmt, bool rc2, int M);
+FusedKernel fused_select_f32(int gfmt, bool rc2, int M);
+FusedKernel fused_select_pn(int gfmt, bool rc2, int M);
 
 }  // namespace swq

@@ -4,10 +4,10 @@
 
 namespace swq {
 
-FusedKernel fused_select_bf16(int gfmt, bool rc2, int M, int wpc) {
-    if (gfmt == kFusedQ4) return rc2 ? fused_by_m<SWQ_BF16, 4, 2, kXBF16, 4, 2, false>(M, wpc) : fused_by_m<SWQ_BF16, 4, 2, kXBF16, 4, 1, false>(M, wpc);
-    if (gfmt == kFusedQ8C2) return rc2 ? fused_by_m<SWQ_BF16, 8, 2, kXF32, 8, 2, false>(M, wpc) : fused_by_m<SWQ_BF16, 8, 2, kXF32, 8, 1, false>(M, wpc);
-    if (gfmt == kFusedQ8C1) return rc2 ? fused_by_m<SWQ_BF16, 8, 1, kXF32, 8, 2, false>(M, wpc) : fused_by_m<SWQ_BF16, 8, 1, kXF32, 8, 1, false>(M, wpc);
+FusedKernel fused_select_bf16(int gfmt, bool rc2, int M) {
+    if (gfmt == kFusedQ4) return rc2 ? fused_by_m<SWQ_BF16, 4, 2, kXBF16, 4, 2, false>(M) : fused_by_m<SWQ_BF16, 4, 2, kXBF16, 4, 1, false>(M);
+    if (gfmt == kFusedQ8C2) return rc2 ? fused_by_m<SWQ_BF16, 8, 2, kXF32, 8, 2, false>(M) : fused_by_m<SWQ_BF16, 8, 2, kXF32, 8, 1, false>(M);
+    if (gfmt == kFusedQ8C1) return rc2 ? fused_by_m<SWQ_BF16, 8, 1, kXF32, 8, 2, false>(M) : fused_by_m<SWQ_BF16, 8, 1, kXF32, 8, 1, false>(M);
     return nullptr;
 }
 

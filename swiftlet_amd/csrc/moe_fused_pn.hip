@@ -4,10 +4,10 @@
 
 namespace swq {
 
-FusedKernel fused_select_pn(int gfmt, bool rc2, int M, int wpc) {
-    if (gfmt == kFusedQ4) return rc2 ? fused_by_m<SWQ_F32, 4, 1, kXF32, 4, 2, true>(M, wpc) : fused_by_m<SWQ_F32, 4, 1, kXF32, 4, 1, true>(M, wpc);
-    if (gfmt == kFusedQ8C2) return rc2 ? fused_by_m<SWQ_F32, 8, 2, kXF32, 8, 2, true>(M, wpc) : fused_by_m<SWQ_F32, 8, 2, kXF32, 8, 1, true>(M, wpc);
-    if (gfmt == kFusedQ8C1) return rc2 ? fused_by_m<SWQ_F32, 8, 1, kXF32, 8, 2, true>(M, wpc) : fused_by_m<SWQ_F32, 8, 1, kXF32, 8, 1, true>(M, wpc);
+FusedKernel fused_select_pn(int gfmt, bool rc2, int M) {
+    if (gfmt == kFusedQ4) return rc2 ? fused_by_m<SWQ_F32, 4, 1, kXF32, 4, 2, true>(M) : fused_by_m<SWQ_F32, 4, 1, kXF32, 4, 1, true>(M);
+    if (gfmt == kFusedQ8C2) return rc2 ? fused_by_m<SWQ_F32, 8, 2, kXF32, 8, 2, true>(M) : fused_by_m<SWQ_F32, 8, 2, kXF32, 8, 1, true>(M);
+    if (gfmt == kFusedQ8C1) return rc2 ? fused_by_m<SWQ_F32, 8, 1, kXF32, 8, 2, true>(M) : fused_by_m<SWQ_F32, 8, 1, kXF32, 8, 1, true>(M);
     return nullptr;
 }
 
