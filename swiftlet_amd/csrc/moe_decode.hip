@@ -521,17 +521,29 @@ __device__ __forceinline__ void gateup_issue(const MoEArgs &a, const Slots &r, c
     load_xraw<XDT>(xr, a.gate, lm, a.x, static_cast<int64_t>(unit_pair(a, r, s, 0) / a.K) * a.H);
 }
 
-template <int BITS, int CPL, int ES, int XF>
+// Stage-2 waves per SIMD by plan: 8-bit tiles fit two waves' registers (the
+// other wave's dot products fill the issue slots one wave's loads leave
+// idle), except with two chunks of fp32 activations per lane; 4-bit ones
+// with packed-bf16 activations do not.
+template <int XDT, int BITS, int CPL>
+constexpr int kStage2Waves = BITS == 8 && (XDT == SWQ_BF16 || CPL == 1) ? 2 : 1;
+
+template <int XDT, int BITS, int CPL, int ES, int XF>
 __device__ __forceinline__ void gateup_pair(const MoEArgs &a, const LaneMap &lm, int row0, int p,
                                             const RowTile<BITS, CPL, ES> &tg, const RowTile<BITS, CPL, ES> &tu,
                                             const XSlice<BITS, CPL, XF> &xs) {
     constexpr int RI = RowTile<BITS, CPL, ES>::kRI;
-    // both tiles' chunks interleaved (independent chains for a wave that has
-    // its SIMD to itself); the same results as a dot_tile per tile
-    const RowTile<BITS, CPL, ES> *tiles[2] = {&tg, &tu};
-    const QMat *mats[2] = {&a.gate, &a.up};
     float r[2][RI];
-    dot_tiles<2>(r, tiles, mats, xs, lm);
+    if constexpr (kStage2Waves<XDT, BITS, CPL> == 1) {
+        // both tiles' chunks interleaved: independent chains for a wave that
+        // has its SIMD to itself; the same results as a dot_tile per tile
+        const RowTile<BITS, CPL, ES> *tiles[2] = {&tg, &tu};
+        const QMat *mats[2] = {&a.gate, &a.up};
+        dot_tiles<2>(r, tiles, mats, xs, lm);
+    } else {
+        dot_tile(r[0], tg, xs, a.gate, lm);
+        dot_tile(r[1], tu, xs, a.up, lm);
+    }
     if (lm.j == lm.lpr - 1) {
 #pragma unroll
         for (int i = 0; i < RI; ++i) {
@@ -553,14 +565,14 @@ __device__ __forceinline__ void gateup_run(const MoEArgs &a, const Slots &r, con
         // sources are never one runtime-selected array.
         XSlice<BITS, CPL, XF> xs;
         xslice_convert(xs, xr);
-        gateup_pair(a, lm, row0, unit_pair(a, r, s, 0), tg, tu, xs);
+        gateup_pair<XDT>(a, lm, row0, unit_pair(a, r, s, 0), tg, tu, xs);
     }
     const int np = r.np[s];
     for (int pi = 1; pi < np; ++pi) {
         const int p = unit_pair(a, r, s, pi);
         XSlice<BITS, CPL, XF> xs;
         load_xslice<XDT>(xs, a.gate, lm, a.x, static_cast<int64_t>(p / a.K) * a.H);
-        gateup_pair(a, lm, row0, p, tg, tu, xs);
+        gateup_pair<XDT>(a, lm, row0, p, tg, tu, xs);
     }
 }
 
@@ -588,8 +600,11 @@ __device__ __forceinline__ void gateup_units(const MoEArgs &a, const Slots &r, i
 
 // The routing stage 1 published into LDS, then the waves take the (slot,
 // row tile) units of the distinct experts' gate/up rows grid-stride.
-template <int XDT>
-__global__ __launch_bounds__(kThreads12) void moe_stage2(MoEArgs a) {
+// One instance per plan of the gate/up matrices, so that each allocates
+// only the registers its own tiles need.
+template <int XDT, int BITS, int CPL, int ES, int XF>
+__global__ __launch_bounds__(kThreads12) __attribute__((amdgpu_waves_per_eu(kStage2Waves<XDT, BITS, CPL>))) void moe_stage2(
+    MoEArgs a) {
     __shared__ Slots sl;
     STAGE_TRACE_DECL;
     STAGE_STAMP(0);
@@ -601,9 +616,52 @@ __global__ __launch_bounds__(kThreads12) void moe_stage2(MoEArgs a) {
     const int tps = (a.I + rows - 1) / rows;
     const int nu = sl.n * tps;
     const int W = gridDim.x * (kThreads12 / kWave);
-    SWQ_DISPATCH(XDT, a.gate, gateup_units, a, sl, blockIdx.x * (kThreads12 / kWave) + wave, W, tps, nu, lane);
+    gateup_units<XDT, BITS, CPL, ES, XF>(a, sl, blockIdx.x * (kThreads12 / kWave) + wave, W, tps, nu, lane);
     STAGE_STAMP(15);
     STAGE_TRACE_FLUSH(0);
+}
+
+// Stage 2 over `units` wave units: at most the workgroups the device holds at
+// once (occupancy x CUs, looked up once per device and instance), each wave
+// walking its units grid-stride.
+template <int XDT, int BITS, int CPL, int ES, int XF>
+void launch_stage2_plan(const MoEArgs &a, int units, hipStream_t s) {
+    static std::atomic<int> resident[64];
+    constexpr int waves = kThreads12 / kWave;
+    int blocks = min(kStage2Blocks, (units + waves - 1) / waves), dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+        int r = resident[dev].load(std::memory_order_acquire);
+        if (r == 0) {
+            int cus = 0, occ = 0;
+            if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, moe_stage2<XDT, BITS, CPL, ES, XF>, kThreads12,
+                                                             0) == hipSuccess)
+                r = cus * occ;
+            r = r > 0 ? r : -1;
+            resident[dev].store(r, std::memory_order_release);
+        }
+        if (r > 0) blocks = min(r, (units + waves - 1) / waves);
+    }
+    hipLaunchKernelGGL((moe_stage2<XDT, BITS, CPL, ES, XF>), dim3(blocks), dim3(kThreads12), 0, s, a);
+}
+
+template <int XDT, int ES>
+void launch_stage2_es(const MoEArgs &a, int units, hipStream_t s) {
+    if constexpr (XDT == SWQ_BF16) {
+        if (a.gate.bits == 4) launch_stage2_plan<XDT, 4, 2, ES, kXBF16>(a, units, s);
+        else if (a.gate.cpl == 1) launch_stage2_plan<XDT, 8, 1, ES, kXF32>(a, units, s);
+        else launch_stage2_plan<XDT, 8, 2, ES, kXF32>(a, units, s);
+    } else {
+        if (a.gate.bits == 4) launch_stage2_plan<XDT, 4, 1, ES, kXF32>(a, units, s);
+        else if (a.gate.cpl == 1) launch_stage2_plan<XDT, 8, 1, ES, kXF32>(a, units, s);
+        else launch_stage2_plan<XDT, 8, 2, ES, kXF32>(a, units, s);
+    }
+}
+
+template <int XDT>
+void launch_stage2(const MoEArgs &a, int units, hipStream_t s) {
+    if (a.gate.stype == SWQ_F32) launch_stage2_es<XDT, 4>(a, units, s);
+    else launch_stage2_es<XDT, 2>(a, units, s);
 }
 
 constexpr int kStage3MaxWaves = 8;
@@ -826,10 +884,9 @@ static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtyp
     const int P = batch * a.K;
     const int max_slots = min(P, a.E);
     const int tps2 = (a.I + tile_rows(a.gate) - 1) / tile_rows(a.gate);
-    const dim3 grid2(min(kStage2Blocks, (max_slots * tps2 + waves12 - 1) / waves12));
     if (stage_mask & 2) {
-        if (x_dtype == SWQ_BF16) hipLaunchKernelGGL(moe_stage2<SWQ_BF16>, grid2, dim3(kThreads12), 0, s, a);
-        else hipLaunchKernelGGL(moe_stage2<SWQ_F32>, grid2, dim3(kThreads12), 0, s, a);
+        if (x_dtype == SWQ_BF16) launch_stage2<SWQ_BF16>(a, max_slots * tps2, s);
+        else launch_stage2<SWQ_F32>(a, max_slots * tps2, s);
         if ((st = launch_status()) != SWQ_OK) return st;
     }
     if (stage_mask & 4) {
