@@ -73,7 +73,6 @@ constexpr int kThreads12 = 256;
 constexpr int kMaxPairs = SWQ_MAX_BATCH * SWQ_MAX_TOPK;
 constexpr int kRows3 = 16;  // stage-3 rows per workgroup (upper bound)
 constexpr int kStage2Blocks = 256;  // stage-2 workgroups at most: one per CU (one wave per SIMD)
-constexpr int kHeld3 = 2;           // stage-3 slots in flight per wave
 
 struct MoEArgs {
     QMat router, gate, up, down, sh_gate, sh_up, sh_down, seg;
@@ -260,9 +259,9 @@ __device__ __forceinline__ void down_tile_row(const QMat &m, const LaneMap &lm, 
 
 // Stage 3's routed slots for one wave: slots s = s0, s0 + ds, ... below nu,
 // each one down tile (rows [r0, r0 + rows3)) against every pair of the slot,
-// results to part[p][row - r0].  kHeld3 slots' tiles and first activation
+// results to part[p][row - r0].  HELD slots' tiles and first activation
 // rows are in flight at once.
-template <int XDT, int BITS, int CPL, int ES, int XF>
+template <int XDT, int BITS, int CPL, int ES, int XF, int HELD = 2>
 __device__ __forceinline__ void down_slots(const MoEArgs &a, const Slots &sl, int s0, int ds, int nu, int r0,
                                            float (*part)[kRows3], int lane) {
     static_assert(XDT == SWQ_F32 && CPL == 1, "down rows read fp32 activations, one chunk per lane");
@@ -286,23 +285,23 @@ __device__ __forceinline__ void down_slots(const MoEArgs &a, const Slots &sl, in
             down_tile_row<BITS, ES, XF>(a.down, lm, t, xo, r0, end, part[p]);
         }
     };
-    // a ring of kHeld3 slots in flight: slot j of each round reuses the
+    // a ring of HELD slots in flight: slot j of each round reuses the
     // buffers of slot j of the previous round
-    Tile t[kHeld3];
-    Raw x[kHeld3];
+    Tile t[HELD];
+    Raw x[HELD];
 #pragma unroll
-    for (int j = 0; j < kHeld3; ++j)
+    for (int j = 0; j < HELD; ++j)
         if (s0 + ds * j < nu) issue(t[j], x[j], s0 + ds * j);
     [[maybe_unused]] int k = 2;
-    for (int base = 0; s0 + ds * base < nu; base += kHeld3) {
+    for (int base = 0; s0 + ds * base < nu; base += HELD) {
 #pragma unroll
-        for (int j = 0; j < kHeld3; ++j) {
+        for (int j = 0; j < HELD; ++j) {
             const int sj = s0 + ds * (base + j);
             if (sj < nu) {
                 run(t[j], x[j], sj);
                 STAGE_STAMP(k);
                 ++k;
-                if (sj + ds * kHeld3 < nu) issue(t[j], x[j], sj + ds * kHeld3);
+                if (sj + ds * HELD < nu) issue(t[j], x[j], sj + ds * HELD);
             }
         }
     }
@@ -664,9 +663,14 @@ void launch_stage2(const MoEArgs &a, int units, hipStream_t s) {
     else launch_stage2_es<XDT, 2>(a, units, s);
 }
 
-constexpr int kStage3MaxWaves = 8;
-
-__global__ __launch_bounds__(kStage3MaxWaves * 64) void moe_stage3(MoEArgs a) {
+// One instance per plan of the routed down matrix, at most WAVES waves of
+// HELD slots in flight each.  SAME_SH: the shared expert's down matrix has
+// the routed one's plan (else it is dispatched on its own plan inside).
+// 8-bit rows with the shared expert on their plan fit sixteen waves (four
+// per SIMD) of one slot each; the rest take eight waves of two.
+template <int BITS, int ES, int XF, int WAVES, int HELD, bool SAME_SH>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVES / 4))) void moe_stage3(
+    MoEArgs a) {
     __shared__ float part[kMaxPairs + SWQ_MAX_BATCH][kRows3];
     __shared__ float s_w[kMaxPairs];
     __shared__ float s_gate[SWQ_MAX_BATCH];
@@ -680,8 +684,8 @@ __global__ __launch_bounds__(kStage3MaxWaves * 64) void moe_stage3(MoEArgs a) {
     load_slots(a, sl);
     // combine weights and shared-gate logits: loaded into registers now,
     // staged in LDS only after the projections, so their latency overlaps.
-    // one weight per lane: the host sizes the block 64 * min(8, min(P, E) +
-    // shared) lanes, which is 512 >= P = B*K <= 256, or >= 64 * P, or
+    // one weight per lane: the host sizes the block 64 * min(WAVES, min(P, E)
+    // + shared) lanes, which is >= 512 >= P = B*K <= 256, or >= 64 * P, or
     // >= 64 * E >= 16 * K >= P (and checks P <= blockDim)
     const float w_pre = threadIdx.x < static_cast<unsigned>(P) ? a.wts[threadIdx.x] : 0.f;
     const float sg_pre = (a.has_shared && threadIdx.x < static_cast<unsigned>(a.B)) ? a.sg[threadIdx.x] : 0.f;
@@ -692,10 +696,11 @@ __global__ __launch_bounds__(kStage3MaxWaves * 64) void moe_stage3(MoEArgs a) {
     // the shared expert's tile on the wave with the fewest routed slots
     // (first, so its loads start with the others'), then the routed slots
     if (a.has_shared && wave == sl.n % nw) {
-        SWQ_DISPATCH_DOWN(a.sh_down, down_shared, a, r0, part, lane);
+        if constexpr (SAME_SH) down_shared<SWQ_F32, BITS, 1, ES, XF>(a, r0, part, lane);
+        else SWQ_DISPATCH_DOWN(a.sh_down, down_shared, a, r0, part, lane);
         STAGE_STAMP(13);
     }
-    SWQ_DISPATCH_DOWN(a.down, down_slots, a, sl, wave, nw, sl.n, r0, part, lane);
+    down_slots<SWQ_F32, BITS, 1, ES, XF, HELD>(a, sl, wave, nw, sl.n, r0, part, lane);
     STAGE_STAMP(14);
     if (threadIdx.x < static_cast<unsigned>(P)) s_w[threadIdx.x] = w_pre;
     if (a.has_shared && threadIdx.x < static_cast<unsigned>(a.B)) s_gate[threadIdx.x] = sigmoidf_ref(sg_pre);
@@ -890,9 +895,21 @@ static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtyp
         if ((st = launch_status()) != SWQ_OK) return st;
     }
     if (stage_mask & 4) {
-        const int nw3 = min(kStage3MaxWaves, max_slots + a.has_shared);
+        const bool same_sh = !a.has_shared || (a.sh_down.bits == a.down.bits && a.sh_down.stype == a.down.stype);
+        const bool wide = a.down.bits == 8 && same_sh;
+        const int nw3 = min(wide ? 16 : 8, max_slots + a.has_shared);
         if (P > nw3 * kWave) return SWQ_ERR_LIMIT;  // one combine weight per lane
-        hipLaunchKernelGGL(moe_stage3, dim3((H + a.rows3 - 1) / a.rows3), dim3(nw3 * kWave), 0, s, a);
+        const dim3 g3((H + a.rows3 - 1) / a.rows3), b3(nw3 * kWave);
+        if (wide) {
+            if (a.down.stype == SWQ_F32) hipLaunchKernelGGL((moe_stage3<8, 4, kXF32, 16, 1, true>), g3, b3, 0, s, a);
+            else hipLaunchKernelGGL((moe_stage3<8, 2, kXF32, 16, 1, true>), g3, b3, 0, s, a);
+        } else if (a.down.stype == SWQ_F32) {
+            if (a.down.bits == 4) hipLaunchKernelGGL((moe_stage3<4, 4, kXBF16X2, 8, 2, false>), g3, b3, 0, s, a);
+            else hipLaunchKernelGGL((moe_stage3<8, 4, kXF32, 8, 2, false>), g3, b3, 0, s, a);
+        } else {
+            if (a.down.bits == 4) hipLaunchKernelGGL((moe_stage3<4, 2, kXBF16X2, 8, 2, false>), g3, b3, 0, s, a);
+            else hipLaunchKernelGGL((moe_stage3<8, 2, kXF32, 8, 2, false>), g3, b3, 0, s, a);
+        }
         if ((st = launch_status()) != SWQ_OK) return st;
     }
     return SWQ_OK;
