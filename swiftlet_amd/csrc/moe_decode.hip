@@ -29,16 +29,17 @@
 // builds only): s_memrealtime per (workgroup, wave, point) into LDS, copied
 // to a global array at the end of the kernel.
 #ifdef SWQ_FUSED_TRACE
-static __device__ unsigned long long g_swq_stage_trace[1024 * 8 * 16];
+constexpr int kTraceWaves = 16;  // waves per workgroup the stamps cover
+static __device__ unsigned long long g_swq_stage_trace[1024 * kTraceWaves * 16];
 extern "C" int swq_stage_trace(void *host, size_t bytes, int clear) {
     if (clear) {
-        static unsigned long long z[1024 * 8 * 16];
+        static unsigned long long z[1024 * kTraceWaves * 16];
         return hipMemcpyToSymbol(HIP_SYMBOL(g_swq_stage_trace), z, sizeof(z)) == hipSuccess ? 0 : -1;
     }
     return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_swq_stage_trace), bytes) == hipSuccess ? 0 : -1;
 }
 __device__ __forceinline__ unsigned long long *stage_trace_lds() {
-    __shared__ unsigned long long t[8 * 16];
+    __shared__ unsigned long long t[kTraceWaves * 16];
     return t;
 }
 #define STAGE_TRACE_DECL                                                                                \
@@ -51,8 +52,8 @@ __device__ __forceinline__ unsigned long long *stage_trace_lds() {
 #define STAGE_TRACE_FLUSH(base)                                                                         \
     do {                                                                                                \
         __syncthreads();                                                                                \
-        for (int i_ = threadIdx.x; i_ < 8 * 16; i_ += blockDim.x)                                       \
-            g_swq_stage_trace[((base) + blockIdx.x) * 128 + i_] =                                       \
+        for (int i_ = threadIdx.x; i_ < kTraceWaves * 16; i_ += blockDim.x)                             \
+            g_swq_stage_trace[((base) + blockIdx.x) * (kTraceWaves * 16) + i_] =                        \
                 i_ < static_cast<int>(blockDim.x >> 6) * 16 ? stage_trace_lds()[i_] : 0ull;             \
     } while (0)
 #else
@@ -257,26 +258,40 @@ __device__ __forceinline__ void down_tile_row(const QMat &m, const LaneMap &lm, 
 }
 
 
-// Stage 3's routed slots for one wave: slots s = s0, s0 + ds, ... below nu,
-// each one down tile (rows [r0, r0 + rows3)) against every pair of the slot,
+// Stage 3's slots for one wave: slots s = s0, s0 + ds, ... below nu, each
+// one down tile (rows [r0, r0 + rows3)) against every pair of the slot,
 // results to part[p][row - r0].  HELD slots' tiles and first activation
-// rows are in flight at once.
-template <int XDT, int BITS, int CPL, int ES, int XF, int HELD = 2>
+// rows are in flight at once.  SH (the shared expert's down matrix on the
+// routed plan): slots 0 .. B-1 are the shared expert's tile against token
+// s's activations (results to part[B*K + s]), then the routed slots.
+template <int XDT, int BITS, int CPL, int ES, int XF, int HELD = 2, bool SH = false>
 __device__ __forceinline__ void down_slots(const MoEArgs &a, const Slots &sl, int s0, int ds, int nu, int r0,
                                            float (*part)[kRows3], int lane) {
     static_assert(XDT == SWQ_F32 && CPL == 1, "down rows read fp32 activations, one chunk per lane");
+    const int nsh = SH && a.has_shared ? a.B : 0;
+    nu += nsh;
     if (s0 >= nu) return;
     const LaneMap lm = lane_map(a.down.lpr_log2, lane);
     const int end = min(r0 + a.rows3, a.H);
     using Tile = RowTile<BITS, 1, ES>;
     using Raw = XRaw<SWQ_F32, BITS, 1>;
     auto first_pair = [&](int s) { return static_cast<int>(sl.pairs[s * a.B]); };
+    // one code path for both kinds of slot: the matrix, expert, activation
+    // row and result row selected (wave-uniform)
     auto issue = [&](Tile &t, Raw &xr, int s) __attribute__((always_inline)) {
-        load_tile(t, a.down, sl.e[s], lm, r0, end);
-        load_xraw<SWQ_F32>(xr, a.down, lm, a.h, static_cast<int64_t>(first_pair(s)) * a.I);
+        const bool sh = SH && s < nsh;
+        const int su = s - nsh;
+        const QMat &m = sh ? a.sh_down : a.down;
+        load_tile(t, m, sh ? 0 : sl.e[su], lm, r0, end);
+        load_xraw<SWQ_F32>(xr, m, lm, sh ? a.h_sh : a.h,
+                           sh ? static_cast<int64_t>(s) * a.Is : static_cast<int64_t>(first_pair(su)) * a.I);
     };
     auto run = [&](const Tile &t, const Raw &xr, int s) __attribute__((always_inline)) {
-        down_tile_row<BITS, ES, XF>(a.down, lm, t, xr, r0, end, part[first_pair(s)]);
+        const bool sh = SH && s < nsh;
+        s -= nsh;
+        down_tile_row<BITS, ES, XF>(sh ? a.sh_down : a.down, lm, t, xr, r0, end,
+                                    part[sh ? a.B * a.K + s + nsh : first_pair(s)]);
+        if (sh) return;
         const int np = sl.np[s];
         for (int pi = 1; pi < np; ++pi) {
             const int p = sl.pairs[s * a.B + pi];
@@ -665,9 +680,10 @@ void launch_stage2(const MoEArgs &a, int units, hipStream_t s) {
 
 // One instance per plan of the routed down matrix, at most WAVES waves of
 // HELD slots in flight each.  SAME_SH: the shared expert's down matrix has
-// the routed one's plan (else it is dispatched on its own plan inside).
-// 8-bit rows with the shared expert on their plan fit sixteen waves (four
-// per SIMD) of one slot each; the rest take eight waves of two.
+// the routed one's plan, and its tile joins the slots once per token (else
+// one wave runs it on its own plan for every token, before its routed
+// slots).  8-bit rows with the shared expert on their plan fit sixteen
+// waves (four per SIMD) of one slot each; the rest take eight waves of two.
 template <int BITS, int ES, int XF, int WAVES, int HELD, bool SAME_SH>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVES / 4))) void moe_stage3(
     MoEArgs a) {
@@ -689,18 +705,17 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVE
     // >= 64 * E >= 16 * K >= P (and checks P <= blockDim)
     const float w_pre = threadIdx.x < static_cast<unsigned>(P) ? a.wts[threadIdx.x] : 0.f;
     const float sg_pre = (a.has_shared && threadIdx.x < static_cast<unsigned>(a.B)) ? a.sg[threadIdx.x] : 0.f;
-    // routed slots on every wave, the shared expert's on the wave with the
-    // fewest routed ones (first, so its loads start with the others')
     __syncthreads();  // sl
     STAGE_STAMP(1);
-    // the shared expert's tile on the wave with the fewest routed slots
-    // (first, so its loads start with the others'), then the routed slots
-    if (a.has_shared && wave == sl.n % nw) {
-        if constexpr (SAME_SH) down_shared<SWQ_F32, BITS, 1, ES, XF>(a, r0, part, lane);
-        else SWQ_DISPATCH_DOWN(a.sh_down, down_shared, a, r0, part, lane);
-        STAGE_STAMP(13);
+    // without SAME_SH: the shared expert's tile on the wave with the fewest
+    // routed slots (first, so its loads start with the others')
+    if constexpr (!SAME_SH) {
+        if (a.has_shared && wave == sl.n % nw) {
+            SWQ_DISPATCH_DOWN(a.sh_down, down_shared, a, r0, part, lane);
+            STAGE_STAMP(13);
+        }
     }
-    down_slots<SWQ_F32, BITS, 1, ES, XF, HELD>(a, sl, wave, nw, sl.n, r0, part, lane);
+    down_slots<SWQ_F32, BITS, 1, ES, XF, HELD, SAME_SH>(a, sl, wave, nw, sl.n, r0, part, lane);
     STAGE_STAMP(14);
     if (threadIdx.x < static_cast<unsigned>(P)) s_w[threadIdx.x] = w_pre;
     if (a.has_shared && threadIdx.x < static_cast<unsigned>(a.B)) s_gate[threadIdx.x] = sigmoidf_ref(sg_pre);
@@ -895,14 +910,22 @@ static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtyp
         if ((st = launch_status()) != SWQ_OK) return st;
     }
     if (stage_mask & 4) {
-        const bool same_sh = !a.has_shared || (a.sh_down.bits == a.down.bits && a.sh_down.stype == a.down.stype);
+        // the shared expert's down matrix on the routed plan (same lane map and tile rows)
+        const bool same_sh = !a.has_shared ||
+                             (a.sh_down.bits == a.down.bits && a.sh_down.stype == a.down.stype &&
+                              a.sh_down.xf == a.down.xf && a.sh_down.cpl == a.down.cpl &&
+                              a.sh_down.lpr_log2 == a.down.lpr_log2);
         const bool wide = a.down.bits == 8 && same_sh;
-        const int nw3 = min(wide ? 16 : 8, max_slots + a.has_shared);
+        const int slots3 = max_slots + (same_sh ? batch : 1) * a.has_shared;
+        const int nw3 = min(wide ? 16 : 8, slots3);
         if (P > nw3 * kWave) return SWQ_ERR_LIMIT;  // one combine weight per lane
         const dim3 g3((H + a.rows3 - 1) / a.rows3), b3(nw3 * kWave);
         if (wide) {
             if (a.down.stype == SWQ_F32) hipLaunchKernelGGL((moe_stage3<8, 4, kXF32, 16, 1, true>), g3, b3, 0, s, a);
             else hipLaunchKernelGGL((moe_stage3<8, 2, kXF32, 16, 1, true>), g3, b3, 0, s, a);
+        } else if (same_sh && a.down.bits == 4) {
+            if (a.down.stype == SWQ_F32) hipLaunchKernelGGL((moe_stage3<4, 4, kXBF16X2, 8, 2, true>), g3, b3, 0, s, a);
+            else hipLaunchKernelGGL((moe_stage3<4, 2, kXBF16X2, 8, 2, true>), g3, b3, 0, s, a);
         } else if (a.down.stype == SWQ_F32) {
             if (a.down.bits == 4) hipLaunchKernelGGL((moe_stage3<4, 4, kXBF16X2, 8, 2, false>), g3, b3, 0, s, a);
             else hipLaunchKernelGGL((moe_stage3<8, 4, kXF32, 8, 2, false>), g3, b3, 0, s, a);
