@@ -339,6 +339,29 @@ __device__ __forceinline__ void fetch_acts(const uint64_t *src, int p0, int p1, 
     }
 }
 
+// Pairs [p0, p1) of the words at src into buf and [s0, s1) of those at ssrc
+// into sbuf, each at most a wave's 64, polled together in one round per
+// lane (the second set is ready earlier: it rides the first's wait).
+template <int DB>
+__device__ __forceinline__ void fetch_acts_with(const uint64_t *src, int p0, int p1, uint32_t *buf,
+                                                const uint64_t *ssrc, int s0, int s1, uint32_t *sbuf, uint32_t g,
+                                                int lane, uint32_t *err) {
+    const uint64_t *pp[4];
+    bool live[4];
+    const int pr = p0 + lane, sr = s0 + lane;
+    live[0] = live[1] = pr < p1;
+    live[2] = live[3] = sr < s1;
+    const int pc = min(pr, max(p1 - 1, p0)), sc = min(sr, max(s1 - 1, s0));
+    pp[0] = src + pair_first<DB>(pc);
+    pp[1] = src + pair_second<DB>(pc);
+    pp[2] = ssrc + pair_first<DB>(sc);
+    pp[3] = ssrc + pair_second<DB>(sc);
+    float v[4];
+    poll_words<4>(pp, live, g, v, err, 1u);
+    if (live[0]) store_pair_lds<DB>(buf, pr, v[0], v[1]);
+    if (live[2]) store_pair_lds<DB>(sbuf, sr, v[2], v[3]);
+}
+
 // Dot products of a down tile with the activations in LDS.
 template <int DB, int DRI>
 __device__ __forceinline__ void down_dot(float (&res)[DRI], const RowTile<DB, 1, 2, DRI> &dt, const QMat &m,
@@ -569,6 +592,13 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     }
 
     // ---- routed slots of the group -------------------------------------------
+    // When a wave's shares of a slot's and of the shared expert's activation
+    // pairs each fit one polling round, the group's first slot fetches the
+    // shared expert's along with its own (they were written in phase A), so
+    // the tail's shared down rows need no fetch of their own.
+    const int np_r = a.I / 2, q_r = (np_r + kFusedWaves - 1) / kFusedWaves;
+    const int np_s = a.Is / 2, q_s = (np_s + kFusedWaves - 1) / kFusedWaves;
+    const bool sh_early = sh_rows && grp < a.K && q_r <= kWave && q_s <= kWave;
     asm volatile("" : "+v"(lane));
     {
         const LaneMap lmd = lane_map(a.down.lpr_log2, lane);
@@ -606,9 +636,13 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
             // would start only once the activations are in.
             asm volatile("" ::: "memory");
             // the slot's activations: each wave polls an eighth into LDS
-            const int np = a.I / 2, q = (np + kFusedWaves - 1) / kFusedWaves;
-            fetch_acts<DB>(a.h_x + static_cast<int64_t>(s) * a.I, min(np, wave * q), min(np, (wave + 1) * q), g,
-                           s_hb, lane, a.err);
+            if (sh_early && s == grp)
+                fetch_acts_with<DB>(a.h_x + static_cast<int64_t>(s) * a.I, min(np_r, wave * q_r),
+                                    min(np_r, (wave + 1) * q_r), s_hb, a.hsh_x, min(np_s, wave * q_s),
+                                    min(np_s, (wave + 1) * q_s), s_hsh, g, lane, a.err);
+            else
+                fetch_acts<DB>(a.h_x + static_cast<int64_t>(s) * a.I, min(np_r, wave * q_r),
+                               min(np_r, (wave + 1) * q_r), g, s_hb, lane, a.err);
             __syncthreads();
             SWQ_STAMP(5);
             for (int t = t0; t < a.dn_tpe; t += NPG * kFusedWaves) {
@@ -661,21 +695,24 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
         }
         SWQ_STAMP(8);
     } else if (sh_rows) {
-        // a share of the shared activations -> LDS, then, once every
-        // wave's share is in, this wave's passes of the shared down rows
-        const int np = a.Is / 2, q3 = (np + kFusedWaves - 2) / (kFusedWaves - 1);
-        fetch_acts<DB>(a.hsh_x, min(np, sp0 * q3), min(np, (sp0 + 1) * q3), g, s_hsh, lane, a.err);
-        SWQ_STAMP(12);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        if (lane == 0) __hip_atomic_fetch_add(&s_arrive, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        for (uint32_t it = 0; __hip_atomic_load(&s_arrive, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
-                              kFusedWaves - 1;
-             ++it) {
-            if (it > kSpinLimit) {
-                if (lane == 0) record_stall(a.err, 16u);
-                break;
+        // (unless the first slot brought them) a share of the shared
+        // activations -> LDS, then, once every wave's share is in, this
+        // wave's passes of the shared down rows
+        if (!sh_early) {
+            const int q3 = (np_s + kFusedWaves - 2) / (kFusedWaves - 1);
+            fetch_acts<DB>(a.hsh_x, min(np_s, sp0 * q3), min(np_s, (sp0 + 1) * q3), g, s_hsh, lane, a.err);
+            SWQ_STAMP(12);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane == 0) __hip_atomic_fetch_add(&s_arrive, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            for (uint32_t it = 0; __hip_atomic_load(&s_arrive, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+                                  kFusedWaves - 1;
+                 ++it) {
+                if (it > kSpinLimit) {
+                    if (lane == 0) record_stall(a.err, 16u);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
             }
-            __builtin_amdgcn_s_sleep(1);
         }
         for (int sp = sp0; sp < sh_passes; sp += kFusedWaves - 1) {
             const int row0 = r0 + sp * lms.rpw;
