@@ -659,7 +659,9 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
                 }
             }
             SWQ_STAMP(6);
-            __syncthreads();  // s_hb is rewritten by the next slot
+            // s_hb is rewritten by the next slot; after the group's last one
+            // each wave goes on to the tail as soon as its own rows are done
+            if (s + kGroups < a.K) __syncthreads();
         }
     }
     // ---- wave 0: the remaining picks, the weights, this workgroup's rows of
