@@ -44,7 +44,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 # 48 distinct layers cycled;
 # the runs' commands and raw counts are kept with the kernel-trace summaries.  Keyed (workload, kernel).
 MEASURED_TRAFFIC = {
-    ("qwen3.6-35b-a3b-q4-b1", "moe_fused"): 17_650_148,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_fused"): 17_652_196,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_743_050,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 9_690_265,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 5_705_215,
