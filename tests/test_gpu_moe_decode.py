@@ -255,3 +255,43 @@ def test_fused_declines_batches():
     with pytest.raises(_lib.SwqError) as e:
         gpu.decode(x, path="fused")
     assert e.value.code == _lib.SWQ_ERR_LIMIT
+
+
+# ---------------------------------------------------------------------------
+# f32 scales and biases (exact widenings of the fp16 ones): the kernels
+# compiled for 4-byte scale elements give the fp16 layer's results bit for
+# bit (the single launch takes fp16/bf16 scales only: the three launches)
+
+def _widen_scales(lin):
+    import torch
+    from swiftlet_amd import _lib
+    from swiftlet_amd.engine import GPULinear
+    s = lin.scales.view(torch.float16).float().contiguous().view(torch.uint8)
+    b = lin.biases.view(torch.float16).float().contiguous().view(torch.uint8)
+    return GPULinear(lin.w, s, b, lin.out_dim, lin.in_dim, lin.group_size, lin.bits, _lib.SWQ_F32,
+                     expert_stride_w=lin.expert_stride_w, expert_stride_sb=2 * lin.expert_stride_sb,
+                     num_experts=lin.num_experts)
+
+
+@pytest.mark.parametrize("name,batch", [
+    ("qwen3.6-35b-a3b-q4", 1),
+    ("qwen3.6-35b-a3b-q4", 4),
+    ("qwen3.6-35b-a3b-q8", 4),
+])
+def test_f32_scales_equal_f16_scales(name, batch):
+    import torch
+    print(f"f32 scales vs f16: {name} batch {batch}", flush=True)
+    shape = synth.SHAPES[name]
+    a = moe.synth_layer(shape, helpers.SEED, 0)
+    w = lambda lin: _widen_scales(lin) if lin is not None else None
+    b = moe.MoELayerGPU(router=w(a.router), gate=w(a.gate), up=w(a.up), down=w(a.down),
+                        shared_gate=w(a.shared_gate), shared_up=w(a.shared_up), shared_down=w(a.shared_down),
+                        shared_expert_gate=w(a.shared_expert_gate), top_k=a.top_k,
+                        norm_topk_prob=a.norm_topk_prob)
+    x = helpers.bf16_bits_to_torch(synth.activations_bf16(helpers.SEED + 91, batch, shape.hidden))
+    wa, wb = a.new_workspace(batch), b.new_workspace(batch)
+    oa, ia, ka = a.decode(x, ws=wa, path="staged")
+    ob, ib, kb = b.decode(x, ws=wb, path="staged")
+    torch.cuda.synchronize()
+    assert a.workspace_error(wa, batch) == 0 and b.workspace_error(wb, batch) == 0
+    assert torch.equal(ia, ib) and torch.equal(ka, kb) and torch.equal(oa, ob)
