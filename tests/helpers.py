@@ -91,3 +91,25 @@ def bf16_bits_to_torch(bits: np.ndarray, device="cuda"):
 def torch_bf16_to_bits(t) -> np.ndarray:
     import torch
     return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def widen_scales(lin):
+    """The GPULinear with its fp16 scales and biases widened to f32 (exact)."""
+    import torch
+    from swiftlet_amd import _lib
+    from swiftlet_amd.engine import GPULinear
+    s = lin.scales.view(torch.float16).float().contiguous().view(torch.uint8)
+    b = lin.biases.view(torch.float16).float().contiguous().view(torch.uint8)
+    return GPULinear(lin.w, s, b, lin.out_dim, lin.in_dim, lin.group_size, lin.bits, _lib.SWQ_F32,
+                     expert_stride_w=lin.expert_stride_w, expert_stride_sb=2 * lin.expert_stride_sb,
+                     num_experts=lin.num_experts)
+
+
+def widen_layer(layer):
+    """The MoE layer with every matrix's scales and biases widened to f32."""
+    from swiftlet_amd import moe
+    w = lambda lin: widen_scales(lin) if lin is not None else None
+    return moe.MoELayerGPU(router=w(layer.router), gate=w(layer.gate), up=w(layer.up), down=w(layer.down),
+                           shared_gate=w(layer.shared_gate), shared_up=w(layer.shared_up),
+                           shared_down=w(layer.shared_down), shared_expert_gate=w(layer.shared_expert_gate),
+                           top_k=layer.top_k, norm_topk_prob=layer.norm_topk_prob)

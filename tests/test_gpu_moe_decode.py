@@ -262,17 +262,6 @@ def test_fused_declines_batches():
 # compiled for 4-byte scale elements give the fp16 layer's results bit for
 # bit (the single launch takes fp16/bf16 scales only: the three launches)
 
-def _widen_scales(lin):
-    import torch
-    from swiftlet_amd import _lib
-    from swiftlet_amd.engine import GPULinear
-    s = lin.scales.view(torch.float16).float().contiguous().view(torch.uint8)
-    b = lin.biases.view(torch.float16).float().contiguous().view(torch.uint8)
-    return GPULinear(lin.w, s, b, lin.out_dim, lin.in_dim, lin.group_size, lin.bits, _lib.SWQ_F32,
-                     expert_stride_w=lin.expert_stride_w, expert_stride_sb=2 * lin.expert_stride_sb,
-                     num_experts=lin.num_experts)
-
-
 @pytest.mark.parametrize("name,batch", [
     ("qwen3.6-35b-a3b-q4", 1),
     ("qwen3.6-35b-a3b-q4", 4),
@@ -283,11 +272,7 @@ def test_f32_scales_equal_f16_scales(name, batch):
     print(f"f32 scales vs f16: {name} batch {batch}", flush=True)
     shape = synth.SHAPES[name]
     a = moe.synth_layer(shape, helpers.SEED, 0)
-    w = lambda lin: _widen_scales(lin) if lin is not None else None
-    b = moe.MoELayerGPU(router=w(a.router), gate=w(a.gate), up=w(a.up), down=w(a.down),
-                        shared_gate=w(a.shared_gate), shared_up=w(a.shared_up), shared_down=w(a.shared_down),
-                        shared_expert_gate=w(a.shared_expert_gate), top_k=a.top_k,
-                        norm_topk_prob=a.norm_topk_prob)
+    b = helpers.widen_layer(a)
     x = helpers.bf16_bits_to_torch(synth.activations_bf16(helpers.SEED + 91, batch, shape.hidden))
     wa, wb = a.new_workspace(batch), b.new_workspace(batch)
     oa, ia, ka = a.decode(x, ws=wa, path="staged")

@@ -206,3 +206,24 @@ def test_prefill_single_token_and_workspace_reuse():
         torch.cuda.synchronize()
         assert torch.equal(out, fresh) and torch.equal(ids, ids_f) and torch.equal(w, w_f), T
     _check(shape, xf, out, ids.cpu().numpy(), w.cpu().numpy())
+
+
+@pytest.mark.parametrize("name,x_dtype", [
+    ("qwen3.6-35b-a3b-q4", "bf16"),
+    ("qwen3.6-35b-a3b-q4", "f32"),
+    ("qwen3.6-35b-a3b-q8", "bf16"),
+])
+def test_prefill_f32_scales_equal_f16_scales(name, x_dtype):
+    """f32 scales and biases (exact widenings of the fp16 ones) take the
+    GEMMs' 4-byte-scale kernels: the same outputs, ids and weights bit for
+    bit as the fp16 layer."""
+    import torch
+    print(f"prefill f32 scales vs f16: {name} x {x_dtype}", flush=True)
+    shape = synth.SHAPES[name]
+    a = moe.synth_layer(shape, helpers.SEED, 0)
+    b = helpers.widen_layer(a)
+    x, _ = _x(4242, 40, shape.hidden, x_dtype)
+    oa, ia, wa = a.prefill(x)
+    ob, ib, wb = b.prefill(x)
+    torch.cuda.synchronize()
+    assert torch.equal(ia, ib) and torch.equal(wa, wb) and torch.equal(oa, ob)
