@@ -95,7 +95,7 @@ struct MoEArgs {
     int32_t xdt, odt, accumulate;
     int32_t B, H, E, K, I, Is, norm, has_shared;
     int32_t nr_blocks;     // stage-1 workgroups holding router rows
-    int32_t router_tasks;  // waves with router rows
+    int32_t router_tasks;  // router row tiles (one wave each per token)
     int32_t shared_tasks;  // waves with shared gate/up rows
     int32_t rows3;         // stage-3 rows per workgroup
 };
@@ -470,6 +470,9 @@ __device__ __forceinline__ uint32_t touch_share(const QMat &m, int64_t expert, i
 __device__ __forceinline__ void keep(uint32_t v) { asm volatile("" ::"v"(v)); }
 
 
+// Tokens per stage-1 router wave.
+constexpr int kRouterTokens = 2;
+
 template <int XDT>
 __global__ __launch_bounds__(kThreads12) void moe_stage1(MoEArgs a) {
     __shared__ Routing r;
@@ -477,9 +480,18 @@ __global__ __launch_bounds__(kThreads12) void moe_stage1(MoEArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int task = blockIdx.x * (kThreads12 / kWave) + wave;
     if (static_cast<int>(blockIdx.x) < a.nr_blocks) {
-        if (task < a.router_tasks)
-            SWQ_DISPATCH(XDT, a.router, gemv_rows_tokens, a.router, task * tile_rows(a.router), a.E, a.x,
-                         a.H, a.B, a.logits, a.E, lane);
+        // one (row tile, kRouterTokens tokens) per wave, the waves of a tile
+        // side by side: the router's dot products are VALU work, spread over
+        // more waves, while the tile's codes come from memory once and then
+        // from cache
+        const int groups = (a.B + kRouterTokens - 1) / kRouterTokens;
+        if (task < a.router_tasks * groups) {
+            const int tile = task / groups, b0 = (task - tile * groups) * kRouterTokens;
+            const void *xb =
+                static_cast<const uint8_t *>(a.x) + static_cast<int64_t>(b0) * a.H * (XDT == SWQ_BF16 ? 2 : 4);
+            SWQ_DISPATCH(XDT, a.router, gemv_rows_tokens, a.router, tile * tile_rows(a.router), a.E, xb, a.H,
+                         min(kRouterTokens, a.B - b0), a.logits + static_cast<int64_t>(b0) * a.E, a.E, lane);
+        }
         // The last router workgroup to finish routes every token (softmax,
         // top-k, the distinct experts) and publishes the tables stage 2 and 3
         // read, while the shared-expert workgroups still run.  Release: this
@@ -876,7 +888,7 @@ static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtyp
     const int waves12 = kThreads12 / kWave;
     const int router_rows_per_task = tile_rows(a.router);
     a.router_tasks = (a.E + router_rows_per_task - 1) / router_rows_per_task;
-    a.nr_blocks = (a.router_tasks + waves12 - 1) / waves12;
+    a.nr_blocks = (a.router_tasks * ((batch + kRouterTokens - 1) / kRouterTokens) + waves12 - 1) / waves12;
     int shared_blocks = 0;
     if (a.has_shared) {
         const int sh_rows_per_task = tile_rows(a.sh_gate);
