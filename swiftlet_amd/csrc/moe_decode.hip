@@ -517,11 +517,17 @@ __global__ __launch_bounds__(kThreads12) void moe_stage1(MoEArgs a) {
     const int sb = blockIdx.x - a.nr_blocks;
     const uint32_t t = touch_share(a.sh_down, 0, sb, gridDim.x - a.nr_blocks);
     const int st = task - a.nr_blocks * (kThreads12 / kWave);
+    // the shared gate/up rows as the router's: one (row tile, kRouterTokens
+    // tokens) per wave
+    const int groups = (a.B + kRouterTokens - 1) / kRouterTokens;
     if (st == 0) {
         SWQ_DISPATCH(XDT, a.seg, gemv_rows_tokens, a.seg, 0, 1, a.x, a.H, a.B, a.sg, 1, lane);
-    } else if (st - 1 < a.shared_tasks) {
-        SWQ_DISPATCH(XDT, a.sh_gate, gateup_rows_tokens, a.sh_gate, a.sh_up, 0, (st - 1) * tile_rows(a.sh_gate),
-                     a.Is, a.x, a.H, a.B, a.h_sh, a.Is, lane);
+    } else if (st - 1 < a.shared_tasks * groups) {
+        const int tile = (st - 1) / groups, b0 = (st - 1 - tile * groups) * kRouterTokens;
+        const void *xb =
+            static_cast<const uint8_t *>(a.x) + static_cast<int64_t>(b0) * a.H * (XDT == SWQ_BF16 ? 2 : 4);
+        SWQ_DISPATCH(XDT, a.sh_gate, gateup_rows_tokens, a.sh_gate, a.sh_up, 0, tile * tile_rows(a.sh_gate), a.Is,
+                     xb, a.H, min(kRouterTokens, a.B - b0), a.h_sh + static_cast<int64_t>(b0) * a.Is, a.Is, lane);
     }
     keep(t);
 }
@@ -893,7 +899,8 @@ static int moe_decode_impl(const swq_moe_layer *layer, const void *x, int x_dtyp
     if (a.has_shared) {
         const int sh_rows_per_task = tile_rows(a.sh_gate);
         a.shared_tasks = (a.Is + sh_rows_per_task - 1) / sh_rows_per_task;
-        shared_blocks = (a.shared_tasks + 1 + waves12 - 1) / waves12;  // +1: shared gate row
+        // +1: shared gate row
+        shared_blocks = (a.shared_tasks * ((batch + kRouterTokens - 1) / kRouterTokens) + 1 + waves12 - 1) / waves12;
     }
     a.rows3 = min(kRows3, tile_rows(a.down));
 
