@@ -45,11 +45,11 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 # the runs' commands and raw counts are kept with the kernel-trace summaries.  Keyed (workload, kernel).
 MEASURED_TRAFFIC = {
     ("qwen3.6-35b-a3b-q4-b1", "moe_fused"): 17_652_196,
-    ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_743_050,
-    ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 9_690_265,
-    ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 5_705_215,
-    ("qwen3.6-35b-a3b-q8-b4", "moe_stage1"): 4_433_523,
-    ("qwen3.6-35b-a3b-q8-b4", "moe_stage2"): 69_521_300,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_757_384,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 9_698_457,
+    ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 5_713_406,
+    ("qwen3.6-35b-a3b-q8-b4", "moe_stage1"): 5_580_301,
+    ("qwen3.6-35b-a3b-q8-b4", "moe_stage2"): 69_525_396,
     ("qwen3.6-35b-a3b-q8-b4", "moe_stage3"): 36_430_644,
     ("qwen3.6-35b-a3b-q4-prefill512", "gate_up"): 347_003_996,
     ("qwen3.6-35b-a3b-q4-prefill512", "down"): 209_619_225,
