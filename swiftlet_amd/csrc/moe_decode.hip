@@ -496,16 +496,18 @@ __global__ __launch_bounds__(kThreads12) void moe_stage1(MoEArgs a) {
         // top-k, the distinct experts) and publishes the tables stage 2 and 3
         // read, while the shared-expert workgroups still run.  Release: this
         // workgroup's logits reach memory before its arrival counts; acquire:
-        // the last one sees every workgroup's logits.
+        // the last one sees every workgroup's logits.  Only the last one
+        // acquires: an agent-scope acquire invalidates the XCD's L2 under the
+        // other workgroups' loads (a full fence here cost ~1 us of stage 1).
         __syncthreads();
         if (threadIdx.x == 0) {
-            __threadfence();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
             const int32_t old = __hip_atomic_fetch_add(a.arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             s_last = old == a.nr_blocks - 1 ? 1 : 0;
         }
         __syncthreads();
         if (s_last) {
-            __threadfence();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             route(a, r, true);
             if (threadIdx.x == 0) __hip_atomic_store(a.arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
