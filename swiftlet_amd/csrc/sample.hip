@@ -258,12 +258,13 @@ __global__ __launch_bounds__(kSampleThreads) void sample_slices(const SampleArgs
     __syncthreads();
     // The list goes out from wave 0, the wave whose thread 0 then counts the
     // arrival: that agent-scope release waits for the wave's stores and
-    // writes them back past this XCD's L2; the last arrival's acquire (and
-    // the acquire fence every thread of that workgroup passes) makes every
-    // slice's list visible on whichever XCD that slice ran.
+    // writes them back past this XCD's L2; the acquire fence every thread of
+    // the last workgroup passes makes every slice's list visible on whichever
+    // XCD that slice ran.  The count itself only releases: an acquire
+    // invalidates the XCD's L2, which only the last workgroup needs.
     if (tid < a.k) a.cand[blockIdx.x * kSampleMaxK + tid] = L.top[tid];
     if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(a.arrived, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t prev = __hip_atomic_fetch_add(a.arrived, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         L.last = prev == static_cast<uint32_t>(a.slices - 1);
         if (L.last) __hip_atomic_store(a.arrived, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
