@@ -516,8 +516,10 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     if (wave >= 1 && sp0 < sh_passes) load_tile(sdt, a.sh_down, 0, lms, r0 + sp0 * lms.rpw, r0 + nr);
     XRaw<XDT, 8, RC> xrr;
     if (has_r || do_seg) load_xraw<XDT>(xrr, a.router, lmr, x, 0);
+    // (the PN kernels read their gate/up slice from LDS after the router
+    // rows: LDS reads ahead of the loads here delay them)
     XRaw<XDT, GB, GC> xgr;
-    load_xraw<XDT>(xgr, a.gate, lmg, x, 0);
+    if constexpr (!PN) load_xraw<XDT>(xgr, a.gate, lmg, x, 0);
     // The call's epoch, loaded after every other load of phase A: vector
     // loads complete in issue order, so the first wait for it waits for them
     // too, which the router row needs anyway; issued first, any wait for it
@@ -549,6 +551,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     }
     // activations in the gate/up format (shared and routed rows), held for
     // the whole call
+    if constexpr (PN) load_xraw<XDT>(xgr, a.gate, lmg, x, 0);
     XSlice<GB, GC, GX> xg;
     xslice_convert(xg, xgr);
     asm volatile("" : "+v"(lane));
