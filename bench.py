@@ -157,7 +157,7 @@ def main():
         return
 
     shape_key, batch = CONFIGS[args.config]
-    path = args.path if args.path != "auto" else ("fused" if batch == 1 else "staged")
+    path = args.path if args.path != "auto" else auto_path(batch)
     shape = synth.SHAPES[shape_key]
     torch.cuda.init()
     K, W = args.steps, args.warmup
@@ -374,6 +374,11 @@ def main():
     print(json.dumps(result), flush=True)
 
 
+def auto_path(batch):
+    """The single launch takes 1, 2 or 4 tokens; other batches run as three launches."""
+    return "fused" if batch in (1, 2, 4) else "staged"
+
+
 def decode_measure(args, torch, lib, name, R=None, K=None, W=None, path="auto", keep=False):
     """µs per MoE-layer decode step of workload `name` on R resident seeded
     layers (all experts each), cycled with a distinct input per layer.
@@ -392,7 +397,7 @@ def decode_measure(args, torch, lib, name, R=None, K=None, W=None, path="auto", 
     R = R or DEFAULT_REPLICAS.get(name, 48)
     K = K or max(R, 96)
     W = W if W is not None else R
-    path = path if path != "auto" else ("fused" if batch == 1 else "staged")
+    path = path if path != "auto" else auto_path(batch)
     mask = _lib.SWQ_STAGES_FUSED if path == "fused" else 7
     dev = "cuda"
     layers = [moe.synth_layer(shape, args.seed, r, dev) for r in range(R)]

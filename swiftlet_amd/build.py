@@ -57,7 +57,7 @@ def _compile(src: Path) -> Path:
 def build(verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     srcs = sources()
-    with ThreadPoolExecutor(max_workers=min(len(srcs), 4)) as ex:
+    with ThreadPoolExecutor(max_workers=min(len(srcs), 8)) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]

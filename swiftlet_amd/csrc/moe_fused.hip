@@ -1,6 +1,6 @@
 // Host side of the single-launch MoE decode step: plan, workspace layout,
 // launch and the per-device probe.  The kernel is in moe_fused.hpp.
-#include "moe_fused.hpp"
+#include "moe_fused_batch.hpp"
 
 #include <atomic>
 #include <mutex>
@@ -16,7 +16,7 @@ namespace swq {
 // gate/up rows in one format, 4- or 8-bit down rows, an 8-bit router and
 // shared-expert gate.  M = ceil(E / 64), as the staged path's routing wave.
 static FusedKernel fused_kernel_for(const QMat &router, const QMat &gate, const QMat &down, int x_dtype, int E,
-                                    bool prenorm) {
+                                    bool prenorm, bool batched) {
     if (router.bits != 8) return nullptr;
     const int m = (E + kWave - 1) / kWave;
     const int M = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
@@ -31,7 +31,8 @@ static FusedKernel fused_kernel_for(const QMat &router, const QMat &gate, const 
         gfmt = gate.cpl == 2 ? kFusedQ8C2 : kFusedQ8C1;
     }
     if (gfmt < 0) return nullptr;
-    if (prenorm) return x_dtype == SWQ_F32 ? fused_select_pn(gfmt, rc2, M) : nullptr;
+    if (prenorm) return x_dtype == SWQ_F32 && !batched ? fused_select_pn(gfmt, rc2, M) : nullptr;
+    if (batched) return x_dtype == SWQ_BF16 ? fused_select_bf16_batch(gfmt, rc2, M) : fused_select_f32_batch(gfmt, rc2, M);
     return x_dtype == SWQ_BF16 ? fused_select_bf16(gfmt, rc2, M) : fused_select_f32(gfmt, rc2, M);
 }
 
@@ -85,9 +86,13 @@ static int fused_blocks(FusedKernel k, int dev) {
 
 // The fused launch's arguments for this layer, or no kernel when the layer,
 // the batch or the device does not take the fused path.
-static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch, bool prenorm, FusedArgs *fa,
-                              int *nb) {
-    if (batch != 1) return nullptr;
+static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch, int max_batch, bool prenorm,
+                              FusedArgs *fa, int *nb) {
+    // one token, or 2 or 4 (a divisor of the eight waves, so that each wave's
+    // phase-A units are of one token); others take the three stages
+    if (batch != 1 && batch != 2 && batch != 4) return nullptr;
+    if (batch > min(max_batch, kFusedMaxBatch) || (prenorm && batch != 1)) return nullptr;
+    if (batch * layer->top_k > kFusedMaxSlots * kGroups) return nullptr;  // slots per XCD group
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
     const swq_qlinear *mats[8] = {&layer->router, &layer->gate, &layer->up, &layer->down,
@@ -127,12 +132,13 @@ static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch
     if (layer->moe_intermediate > kMaxInterFused || layer->moe_intermediate % 2 != 0) return nullptr;
     if (prenorm && layer->hidden > kPrenormMaxHidden) return nullptr;
     if (layer->hidden > kFusedMaxHidden || layer->num_experts > kMaxExperts) return nullptr;
-    FusedKernel kern = fused_kernel_for(a.router, a.gate, a.down, x_dtype, layer->num_experts, prenorm);
+    FusedKernel kern = fused_kernel_for(a.router, a.gate, a.down, x_dtype, layer->num_experts, prenorm, batch > 1);
     if (!kern) return nullptr;
     const int blocks = fused_blocks(kern, dev);
     if (blocks <= 0) return nullptr;
     const int H = layer->hidden;
     a.nb = blocks;
+    a.B = batch;
     a.rows_cmb = (H + blocks - 1) / blocks;
     if (a.rows_cmb > kMaxCombineRows) return nullptr;
     a.H = H;
@@ -160,7 +166,7 @@ int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int bat
     *taken = false;
     FusedArgs a;
     int nb = 0;
-    FusedKernel k = fused_plan(layer, x_dtype, batch, pn != nullptr, &a, &nb);
+    FusedKernel k = fused_plan(layer, x_dtype, batch, fl.max_batch, pn != nullptr, &a, &nb);
     if (!k) return SWQ_OK;
     uint8_t *wsb = static_cast<uint8_t *>(ws);
     a.x = x;

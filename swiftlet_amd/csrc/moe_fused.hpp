@@ -117,10 +117,10 @@ struct FusedArgs {
     float *user_w;
     uint32_t *gen;      // [kFusedMaxBlocks]
     uint32_t *err;      // the workspace's stall record
-    uint64_t *logit_x;  // [kReplicas][rep_stride] (logit, epoch)
-    uint64_t *hsh_x;    // [Is] shared SwiGLU activations
-    uint64_t *h_x;      // [K][I] routed SwiGLU activations
-    uint64_t *part_x;   // [K][H] routed down outputs
+    uint64_t *logit_x;  // [B][kReplicas][rep_stride] (logit, epoch): token-major replica sets
+    uint64_t *hsh_x;    // [B][Is] shared SwiGLU activations
+    uint64_t *h_x;      // [B K][I] routed SwiGLU activations, slot s = token s / K, pick s % K
+    uint64_t *part_x;   // [B K][H] routed down outputs
     int32_t rep_stride;
     int32_t odt, accumulate;
     int32_t H, E, K, I, Is, norm, has_shared;
@@ -136,6 +136,9 @@ struct FusedArgs {
     const void *norm_w;
     int32_t norm_dtype;
     float norm_eps;
+    // tokens of the batched kernel (moe_fused_batch.hpp); last, so that the
+    // fields the single-token kernel reads first keep their places
+    int32_t B;
 };
 
 // ---------------------------------------------------------------------------
@@ -792,5 +795,8 @@ enum FusedGateFormat { kFusedQ4 = 0, kFusedQ8C2 = 1, kFusedQ8C1 = 2 };
 FusedKernel fused_select_bf16(int gfmt, bool rc2, int M);
 FusedKernel fused_select_f32(int gfmt, bool rc2, int M);
 FusedKernel fused_select_pn(int gfmt, bool rc2, int M);
+// the same for 2 or 4 tokens (kernels holding kFusedMaxBatch)
+FusedKernel fused_select_bf16_batch(int gfmt, bool rc2, int M);
+FusedKernel fused_select_f32_batch(int gfmt, bool rc2, int M);
 
 }  // namespace swq

@@ -106,9 +106,11 @@ constexpr int kFusedMaxBlocks = 1024;   // epoch counters kept in step
 constexpr int kFusedReplicas = 8;       // logit replicas (one per XCD group)
 constexpr int kFusedMaxHidden = 8192;   // the compiled maxima of the scratch layout
 constexpr int kFusedMaxInter = 2048;
+constexpr int kFusedMaxBatch = 4;       // tokens of one single-launch step
 struct FusedLayout {
     size_t gen, logit_x, hsh_x, h_x, part_x, total;
     int rep_stride;
+    int max_batch;  // tokens the exchange regions hold
 };
 
 inline FusedLayout fused_layout(const swq_moe_layer *l, bool max_shape) {
@@ -124,15 +126,20 @@ inline FusedLayout fused_layout(const swq_moe_layer *l, bool max_shape) {
     const size_t I = max_shape ? kFusedMaxInter : l->moe_intermediate;
     const size_t Is = max_shape ? kFusedMaxInter : (l->has_shared ? l->shared_intermediate : 1);
     const size_t H = max_shape ? kFusedMaxHidden : l->hidden;
+    // a layer's own layout holds the largest single-launch batch, so that
+    // one workspace serves every batch; the compiled-maxima layout (the
+    // no-allocation scratch) holds one token
+    const size_t Bc = max_shape ? 1 : kFusedMaxBatch;
+    f.max_batch = static_cast<int>(Bc);
     // replicas 4 KiB apart plus a 256-byte skew, so they sit in different
     // memory channels
     const size_t rep_bytes = ((E * 8 + 4095) & ~static_cast<size_t>(4095)) + 256;
     f.rep_stride = static_cast<int>(rep_bytes / 8);
     f.gen = take(kFusedMaxBlocks * 4);
-    f.logit_x = take(rep_bytes * kFusedReplicas);
-    f.hsh_x = take(Is * 8);
-    f.h_x = take(K * I * 8);
-    f.part_x = take(K * H * 8);
+    f.logit_x = take(rep_bytes * kFusedReplicas * Bc);  // a set of replicas per token
+    f.hsh_x = take(Bc * Is * 8);
+    f.h_x = take(Bc * K * I * 8);
+    f.part_x = take(Bc * K * H * 8);
     f.total = off;
     return f;
 }

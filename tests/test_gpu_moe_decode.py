@@ -74,8 +74,10 @@ def _check_against_oracle(shape, xf, out, ids, w, seed=helpers.SEED, layer=0):
     ("qwen3.6-35b-a3b-q4", 1),
     ("qwen3-next-80b-a3b-q4", 1),
     ("qwen3.6-35b-a3b-q8", 1),
-    ("qwen3.6-35b-a3b-q8", 4),
-    ("qwen3.6-35b-a3b-q4", 3),
+    ("qwen3.6-35b-a3b-q8", 4),   # one launch, token-major slots
+    ("qwen3.6-35b-a3b-q4", 4),
+    ("qwen3-next-80b-a3b-q4", 2),
+    ("qwen3.6-35b-a3b-q4", 3),   # three launches
 ])
 def test_moe_decode_matches_oracle(name, batch):
     shape = synth.SHAPES[name]
@@ -117,7 +119,8 @@ def test_moe_decode_deterministic_and_accumulate():
 def test_moe_decode_odd_shapes(E, K, I, Is, H, bits, norm):
     shape = synth.MoEShape("odd", H, E, K, I, Is, expert_bits=bits, router_bits=8,
                            group=64 if H % 64 == 0 and I % 64 == 0 else 32, norm_topk_prob=norm)
-    for batch in (1, 5):
+    for batch in (1, 2, 4, 5):  # 5: the three launches
+        print(f"odd shape {E},{K},{I},{Is},{H},{bits} batch {batch}", flush=True)
         gpu, xf, out, ids, w = _run(shape, batch, seed=77)
         _check_against_oracle(shape, xf, out, ids, w, seed=77)
 
@@ -147,6 +150,26 @@ def test_fused_equals_staged(name, x_dtype, out_dtype):
     ws_f, ws_s = gpu.new_workspace(1), gpu.new_workspace(1)
     (of, i_f, w_f), (os_, i_s, w_s) = _pair(gpu, shape, x, out_dtype, ws_f, ws_s)
     assert gpu.workspace_error(ws_f) == 0
+    assert torch.equal(i_f, i_s) and torch.equal(w_f, w_s)
+    assert torch.equal(of, os_)
+    _check_against_oracle(shape, synth.bf16_to_f32(xb), of, i_f.cpu().numpy(), w_f.cpu().numpy())
+
+
+@pytest.mark.parametrize("name,batch", [
+    ("qwen3.6-35b-a3b-q8", 4), ("qwen3.6-35b-a3b-q4", 4), ("qwen3.6-35b-a3b-q4", 2), ("qwen3-next-80b-a3b-q4", 2)])
+def test_fused_batch_equals_staged(name, batch):
+    """2 or 4 tokens in one launch (slot s = pick s % K of token s / K):
+    the per-token tiles and sums of the single-token launch, so equal bit for
+    bit to the three launches, which read each distinct expert once."""
+    import torch
+    shape = synth.SHAPES[name]
+    print(f"fused vs staged: {name} batch {batch}", flush=True)
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    xb = synth.activations_bf16(helpers.SEED + 12, batch, shape.hidden)
+    x = helpers.bf16_bits_to_torch(xb)
+    ws_f, ws_s = gpu.new_workspace(batch), gpu.new_workspace(batch)
+    (of, i_f, w_f), (os_, i_s, w_s) = _pair(gpu, shape, x, "f32", ws_f, ws_s)
+    assert gpu.workspace_error(ws_f, batch) == 0
     assert torch.equal(i_f, i_s) and torch.equal(w_f, w_s)
     assert torch.equal(of, os_)
     _check_against_oracle(shape, synth.bf16_to_f32(xb), of, i_f.cpu().numpy(), w_f.cpu().numpy())
@@ -201,8 +224,8 @@ def test_workspace_serves_every_batch():
     import torch
     shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
     gpu = moe.synth_layer(shape, helpers.SEED, 0)
-    ws = gpu.new_workspace(4)
-    for i, batch in enumerate((4, 1, 4, 1)):
+    ws = gpu.new_workspace(5)
+    for i, batch in enumerate((4, 1, 5, 2, 4, 1)):
         x = helpers.bf16_bits_to_torch(synth.activations_bf16(helpers.SEED + 60 + i, batch, shape.hidden))
         o, ids, w = gpu.decode(x, ws=ws)
         fo, fids, fw = gpu.decode(x, ws=gpu.new_workspace(batch))
@@ -247,13 +270,23 @@ def test_single_expert_layer():
 
 
 def test_fused_declines_batches():
+    """The single launch takes 1, 2 or 4 tokens (a divisor of its eight
+    waves, up to its four-token exchange regions) and at most 32 (token,
+    pick) slots; other batches go to the three launches."""
     from swiftlet_amd import _lib
-    import torch
     shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
     gpu = moe.synth_layer(shape, helpers.SEED, 0)
-    x = helpers.bf16_bits_to_torch(synth.activations_bf16(3, 2, shape.hidden))
+    for batch in (3, 8):
+        x = helpers.bf16_bits_to_torch(synth.activations_bf16(3, batch, shape.hidden))
+        with pytest.raises(_lib.SwqError) as e:
+            gpu.decode(x, path="fused")
+        assert e.value.code == _lib.SWQ_ERR_LIMIT
+    # at most 32 (token, pick) slots: 4 tokens of top-10 go to the three launches
+    s80 = synth.SHAPES["qwen3-next-80b-a3b-q4"]
+    g80 = moe.synth_layer(s80, helpers.SEED, 0)
+    x = helpers.bf16_bits_to_torch(synth.activations_bf16(3, 4, s80.hidden))
     with pytest.raises(_lib.SwqError) as e:
-        gpu.decode(x, path="fused")
+        g80.decode(x, path="fused")
     assert e.value.code == _lib.SWQ_ERR_LIMIT
 
 
