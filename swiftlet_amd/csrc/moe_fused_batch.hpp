@@ -10,8 +10,9 @@
 // into (tile, token) units over the waves (B divides 8, so a wave's units are
 // of one token); wave t routes token t; the routed work is phase-major: the
 // gate/up rows of every owned slot stream with one slot in flight ahead,
-// then one exchange wait brings every owned slot's activations, then the
-// down rows stream; the combine writes token t's rows on wave t.
+// then one exchange wait brings the activations of every owned slot but the
+// last, whose wait comes after the other slots' down rows; the combine
+// writes token t's rows on wave t.
 #pragma once
 
 #include "moe_fused.hpp"
@@ -19,6 +20,60 @@
 namespace swq {
 
 constexpr int kFusedMaxSlots = 4;  // slots per XCD group: B K <= 32
+
+// One wave's activation pairs [p0, p1) of the slots grp + 8 j, j0 <= j < j1
+// (token-major rows of I words at hx), into hbb[j], and with NS > 0 its
+// pairs [f0, f1) of the shared expert's activations of all tokens laid end to
+// end (rows of Is words at hs, nps pairs each) into hsh: each polling round
+// takes 2 routed and NS shared pairs per lane, so the usual shapes need one
+// round trip for everything.
+template <int DB, int NS>
+__device__ __forceinline__ void fetch_slots(const uint64_t *hx, int I, int grp, int j0, int j1, int p0, int p1,
+                                            uint32_t (*hbb)[kMaxInterFused], const uint64_t *hs, int Is, int nps,
+                                            int f0, int f1, uint32_t (*hsh)[kMaxInterFused], uint32_t g, int lane,
+                                            uint32_t *err) {
+    constexpr int N = 4 + 2 * NS;
+    const int c = p1 - p0, nr = c > 0 && j1 > j0 ? (j1 - j0) * c : 0;
+    const int ns = NS > 0 ? max(f1 - f0, 0) : 0;
+    for (int q = 0, qs = 0; q < nr || qs < ns; q += 2 * kWave, qs += NS * kWave) {
+        const uint64_t *pp[N];
+        bool live[N];
+        int rj[2], rp[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int f = q + u * kWave + lane;
+            live[2 * u] = live[2 * u + 1] = f < nr;
+            const int fc = f < nr ? f : 0;
+            const int jj = c > 0 ? fc / c : 0;
+            rj[u] = j0 + jj;
+            rp[u] = p0 + fc - jj * c;
+            const uint64_t *row = hx + static_cast<int64_t>(grp + kGroups * rj[u]) * I;
+            pp[2 * u] = row + pair_first<DB>(rp[u]);
+            pp[2 * u + 1] = row + pair_second<DB>(rp[u]);
+        }
+        int st[NS > 0 ? NS : 1], sq[NS > 0 ? NS : 1];
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            const int f = f0 + qs + u * kWave + lane;
+            const bool l = qs + u * kWave + lane < ns;
+            live[4 + 2 * u] = live[5 + 2 * u] = l;
+            const int fc = l ? f : f0;
+            st[u] = fc / nps;
+            sq[u] = fc - st[u] * nps;
+            const uint64_t *row = hs + static_cast<int64_t>(st[u]) * Is;
+            pp[4 + 2 * u] = row + pair_first<DB>(sq[u]);
+            pp[5 + 2 * u] = row + pair_second<DB>(sq[u]);
+        }
+        float v[N];
+        poll_words<N>(pp, live, g, v, err, 1u);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            if (live[2 * u]) store_pair_lds<DB>(hbb[rj[u]], rp[u], v[2 * u], v[2 * u + 1]);
+#pragma unroll
+        for (int u = 0; u < NS; ++u)
+            if (live[4 + 2 * u]) store_pair_lds<DB>(hsh[st[u]], sq[u], v[4 + 2 * u], v[5 + 2 * u]);
+    }
+}
 
 template <int XDT, int GB, int GC, int GX, int GRI, int DB, int DRI, int RC, int M>
 __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(kFusedWaves / 4, kFusedWaves / 4))) void moe_fused_batch(FusedArgs a) {
@@ -89,8 +144,6 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     const int sh_passes = sh_rows ? (nr + lms.rpw - 1) / lms.rpw : 0;
     // (the waves from B on, which have no token to route and combine)
     const int sp0 = wave - B, nsw = kFusedWaves - B;
-    RowTile<DB, 1, 2, 1> sdt;
-    if (wave >= B && sp0 < sh_passes) load_tile(sdt, a.sh_down, 0, lms, r0 + sp0 * lms.rpw, r0 + nr);
     XRaw<XDT, 8, RC> xrr;
     if (has_r) load_xraw<XDT>(xrr, a.router, lmr, xtok(wave & (B - 1)), 0);
     else if (do_seg) load_xraw<XDT>(xrr, a.router, lmr, xtok(seg_tok), 0);
@@ -187,9 +240,9 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     // Slot s (0 <= s < B K) is pick s % K of token s / K; group grp owns the
     // slots grp + 8 j, j < nsl <= kFusedMaxSlots.  Phase G streams their
     // gate/up rows with the next slot's tiles (and its token's x slice) in
-    // flight during the current slot's dot products; phase D polls every
-    // owned slot's activations (one exchange wait for all of them, not one
-    // per slot) and streams the down rows the same way.
+    // flight during the current slot's dot products; phase D streams the
+    // down rows the same way, polling the last slot's activations only after
+    // the other slots' down rows.
     const int S = B * a.K;
     const int nsl = S > grp ? (S - 1 - grp) / kGroups + 1 : 0;
     const int np_r = a.I / 2, q_r = (np_r + kFusedWaves - 1) / kFusedWaves;
@@ -199,6 +252,14 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     const int t0 = rank + NPG * wave;  // this wave's first tile of a slot
     const bool gu1 = t0 < a.gu_tpe, dn1 = t0 < a.dn_tpe;
     int64_t ex[kFusedMaxSlots];  // the owned slots' experts
+    // Down tiles of slots j (mod 2): the first two go out before the
+    // activation polls, slot j + 2's as soon as slot j's down rows are done.
+    // (Issued during the last slot's gate/up rows instead, they overlap
+    // more, but the tiles then live across the gate/up code and the 8-bit
+    // kernels spill: 68.7 against 39.0 us at batch 4.)
+    using DTile = RowTile<DB, 1, 2, DRI>;
+    DTile dt0, dt1;
+    RowTile<DB, 1, 2, 1> sdt;
     {
         using GTile = RowTile<GB, GC, 2, GRI>;
         using GX_ = XRaw<XDT, GB, GC>;
@@ -253,40 +314,42 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
         }
     }
     {
-        using DTile = RowTile<DB, 1, 2, DRI>;
-        DTile dta, dtb;
-        // the first slot's down tile, issued before the activation polls
-        if (nsl > 0 && dn1) load_tile(dta, a.down, ex[0], lmd, t0 * DRI * lmd.rpw, a.H);
-        // Without this the compiler may sink the loads below the polls
-        // and the barrier that follow (allowed across an acquire), so they
-        // would start only once the activations are in.
+        if (nsl > 0 && dn1) {
+            load_tile(dt0, a.down, ex[0], lmd, t0 * DRI * lmd.rpw, a.H);
+            if (nsl > 1) load_tile(dt1, a.down, ex[1], lmd, t0 * DRI * lmd.rpw, a.H);
+        }
+        if (wave >= B && sp0 < sh_passes) load_tile(sdt, a.sh_down, 0, lms, r0 + sp0 * lms.rpw, r0 + nr);
+        // Without this the compiler may sink the down tiles' loads below the
+        // polls and the barrier that follow (allowed across an acquire), so
+        // they would start only once the activations are in.
         asm volatile("" ::: "memory");
-        // the shared expert's activations of every token (written in phase
-        // A): a share on each wave from B on, in LDS by the barrier below
+        // The activations of every owned slot but the last (an eighth polled
+        // by each wave) and, on the waves from B on, a share of the shared
+        // expert's activations of every token (written in phase A), in one
+        // round trip; the last slot's come after the other slots' down rows,
+        // so that the group's last gate/up rows are not waited for first.
+        const int pr0 = min(np_r, wave * q_r), pr1 = min(np_r, (wave + 1) * q_r);
+        const int jl = max(nsl - 1, 0);
         if (wave >= B && sh_rows) {
             const int nf = B * np_s, q3 = (nf + nsw - 1) / nsw;
-            const int f0 = min(nf, sp0 * q3), f1 = min(nf, (sp0 + 1) * q3);
-            for (int tok = 0; tok < B; ++tok) {
-                // this wave's pairs of token tok: [f0, f1) within [tok np_s, (tok + 1) np_s)
-                const int p0 = max(f0 - tok * np_s, 0), p1 = min(f1 - tok * np_s, np_s);
-                if (p0 < p1) fetch_acts<DB>(a.hsh_x + tok * a.Is, p0, p1, g, s_hsh[tok], lane, a.err);
-            }
-            SWQ_STAMP(12);
+            fetch_slots<DB, 4>(a.h_x, a.I, grp, 0, jl, pr0, pr1, s_hbb, a.hsh_x, a.Is, np_s, min(nf, sp0 * q3),
+                               min(nf, (sp0 + 1) * q3), s_hsh, g, lane, a.err);
+        } else {
+            fetch_slots<DB, 0>(a.h_x, a.I, grp, 0, jl, pr0, pr1, s_hbb, a.hsh_x, a.Is, np_s, 0, 0, s_hsh, g, lane,
+                               a.err);
         }
-        // every owned slot's activations: each wave polls an eighth of each
-#pragma unroll
-        for (int j = 0; j < kFusedMaxSlots; ++j)
-            if (j < nsl)
-                fetch_acts<DB>(a.h_x + static_cast<int64_t>(grp + kGroups * j) * a.I, min(np_r, wave * q_r),
-                               min(np_r, (wave + 1) * q_r), g, s_hbb[j], lane, a.err);
         __syncthreads();
         SWQ_STAMP(5);
 #pragma unroll
         for (int j = 0; j < kFusedMaxSlots; ++j) {
             if (j < nsl) {
                 const int s = grp + kGroups * j;
-                DTile &dt = (j & 1) ? dtb : dta;
-                if (j + 1 < nsl && dn1) load_tile((j & 1) ? dta : dtb, a.down, ex[j + 1], lmd, t0 * DRI * lmd.rpw, a.H);
+                if (j == jl) {  // nsl is the same on every wave
+                    fetch_slots<DB, 0>(a.h_x, a.I, grp, jl, jl + 1, pr0, pr1, s_hbb, a.hsh_x, a.Is, np_s, 0, 0,
+                                       s_hsh, g, lane, a.err);
+                    __syncthreads();
+                }
+                DTile &dt = (j & 1) ? dt1 : dt0;
                 for (int t = t0; t < a.dn_tpe; t += NPG * kFusedWaves) {
                     const int row0 = t * DRI * lmd.rpw;
                     if (t != t0) load_tile(dt, a.down, ex[j], lmd, row0, a.H);
@@ -300,6 +363,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
                         }
                     }
                 }
+                if (j + 2 < nsl && dn1) load_tile(dt, a.down, ex[j + 2], lmd, t0 * DRI * lmd.rpw, a.H);
             }
         }
         SWQ_STAMP(6);
