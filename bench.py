@@ -607,6 +607,10 @@ def model_measure(args, torch, lib, shape, moe_layers, moe_ws, tokens=4):
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1000.0 / tokens
+    # every MoE step of the replays completed normally (a stalled single
+    # launch leaves its record in the workspace; its outputs would be invalid)
+    for i, ws in enumerate(moe_ws):
+        check(lib.swq_moe_workspace_status(ws.data_ptr(), ws.numel(), 1, None), f"model: MoE layer {i} workspace status")
     del gr, blocks, head
     torch.cuda.synchronize()
     torch.cuda.empty_cache()

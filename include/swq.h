@@ -425,7 +425,9 @@ int swq_moe_workspace_init(void *ws, size_t ws_bytes, void *stream);
  * outputs are invalid (the reference throws, MetalEngine.swift:8-11;
  * a stream-ordered call cannot, so the failure is recorded here).
  * Blocking: waits for the stream's earlier work, then reads the record
- * (one 4-byte copy) and, when clear != 0, resets it.  Not capturable. */
+ * (one 4-byte copy) and, when clear != 0, resets it.  Not capturable.
+ * ws = NULL with ws_bytes = 0 names the current device's
+ * swq_moe_decode_noalloc array (SWQ_OK if it was never set up). */
 int swq_moe_workspace_status(void *ws, size_t ws_bytes, int clear, void *stream);
 
 /* One MoE-layer decode step for `batch` independent tokens, entirely on the
@@ -461,11 +463,12 @@ int swq_moe_decode(const swq_moe_layer *layer,
  * SWQ_ERR_LIMIT (the limit covers the benchmark shapes at any batch up to
  * SWQ_MAX_BATCH; use swq_moe_decode for larger ones).  The first call on a
  * device sets the array up (its address, the single launch's XCD probe, a
- * zero fill) and blocks until done: make it outside stream capture.  Calls
- * on any layer and batch may follow one another.  A stall of the single
- * launch (see swq_moe_workspace_status) is recorded in the array and has no
- * query: this path assumes a device running nothing else.  Arguments and
- * results are swq_moe_decode's. */
+ * zero fill) and blocks until done: make it outside stream capture (under
+ * capture it returns SWQ_ERR_INVALID_ARGUMENT and the set-up waits for the
+ * next call; after it, calls may be captured).  Calls on any layer and
+ * batch may follow one another.  A stall of the single launch is recorded
+ * in the array: swq_moe_workspace_status(NULL, 0, clear, stream) reads it.
+ * Arguments and results are swq_moe_decode's. */
 int swq_moe_decode_noalloc(const swq_moe_layer *layer,
                            const void *x, int x_dtype, int batch,
                            void *out, int out_dtype,

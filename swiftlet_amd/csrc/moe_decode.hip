@@ -807,7 +807,18 @@ extern "C" size_t swq_moe_workspace_error_offset(const swq_moe_layer *layer, int
     return kWsErrByte;
 }
 
+static int scratch_if_set(uint8_t **out);
+
 extern "C" int swq_moe_workspace_status(void *ws, size_t ws_bytes, int clear, void *stream) {
+    if (!ws && ws_bytes == 0) {
+        // the current device's swq_moe_decode_noalloc array (nothing ran on
+        // this device if it was never set up)
+        uint8_t *p = nullptr;
+        const int st = scratch_if_set(&p);
+        if (st != SWQ_OK || !p) return st;
+        ws = p;
+        ws_bytes = 256;
+    }
     if (!ws || ws_bytes < 256) return SWQ_ERR_WORKSPACE;
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint32_t *word = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(ws) + kWsErrByte);
@@ -1014,34 +1025,60 @@ static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {
 struct ScratchDevice {
-    std::once_flag once;
-    std::atomic<uint8_t *> ptr{nullptr};
-    std::atomic<int> status{SWQ_ERR_HIP};
+    std::mutex mu;  // serialises the set-up
+    std::atomic<uint8_t *> ptr{nullptr};  // set once the set-up succeeded
 };
 ScratchDevice g_scratch_dev[64];
 }  // namespace
+
+static int current_device(int *dev) {
+    if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= 64) return SWQ_ERR_HIP;
+    return SWQ_OK;
+}
+
+// This device's array if its set-up has run (else null).
+static int scratch_if_set(uint8_t **out) {
+    int dev = 0;
+    const int st = current_device(&dev);
+    if (st != SWQ_OK) return st;
+    *out = g_scratch_dev[dev].ptr.load(std::memory_order_acquire);
+    return SWQ_OK;
+}
 
 // Once per device, with that device current: the array's device address
 // (in host code the array's name is only a stand-in, so it appears nowhere
 // but in HIP_SYMBOL here), the single launch's XCD probe (writing into the
 // array rather than into an allocation), then the whole array zero-filled by
-// a kernel.  Blocking (first call on a device only).
+// a kernel.  Blocking (first call on a device only).  A stream under capture
+// cannot run it: the call returns SWQ_ERR_INVALID_ARGUMENT and the set-up
+// stays pending, as it does after any failure, for the next call outside
+// capture.
 static int scratch_for_device(hipStream_t stream, uint8_t **out) {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return SWQ_ERR_HIP;
-    ScratchDevice &d = g_scratch_dev[dev];
-    std::call_once(d.once, [&]() {
-        void *p = nullptr;
-        int st = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess && p ? SWQ_OK : SWQ_ERR_HIP;
-        if (st == SWQ_OK) st = fused_probe_device(stream, p);
-        if (st == SWQ_OK) st = zero_fill(p, kScratchBytes, stream);
-        if (st == SWQ_OK && hipStreamSynchronize(stream) != hipSuccess) st = SWQ_ERR_HIP;
-        d.ptr.store(static_cast<uint8_t *>(p), std::memory_order_release);
-        d.status.store(st, std::memory_order_release);
-    });
-    const int st = d.status.load(std::memory_order_acquire);
+    int st = current_device(&dev);
     if (st != SWQ_OK) return st;
-    *out = d.ptr.load(std::memory_order_acquire);
+    ScratchDevice &d = g_scratch_dev[dev];
+    uint8_t *p = d.ptr.load(std::memory_order_acquire);
+    if (p) {
+        *out = p;
+        return SWQ_OK;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) return SWQ_ERR_HIP;
+    if (cs != hipStreamCaptureStatusNone) return SWQ_ERR_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(d.mu);
+    p = d.ptr.load(std::memory_order_acquire);
+    if (!p) {
+        void *q = nullptr;
+        st = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) == hipSuccess && q ? SWQ_OK : SWQ_ERR_HIP;
+        if (st == SWQ_OK) st = fused_probe_device(stream, q);
+        if (st == SWQ_OK) st = zero_fill(q, kScratchBytes, stream);
+        if (st == SWQ_OK && hipStreamSynchronize(stream) != hipSuccess) st = SWQ_ERR_HIP;
+        if (st != SWQ_OK) return st;
+        p = static_cast<uint8_t *>(q);
+        d.ptr.store(p, std::memory_order_release);
+    }
+    *out = p;
     return SWQ_OK;
 }
 

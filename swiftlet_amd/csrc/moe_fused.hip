@@ -36,13 +36,13 @@ static FusedKernel fused_kernel_for(const QMat &router, const QMat &gate, const 
     return x_dtype == SWQ_BF16 ? fused_select_bf16(gfmt, rc2, M) : fused_select_f32(gfmt, rc2, M);
 }
 
-// Per device, set once by fused_probe_device (under std::call_once, then
-// read with acquire loads): the CU count and whether the workgroups of each
-// group (b mod kGroups) of a grid of one workgroup per CU
+// Per device, set once by fused_probe_device (under probe_mu, then read
+// with acquire loads; cus > 0 once set): the CU count and whether the
+// workgroups of each group (b mod kGroups) of a grid of one workgroup per CU
 // run on one XCD.  The kernels whose occupancy has been checked sit in a
 // small list under a mutex.
 struct FusedDevice {
-    std::once_flag once;
+    std::mutex probe_mu;
     std::atomic<int> cus{0};
     std::atomic<int> local{0};
     std::mutex mu;
@@ -199,46 +199,43 @@ int fused_decode(const swq_moe_layer *layer, const void *x, int x_dtype, int bat
 // Once per device: the CU count and whether a grid of one workgroup per CU
 // places every group's workgroups on one XCD (a launch of that grid reports
 // each workgroup's XCC_ID).  Blocking; runs on `stream`.  Thread-safe: the
-// first caller for a device runs the probe (std::call_once), later ones
-// wait for it; if it fails the device keeps the three-launch path.  The
+// first caller for a device runs the probe under a mutex, later ones wait
+// for it.  Until a probe has succeeded the device keeps the three-launch
+// path, and a failed probe (or a call on a stream under capture, which
+// cannot block: SWQ_ERR_INVALID_ARGUMENT) leaves it to the next call.  The
 // probe writes one word per workgroup into `given` when the caller passes
 // device memory of kFusedMaxBlocks words, else into a buffer it allocates.
 int fused_probe_device(hipStream_t stream, void *given) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return SWQ_ERR_HIP;
     FusedDevice &d = g_fused_dev[dev];
-    int status = SWQ_OK;
-    std::call_once(d.once, [&]() {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-            status = SWQ_ERR_HIP;
-            return;
-        }
-        const int n = min(cus, kFusedMaxBlocks) / kGroups * kGroups;  // the fused grid
-        int ok = 0;
-        if (n >= kGroups) {
-            int32_t *buf = static_cast<int32_t *>(given);
-            if (!buf && hipMalloc(&buf, n * sizeof(int32_t)) != hipSuccess) {
-                status = SWQ_ERR_HIP;
-                return;
-            }
-            hipLaunchKernelGGL(xcd_probe_kernel, dim3(n), dim3(kFusedThreads), 0, stream, buf);
-            int32_t h[kFusedMaxBlocks];
-            hipError_t e = hipGetLastError();
-            if (e == hipSuccess) e = hipMemcpyAsync(h, buf, n * sizeof(int32_t), hipMemcpyDeviceToHost, stream);
-            if (e == hipSuccess) e = hipStreamSynchronize(stream);
-            if (!given) hipFree(buf);
-            if (e != hipSuccess) {
-                status = SWQ_ERR_HIP;
-                return;
-            }
-            ok = 1;
-            for (int i = kGroups; i < n; ++i) ok &= h[i] == h[i % kGroups];
-        }
-        d.local.store(ok, std::memory_order_release);
-        d.cus.store(cus, std::memory_order_release);
-    });
-    return status;
+    if (d.cus.load(std::memory_order_acquire) > 0) return SWQ_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) return SWQ_ERR_HIP;
+    if (cs != hipStreamCaptureStatusNone) return SWQ_ERR_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(d.probe_mu);
+    if (d.cus.load(std::memory_order_acquire) > 0) return SWQ_OK;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return SWQ_ERR_HIP;
+    const int n = min(cus, kFusedMaxBlocks) / kGroups * kGroups;  // the fused grid
+    int ok = 0;
+    if (n >= kGroups) {
+        int32_t *buf = static_cast<int32_t *>(given);
+        if (!buf && hipMalloc(&buf, n * sizeof(int32_t)) != hipSuccess) return SWQ_ERR_HIP;
+        hipLaunchKernelGGL(xcd_probe_kernel, dim3(n), dim3(kFusedThreads), 0, stream, buf);
+        int32_t h[kFusedMaxBlocks];
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = hipMemcpyAsync(h, buf, n * sizeof(int32_t), hipMemcpyDeviceToHost, stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(stream);
+        if (!given) hipFree(buf);
+        if (e != hipSuccess) return SWQ_ERR_HIP;
+        ok = 1;
+        for (int i = kGroups; i < n; ++i) ok &= h[i] == h[i % kGroups];
+    }
+    d.local.store(ok, std::memory_order_release);
+    d.cus.store(cus, std::memory_order_release);
+    return SWQ_OK;
 }
 
 }  // namespace swq

@@ -89,6 +89,9 @@ class MoELayerGPU:
         ``path``: "auto" (swq_moe_decode: one launch when the layer and batch
         allow, else three), "staged" (the three launches) or "fused" (the
         single launch; raises SwqError LIMIT when it cannot take the call).
+        Without ``ws`` the call makes a workspace and reads its stall record
+        afterwards (blocking; SwqError STALLED if a bounded wait ran out);
+        with ``ws`` the caller reads it with workspace_status.
         Returns (out [B, H], topk_ids [B, K] int32, topk_weights [B, K] f32)."""
         torch = _torch()
         if x.dim() == 1:
@@ -99,7 +102,8 @@ class MoELayerGPU:
             odt = out_dtype or torch.float32
             out = torch.empty((B, self.hidden), dtype=odt, device=x.device)
         o_dtype = {torch.bfloat16: SWQ_BF16, torch.float32: SWQ_F32}[out.dtype]
-        if ws is None:
+        own_ws = ws is None
+        if own_ws:
             ws = self.new_workspace(B, stream)
         if topk_ids is None:
             topk_ids = torch.empty((B, self.top_k), dtype=torch.int32, device=x.device)
@@ -113,6 +117,10 @@ class MoELayerGPU:
         else:
             mask = {"staged": 7, "fused": _lib.SWQ_STAGES_FUSED}[path]
             check(self.lib.swq_moe_decode_stages(*args, mask, _stream_handle(stream)), f"moe_decode ({path})")
+        if own_ws:
+            # a workspace made for this call: its stall record is read here
+            # (blocking), as no caller can read it later
+            check(self.workspace_status(ws, stream=stream), "moe_decode")
         return out, topk_ids, topk_weights
 
     def decode_norm(self, h, norm_weight, eps: float, residual=None, out=None, ws=None, topk_ids=None,
@@ -126,7 +134,8 @@ class MoELayerGPU:
         h = h.reshape(-1)
         if out is None:
             out = torch.empty(self.hidden, dtype=torch.float32, device=h.device)
-        if ws is None:
+        own_ws = ws is None
+        if own_ws:
             ws = self.new_workspace(1, stream)
         if topk_ids is None:
             topk_ids = torch.empty((1, self.top_k), dtype=torch.int32, device=h.device)
@@ -138,6 +147,8 @@ class MoELayerGPU:
                                            norm_weight.data_ptr(), wdt, eps, out.data_ptr(), topk_ids.data_ptr(),
                                            topk_weights.data_ptr(), ws.data_ptr(), ws.numel(),
                                            _stream_handle(stream)), "moe_decode_norm")
+        if own_ws:
+            check(self.workspace_status(ws, stream=stream), "moe_decode_norm")
         return out, topk_ids, topk_weights
 
     # -- prefill -------------------------------------------------------

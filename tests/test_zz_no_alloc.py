@@ -3,8 +3,11 @@ static device array inside the library, against swq_moe_decode itself (a
 workspace of its own per layer): equal bit for bit on two calls in a row, the
 second with a smaller input (batch 4 on the three launches, then batch 1 on
 the single launch), then a different, smaller layer sharing the same array,
-then the first layer again.  A layer whose workspace exceeds the array is
-refused before any launch."""
+then the first layer again; f32 activations, bf16 outputs and the
+accumulate flag; calls between swq_moe_decode_norm calls; the entry point
+captured in a HIP graph and replayed.  Every test ends with the array's stall
+record clear.  A layer whose workspace exceeds the array is refused before
+any launch."""
 
 import ctypes
 
@@ -16,9 +19,18 @@ from tests import helpers
 pytestmark = pytest.mark.gpu
 
 
-def _noalloc(lib, layer, x, out, ids, w):
-    return lib.swq_moe_decode_noalloc(ctypes.byref(layer._c), x.data_ptr(), _lib.SWQ_BF16, x.shape[0],
-                                      out.data_ptr(), _lib.SWQ_F32, ids.data_ptr(), w.data_ptr(), 0, None)
+def _noalloc(lib, layer, x, out, ids, w, flags=0, stream=None):
+    import torch
+    xdt = _lib.SWQ_BF16 if x.dtype == torch.bfloat16 else _lib.SWQ_F32
+    odt = _lib.SWQ_BF16 if out.dtype == torch.bfloat16 else _lib.SWQ_F32
+    return lib.swq_moe_decode_noalloc(ctypes.byref(layer._c), x.data_ptr(), xdt, x.shape[0], out.data_ptr(), odt,
+                                      ids.data_ptr(), w.data_ptr(), flags, stream)
+
+
+def _status(lib):
+    """The stall record of this device's array (a NULL workspace of 0 bytes
+    names it), cleared by the read."""
+    return lib.swq_moe_workspace_status(None, 0, 1, None)
 
 
 def _compare(lib, layer, batch, seed):
@@ -46,6 +58,7 @@ def test_noalloc_matches_decode():
     _compare(lib, small, 1, 78)
     _compare(lib, small, 3, 79)
     _compare(lib, big, 1, helpers.SEED + 43)
+    assert _status(lib) == _lib.SWQ_OK
 
 
 def test_noalloc_refuses_layers_beyond_its_array():
@@ -60,3 +73,98 @@ def test_noalloc_refuses_layers_beyond_its_array():
     ids = torch.empty((16, 16), dtype=torch.int32, device="cuda")
     w = torch.empty((16, 16), dtype=torch.float32, device="cuda")
     assert _noalloc(lib, layer, x, out, ids, w) == _lib.SWQ_ERR_LIMIT
+
+
+def test_noalloc_dtypes_and_accumulate():
+    """f32 activations, bf16 outputs and the accumulate flag, on the single
+    launch and the three launches, against swq_moe_decode with the same
+    arguments."""
+    import torch
+    lib = _lib.load()
+    layer = moe.synth_layer(synth.SHAPES["qwen3.6-35b-a3b-q4"], helpers.SEED, 0)
+    for batch in (1, 3):
+        print(f"noalloc dtypes/accumulate: batch {batch}", flush=True)
+        xb = helpers.bf16_bits_to_torch(synth.activations_bf16(helpers.SEED + 50 + batch, batch, layer.hidden))
+        x32 = xb.float() * 1.25
+        ids = torch.empty((batch, layer.top_k), dtype=torch.int32, device="cuda")
+        w = torch.empty((batch, layer.top_k), dtype=torch.float32, device="cuda")
+        # f32 x -> bf16 out
+        ref, ref_ids, ref_w = layer.decode(x32, out_dtype=torch.bfloat16)
+        out = torch.full_like(ref, float("nan"))
+        _lib.check(_noalloc(lib, layer, x32, out, ids, w), "moe_decode_noalloc")
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref) and torch.equal(ids, ref_ids) and torch.equal(w, ref_w)
+        # bf16 x, accumulate into f32 out that already holds values
+        base = torch.linspace(-1.0, 1.0, batch * layer.hidden, device="cuda").reshape(batch, layer.hidden)
+        ref_acc = base.clone()
+        layer.decode(xb, out=ref_acc, accumulate=True)
+        out_acc = base.clone()
+        _lib.check(_noalloc(lib, layer, xb, out_acc, ids, w, flags=_lib.SWQ_MOE_ACCUMULATE), "moe_decode_noalloc")
+        torch.cuda.synchronize()
+        assert torch.equal(out_acc, ref_acc)
+    assert _status(lib) == _lib.SWQ_OK
+
+
+def test_noalloc_interleaved_with_norm_step():
+    """No-alloc calls between swq_moe_decode_norm calls (their own workspace)
+    leave both results as they are alone."""
+    import torch
+    lib = _lib.load()
+    layer = moe.synth_layer(synth.SHAPES["qwen3.6-35b-a3b-q4"], helpers.SEED, 0)
+    H = layer.hidden
+    g = torch.Generator(device="cpu").manual_seed(7)
+    h = (torch.randn(H, generator=g) * 0.5).cuda()
+    r = (torch.randn(H, generator=g) * 0.5).cuda()
+    nw = (1.0 + 0.1 * torch.randn(H, generator=g)).cuda()
+    ws = layer.new_workspace(1)
+    ref_norm = layer.decode_norm(h, nw, 1e-6, residual=r, ws=ws)[0].clone()
+    xb = helpers.bf16_bits_to_torch(synth.activations_bf16(helpers.SEED + 60, 1, H))
+    ref, ref_ids, ref_w = layer.decode(xb)
+    out = torch.empty_like(ref)
+    ids = torch.empty_like(ref_ids)
+    w = torch.empty_like(ref_w)
+    for i in range(3):
+        print(f"noalloc / decode_norm interleave {i}", flush=True)
+        _lib.check(_noalloc(lib, layer, xb, out, ids, w), "moe_decode_noalloc")
+        got_norm = layer.decode_norm(h, nw, 1e-6, residual=r, ws=ws)[0]
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref) and torch.equal(ids, ref_ids)
+        assert torch.equal(got_norm, ref_norm)
+    assert layer.workspace_status(ws) == _lib.SWQ_OK
+    assert _status(lib) == _lib.SWQ_OK
+
+
+def test_noalloc_replays_under_graph_capture():
+    """The entry point captured in a HIP graph (after a first call outside
+    capture has set the array up): every replay, with new activations copied
+    into the captured input between replays and eager work in between,
+    equals swq_moe_decode on the same input."""
+    import torch
+    lib = _lib.load()
+    layer = moe.synth_layer(synth.SHAPES["qwen3.6-35b-a3b-q4"], helpers.SEED, 0)
+    H, K = layer.hidden, layer.top_k
+    x = torch.zeros((1, H), dtype=torch.bfloat16, device="cuda")
+    out = torch.empty((1, H), dtype=torch.float32, device="cuda")
+    ids = torch.empty((1, K), dtype=torch.int32, device="cuda")
+    w = torch.empty((1, K), dtype=torch.float32, device="cuda")
+    _lib.check(_noalloc(lib, layer, x, out, ids, w), "moe_decode_noalloc")  # set-up, outside capture
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            st = _noalloc(lib, layer, x, out, ids, w, stream=ctypes.c_void_p(side.cuda_stream))
+    _lib.check(st, "moe_decode_noalloc under capture")
+    for i in range(4):
+        print(f"graph replay {i}", flush=True)
+        xi = helpers.bf16_bits_to_torch(synth.activations_bf16(helpers.SEED + 70 + i, 1, H))
+        x.copy_(xi)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref, ref_ids, ref_w = layer.decode(xi)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(ids, ref_ids)
+        assert torch.equal(w, ref_w)
+        assert torch.equal(out, ref)
+    assert _status(lib) == _lib.SWQ_OK
