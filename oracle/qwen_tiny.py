@@ -6,15 +6,21 @@ top-k, renormalisation, SwiGLU experts, shared expert gate) and the MLX
 affine dequantisation together are mlx's captures of a tiny whole model
 (fixtures/tiny_forward*.safetensors).  Reaching the MoE block requires the
 rest of each decoder layer, so this module restates QwenCPUModel's
-non-MoE ops for that model (qwen3_next, fused-interleaved DeltaNet layout)
-and delegates the MoE block to oracle.moe_ref.moe_forward:
+non-MoE ops for that model and delegates the MoE block to
+oracle.moe_ref.moe_forward.  Both checkpoint families the reference reads:
+qwen3_next (flat config, fused-interleaved DeltaNet projections) and qwen3_5
+(config nested under text_config, rope under rope_parameters, split DeltaNet
+projections, weights named "language_model.*"):
 
+  config (both families)           QwenConfig.swift:50-105
+  "language_model." names          Checkpoint.swift:74-80
   Checkpoint quant spec / dequant  Checkpoint.swift:31-49, 126-133, 168-209
   rms_norm                         QwenCPUModel.swift:47-59
   layer_forward                    QwenCPUModel.swift:259-281
   attention_forward                QwenCPUModel.swift:285-345
   apply_rope                       QwenCPUModel.swift:348-367
-  deltanet_forward                 QwenCPUModel.swift:371-496
+  deltanet_forward                 QwenCPUModel.swift:371-496 (split
+                                   projections: :415-420)
   forward / greedy                 QwenCPUModel.swift:208-236
 """
 
@@ -33,13 +39,43 @@ from . import moe_ref as R
 f32 = np.float32
 
 
+def text_config(cfg: dict) -> dict:
+    """QwenConfig(url:) (QwenConfig.swift:50-105): the text model's fields
+    (nested under text_config in multimodal checkpoints), rope_theta and
+    partial_rotary_factor from rope_parameters when present, plus
+    "split_layout" (the qwen3_5 family: model_type qwen3_5* / qwen3_6* or a
+    nested config) and "weight_prefix" ("language_model." when nested)."""
+    text = cfg.get("text_config", cfg)
+    nested = "text_config" in cfg
+    c = dict(text)
+    c["model_type"] = text.get("model_type", cfg.get("model_type", "qwen3_next"))
+    c["tie_word_embeddings"] = text.get("tie_word_embeddings", cfg.get("tie_word_embeddings", False))
+    rp = text.get("rope_parameters")
+    if isinstance(rp, dict):
+        c["rope_theta"] = float(rp.get("rope_theta", 10_000_000))
+        c["partial_rotary_factor"] = float(rp.get("partial_rotary_factor", 0.25))
+    else:
+        c["rope_theta"] = float(text["rope_theta"])
+        c["partial_rotary_factor"] = float(text.get("partial_rotary_factor", 0.25))
+    mt = c["model_type"]
+    c["split_layout"] = mt.startswith("qwen3_5") or mt.startswith("qwen3_6") or nested
+    c["weight_prefix"] = "language_model." if nested else ""
+    return c
+
+
 class TinyCheckpoint:
-    """Checkpoint(dir:) for a single-file mlx checkpoint."""
+    """Checkpoint(dir:) for a single-file mlx checkpoint.  Names resolve as
+    given, else with the "language_model." prefix (Checkpoint.swift:74-80)."""
 
     def __init__(self, directory: Path):
         directory = Path(directory)
         self.cfg = json.loads((directory / "config.json").read_text())
-        self.t = load_file(str(directory / "model.safetensors"))
+        raw = load_file(str(directory / "model.safetensors"))
+        pre = "language_model."
+        self.t = dict(raw)
+        for k, v in raw.items():
+            if k.startswith(pre) and k[len(pre):] not in raw:
+                self.t[k[len(pre):]] = v
         q = self.cfg.get("quantization") or {}
         self.default = (q["group_size"], q["bits"]) if "group_size" in q and "bits" in q else None
         self.overrides = {k: (v["group_size"], v["bits"]) for k, v in q.items()
@@ -92,8 +128,9 @@ def rms_norm(x: np.ndarray, w, eps: float) -> np.ndarray:
 class TinyQwen:
     def __init__(self, directory: Path):
         self.ck = TinyCheckpoint(directory)
-        c = self.ck.cfg
+        c = text_config(self.ck.cfg)
         self.c = c
+        self.split = c["split_layout"]
         self.D = c["hidden_size"]
         self.eps = c.get("rms_norm_eps", 1e-6)
         self.L = c["num_hidden_layers"]
@@ -134,7 +171,7 @@ class TinyQwen:
         hd = c["head_dim"]
         return dict(q_norm_w=ck.tensor(p + "q_norm.weight"), k_norm_w=ck.tensor(p + "k_norm.weight"),
                     H=c["num_attention_heads"], KVH=c["num_key_value_heads"], hd=hd,
-                    rot=int(hd * c.get("partial_rotary_factor", 0.25)), theta=float(c["rope_theta"]), eps=self.eps)
+                    rot=int(hd * c["partial_rotary_factor"]), theta=c["rope_theta"], eps=self.eps)
 
     def attention_projections(self, x: np.ndarray, i: int):
         """q_proj (query | gate per head), k_proj and v_proj outputs."""
@@ -147,7 +184,7 @@ class TinyQwen:
         out, _, _ = A.attention_core(q_out, k, v, **self.attention_params(i))
         return (out @ self.ck.module_weight(f"model.layers.{i}.self_attn.o_proj").T).astype(f32)
 
-    # -- gated DeltaNet, fused interleaved layout (QwenCPUModel.swift:371-496)
+    # -- gated DeltaNet, either projection layout (QwenCPUModel.swift:371-496)
     def deltanet_params(self, i: int):
         """Layer i's DeltaNet shapes and small parameters for deltanet_core."""
         c, ck = self.c, self.ck
@@ -158,15 +195,25 @@ class TinyQwen:
                     dk=c["linear_key_head_dim"], dv=c["linear_value_head_dim"], eps=self.eps)
 
     def deltanet_projections(self, x: np.ndarray, i: int):
-        """The fused projections' outputs (in_proj_qkvz, in_proj_ba)."""
+        """The projections' outputs: (in_proj_qkvz, in_proj_ba) in the fused
+        layout, (in_proj_qkv, in_proj_z, in_proj_b, in_proj_a) in the split."""
         p = f"model.layers.{i}.linear_attn."
-        return (x @ self.ck.module_weight(p + "in_proj_qkvz").T).astype(f32), \
-            (x @ self.ck.module_weight(p + "in_proj_ba").T).astype(f32)
+        names = ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a") if self.split else ("in_proj_qkvz", "in_proj_ba")
+        return tuple((x @ self.ck.module_weight(p + n).T).astype(f32) for n in names)
+
+    def deltanet_inputs(self, x: np.ndarray, i: int):
+        """(mixed [q|k|v], z, b, a) of the core: the split layout's
+        projections are these already (QwenCPUModel.swift:415-420); the fused
+        ones are de-interleaved per key head."""
+        prm = self.deltanet_params(i)
+        pr = self.deltanet_projections(x, i)
+        if self.split:
+            return pr
+        return D.deinterleave(pr[0], pr[1], prm["nk"], prm["nv"], prm["dk"], prm["dv"])
 
     def deltanet_forward(self, x: np.ndarray, i: int) -> np.ndarray:
         prm = self.deltanet_params(i)
-        qkvz, ba = self.deltanet_projections(x, i)
-        mixed, z, b, a = D.deinterleave(qkvz, ba, prm["nk"], prm["nv"], prm["dk"], prm["dv"])
+        mixed, z, b, a = self.deltanet_inputs(x, i)
         y, _, _ = D.deltanet_core(mixed, z, b, a, **prm)
         return (y @ self.ck.module_weight(f"model.layers.{i}.linear_attn.out_proj").T).astype(f32)
 

@@ -523,7 +523,9 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
     };
 
     // ---- the slice's scales and biases into s_tab, every load at once
-    // (rows of 4-byte aligned words: an even group count per row)
+    // (4-byte words of an even group count per row; 2-byte entries may
+    // start 2 bytes past a word boundary, and are then taken from the two
+    // aligned words around them with a byte shift: no branch around the loads)
     {
         constexpr int ES = ST == SWQ_F32 ? 4 : 2;
         constexpr int WPE = kBlockG * ES / 4;  // words per (operand, array, column)
@@ -538,7 +540,17 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(const GemmArgs a) {
             const int c = min(nb * a.col_block + (lc >> 4) * a.col_wave + j * a.col_op + (lc & 15), N - 1);
             const uint8_t *base = arr ? (j ? bbase[1] : bbase[0]) : (j ? sbase[1] : sbase[0]);
             const int64_t byte = (static_cast<int64_t>(c) * (K / kGroupK) + gb) * ES + 4 * min(q, valid - 1);
-            v[u] = *reinterpret_cast<const uint32_t *>(base + byte);
+            if constexpr (ES == 4) {
+                v[u] = *reinterpret_cast<const uint32_t *>(base + byte);
+            } else {
+                // mis = 0 or 2; the second word is read only when the entries
+                // straddle it (it lies in the same aligned word as their end)
+                const uintptr_t pa = reinterpret_cast<uintptr_t>(base + byte);
+                const uint32_t mis = static_cast<uint32_t>(pa & 3u);
+                const uint32_t *w = reinterpret_cast<const uint32_t *>(pa & ~static_cast<uintptr_t>(3));
+                const uint32_t w0 = w[0], w1 = w[mis ? 1 : 0];
+                v[u] = __builtin_amdgcn_alignbyte(w1, w0, mis);
+            }
         }
 #pragma unroll
         for (int u = 0; u < PER; ++u) s_tab[tid + u * kPfThreads] = v[u];
@@ -1491,9 +1503,11 @@ int check_prefill_layer(const swq_moe_layer *l, int T) {
     const int H = l->hidden, E = l->num_experts, I = l->moe_intermediate;
     int st;
     if ((st = check_mfma(&l->router, E, H, false, E, false)) != SWQ_OK) return st;
-    // the router GEMM stages its scales and biases as aligned 4-byte words
-    if (((reinterpret_cast<uintptr_t>(l->router.scales) + l->router.s_off) % 4 != 0) ||
-        ((reinterpret_cast<uintptr_t>(l->router.biases) + l->router.b_off) % 4 != 0))
+    // the router GEMM stages f32 scales and biases as aligned 4-byte words
+    // (2-byte ones at any even offset)
+    if (l->router.scales_type == SWQ_F32 &&
+        (((reinterpret_cast<uintptr_t>(l->router.scales) + l->router.s_off) % 4 != 0) ||
+         ((reinterpret_cast<uintptr_t>(l->router.biases) + l->router.b_off) % 4 != 0)))
         return SWQ_ERR_MISALIGNED;
     if ((st = check_mfma(&l->gate, I, H, true, E)) != SWQ_OK) return st;
     if ((st = check_mfma(&l->up, I, H, true, E)) != SWQ_OK) return st;

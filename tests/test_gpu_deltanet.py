@@ -12,7 +12,13 @@ and from a random state at a position past the ring's wrap, and the tiny
 4-bit qwen3_next model with every DeltaNet layer (projections, step,
 out_proj), post-attention norm, MoE block and lm_head on the device
 (attention on the host) against mlx's logits (2e-3,
-FixtureForwardTests.swift:94-95) and greedy ids."""
+FixtureForwardTests.swift:94-95) and greedy ids; the tiny f32 qwen3_5 model
+(split projections, nested config, "language_model." names) with every
+DeltaNet step on the device, its parameters read through the library's
+checkpoint loader, against mlx's per-layer outputs and greedy ids
+(FixtureForwardTests.swift:55-82).  That model's weights are f32: its
+projections, attention and MoE blocks (quantized-only on the device) run in
+the oracle."""
 
 import json
 from pathlib import Path
@@ -156,3 +162,50 @@ def test_tiny_q4_model_with_device_deltanet_matches_mlx():
     assert diff < 2e-3, diff
     want = json.loads((G / "tiny_forward_q4.json").read_text())["greedy_next_tokens"]
     assert np.argmax(got, axis=-1).tolist() == want
+
+
+def test_tiny_q35_model_with_device_deltanet_matches_mlx():
+    import torch
+    from safetensors.numpy import load_file
+    from oracle.qwen_tiny import rms_norm, text_config
+    from oracle import moe_ref as R
+    from swiftlet_amd.checkpoint import Checkpoint
+    d = G / "tiny-model-q35"
+    c = text_config(json.loads((d / "config.json").read_text()))
+    ck, m = Checkpoint(d), TinyQwen(d)
+    assert c["split_layout"] and m.split
+    fx = load_file(str(G / "tiny_forward_q35.safetensors"))
+    toks = fx["input_ids"][0]
+    S = len(toks)
+    h = fx["embed"][0].astype(np.float32)
+    for i in range(m.L):
+        x = rms_norm(h, m.ck.tensor(f"model.layers.{i}.input_layernorm.weight"), m.eps)
+        if m.is_linear(i):
+            p = f"model.layers.{i}.linear_attn."
+            # unprefixed names, resolved by the library to language_model.*
+            blk = DeltaNetGPU(c["linear_num_key_heads"], c["linear_num_value_heads"], c["linear_key_head_dim"],
+                              c["linear_value_head_dim"], c["linear_conv_kernel_dim"], SWQ_DELTA_SPLIT,
+                              c["rms_norm_eps"], *(ck.load(p + n).float() for n in
+                                                   ("conv1d.weight", "A_log", "dt_bias", "norm.weight")))
+            mixed, z, b, a = m.deltanet_inputs(x, i)
+            qkvz = torch.from_numpy(np.ascontiguousarray(np.concatenate([mixed, z], -1), np.float32)).cuda()
+            ba = torch.from_numpy(np.ascontiguousarray(np.concatenate([b, a], -1), np.float32)).cuda()
+            state = blk.new_state()
+            y = torch.stack([blk.step(qkvz[t], ba[t], state, t) for t in range(S)])
+            torch.cuda.synchronize()
+            want, _, _ = D.deltanet_core(mixed, z, b, a, **m.deltanet_params(i))
+            err = _rel(y.cpu().numpy(), want)
+            print(f"q35 layer {i}: device DeltaNet vs oracle {err:.2e}", flush=True)
+            assert err < 1e-5, (i, err)
+            r = (y.cpu().numpy() @ m.ck.module_weight(p + "out_proj").T).astype(np.float32)
+        else:
+            r = m.attention_forward(x, i)
+        h = (h + r).astype(np.float32)
+        x2 = rms_norm(h, m.ck.tensor(f"model.layers.{i}.post_attention_layernorm.weight"), m.eps)
+        h = (h + R.moe_forward(x2, m.moe_layer(i))[0]).astype(np.float32)
+        diff = np.abs(h - fx[f"layer_{i:02d}"][0]).max()
+        assert diff < 5e-4, (i, diff)  # chained from mlx's embedding (the oracle alone: 1.3e-5 at layer 7)
+    logits = (rms_norm(h, m.final_norm, m.eps) @ m.lm_head.T).astype(np.float32)
+    assert np.abs(logits - fx["logits"][0]).max() < 0.05
+    want = json.loads((G / "tiny_forward_q35.json").read_text())["greedy_next_tokens"]
+    assert np.argmax(logits, axis=-1).tolist() == want

@@ -227,3 +227,32 @@ def test_prefill_f32_scales_equal_f16_scales(name, x_dtype):
     ob, ib, wb = b.prefill(x)
     torch.cuda.synchronize()
     assert torch.equal(ia, ib) and torch.equal(wa, wb) and torch.equal(oa, ob)
+
+
+def test_prefill_router_scales_two_bytes_past_a_word():
+    """2-byte router scales and biases that start 2 bytes past a 4-byte
+    boundary (a layer swq_moe_decode takes) give the same prefill, bit for
+    bit, as the same values on aligned words."""
+    import torch
+    from swiftlet_amd.engine import GPULinear
+    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    layer = moe.synth_layer(shape, helpers.SEED, 0)
+    x, _ = _x(helpers.SEED + 90, 24, shape.hidden)
+    ref_out, ref_ids, ref_w = layer.prefill(x)
+    r = layer.router
+
+    def shifted(t):
+        buf = torch.zeros(t.numel() + 8, dtype=torch.uint8, device=t.device)
+        buf[2:2 + t.numel()].copy_(t)
+        return buf
+
+    r2 = GPULinear(r.w, shifted(r.scales), shifted(r.biases), r.out_dim, r.in_dim, r.group_size, r.bits,
+                   r.scales_type, w_off=r.w_off, s_off=r.s_off + 2, b_off=r.b_off + 2)
+    assert (r2.scales.data_ptr() + r2.s_off) % 4 == 2
+    layer2 = moe.MoELayerGPU(r2, layer.gate, layer.up, layer.down, layer.shared_gate, layer.shared_up,
+                             layer.shared_down, layer.shared_expert_gate, layer.top_k, layer.norm_topk_prob)
+    out, ids, w = layer2.prefill(x)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ref_ids)
+    assert torch.equal(w, ref_w)
+    assert torch.equal(out, ref_out)

@@ -109,6 +109,24 @@ def test_sharded_checkpoint_with_prefixed_names(tmp_path):
     assert c.quant_spec("model.layers.1.mlp.gate") == (32, 4)
 
 
+def test_qwen35_checkpoint_resolves_unprefixed_names():
+    """The tiny qwen3_5 fixture stores every weight as language_model.*: each
+    resolves by its unprefixed name with the stored bytes, and it holds the
+    split DeltaNet projections the loader's layout choice looks for."""
+    from safetensors.numpy import load_file
+    d = FIXTURES / "tiny-model-q35"
+    raw = load_file(str(d / "model.safetensors"))
+    c = Checkpoint(d)
+    assert len(c.tensor_names) == len(raw)
+    for stored, arr in raw.items():
+        assert stored.startswith("language_model.")
+        n = stored[len("language_model."):]
+        assert c.raw_tensor(n) == arr.tobytes(), n
+    assert c.contains("model.layers.0.linear_attn.in_proj_qkv.weight")
+    assert not c.contains("model.layers.0.linear_attn.in_proj_qkvz.weight")
+    assert c.quant_spec("model.layers.0.mlp.gate") is None  # stored unquantized
+
+
 def test_repack_round_trip(container):
     """QpackTests.repackRoundTrip (QpackTests.swift:15-63)."""
     cfg = json.loads((Q4 / "config.json").read_text())

@@ -2,7 +2,9 @@
 copied from Swiftlet's fixtures/).  Mirrors FixtureForwardTests
 (FixtureForwardTests.swift:21-102): layer-local checks of every decoder layer
 from the reference input (5e-4), end-to-end logits (0.05 for f32, 2e-3 for
-the 4-bit model) and greedy ids.  Every layer contains the MoE block, so these
+the 4-bit model) and greedy ids, for the qwen3_next models and the qwen3_5
+one (nested text_config, rope_parameters, split DeltaNet projections,
+"language_model." names; :55-82).  Every layer contains the MoE block, so these
 pin the oracle's router softmax, top-k, renormalisation, SwiGLU experts,
 shared-expert gate and (through the 4-bit model) the MLX affine dequant
 against mlx itself."""
@@ -28,6 +30,11 @@ def f32_model():
 @pytest.fixture(scope="module")
 def q4_model():
     return TinyQwen(G / "tiny-model-q4"), load_file(str(G / "tiny_forward_q4.safetensors"))
+
+
+@pytest.fixture(scope="module")
+def q35_model():
+    return TinyQwen(G / "tiny-model-q35"), load_file(str(G / "tiny_forward_q35.safetensors"))
 
 
 def test_tiny_model_layers_match_mlx(f32_model):
@@ -86,3 +93,56 @@ def test_planted_mistake_is_caught(q4_model):
     finally:
         R.dequantize = orig
     assert np.abs(logits - fx["logits"][0]).max() > 2e-3
+
+
+def test_tiny_q35_model_layers_match_mlx(q35_model):
+    """FixtureForwardTests.tinyQwen35ModelMatchesMLX (:55-82): the split
+    layout is detected, every layer (DeltaNet and attention) from mlx's input
+    within 5e-4 of mlx's output."""
+    m, fx = q35_model
+    assert m.split and m.c["weight_prefix"] == "language_model."
+    assert m.c["rope_theta"] == 1e7 and m.c["partial_rotary_factor"] == 0.25
+    toks = fx["input_ids"][0]
+    assert np.abs(m.embed[toks] - fx["embed"][0]).max() < 1e-6
+    prev = fx["embed"][0]
+    for i in range(m.L):
+        ref = fx[f"layer_{i:02d}"][0]
+        diff = np.abs(m.layer_forward(prev, i) - ref).max()
+        assert diff < 5e-4, (i, "deltanet" if m.is_linear(i) else "attention", diff)
+        prev = ref
+
+
+def test_tiny_q35_model_logits_and_greedy_match_mlx(q35_model):
+    m, fx = q35_model
+    logits, _, greedy = m.forward(fx["input_ids"][0])
+    assert np.abs(logits - fx["logits"][0]).max() < 0.05
+    want = json.loads((G / "tiny_forward_q35.json").read_text())["greedy_next_tokens"]
+    assert greedy.tolist() == want
+
+
+def test_q35_split_projections_are_pinned(q35_model):
+    """Planted mistakes in the split layout, each caught by the layer-local
+    bar: b and a swapped, or the fused layout's de-interleave applied to the
+    split projections' outputs."""
+    from oracle import deltanet_ref as D
+    m, fx = q35_model
+    x = fx["embed"][0]
+    ref = fx["layer_00"][0]
+    assert np.abs(m.layer_forward(x, 0) - ref).max() < 5e-4
+    orig = m.deltanet_inputs
+    try:
+        def swapped(xx, i):
+            mixed, z, b, a = orig(xx, i)
+            return mixed, z, a, b
+        m.deltanet_inputs = swapped
+        assert np.abs(m.layer_forward(x, 0) - ref).max() > 5e-4
+
+        def fused(xx, i):
+            mixed, z, b, a = orig(xx, i)
+            prm = m.deltanet_params(i)
+            return D.deinterleave(np.concatenate([mixed, z], -1), np.concatenate([b, a], -1),
+                                  prm["nk"], prm["nv"], prm["dk"], prm["dv"])
+        m.deltanet_inputs = fused
+        assert np.abs(m.layer_forward(x, 0) - ref).max() > 5e-4
+    finally:
+        m.deltanet_inputs = orig
