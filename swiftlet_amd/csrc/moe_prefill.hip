@@ -1562,15 +1562,20 @@ int launch_gemm(const swq_qlinear &lin, const GemmArgs &a, int blocks, hipStream
     return launch_status();
 }
 
-// Waves per workgroup and ring depths of the DMA GEMMs, chosen so that two
-// workgroups fit in a CU's 160 KB of LDS: 8 waves (128 gate/up or 256 down
-// columns per workgroup: the tile's activation rows are shared by twice the
-// columns) except for 8-bit codes with two activation planes.
-int dma_waves(int bits, int npl) { return bits == 8 && npl == 2 ? 4 : 8; }
+// Waves per workgroup and ring depths of the DMA GEMMs.  Down and 8-bit
+// gate/up (bf16 x): 8 waves (256 down or 128 gate/up columns per workgroup:
+// the tile's activation rows are shared by twice the columns), two
+// workgroups in a CU's 160 KB of LDS.  4-bit gate/up with bf16 x: 4 waves
+// (64 columns, 49 KB), three workgroups per CU: twice the workgroups, which
+// spreads the last, partly filled round of tiles over more CUs (gate/up
+// 113 -> 108.5 us on the 512-token chunk; down at 4 waves fits only two
+// per CU and loses, 80 -> 87 us).  8-bit codes with two activation planes:
+// 4 waves.
+int dma_waves(int bits, int npl) { return (bits == 8 && npl == 2) || (bits == 4 && npl == 1) ? 4 : 8; }
 
 template <int BITS, int NPL, int EPI>
 void launch_dma_st(int stype, const GemmArgs &a, int blocks, hipStream_t s) {
-    constexpr int W = BITS == 8 && NPL == 2 ? 4 : 8;
+    constexpr int W = (BITS == 8 && NPL == 2) || (BITS == 4 && NPL == 1) ? 4 : 8;
     constexpr int DA = BITS == 4 && NPL == 1 ? 3 : 2;
     constexpr int DB = DA + 1;
     const dim3 th(64 * W);
