@@ -48,11 +48,12 @@ MEASURED_TRAFFIC = {
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage1"): 2_757_384,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage2"): 9_698_457,
     ("qwen3.6-35b-a3b-q4-b1", "moe_stage3"): 5_713_406,
+    ("qwen3.6-35b-a3b-q8-b4", "moe_fused"): 115_208_204,
     ("qwen3.6-35b-a3b-q8-b4", "moe_stage1"): 5_580_301,
     ("qwen3.6-35b-a3b-q8-b4", "moe_stage2"): 69_525_396,
     ("qwen3.6-35b-a3b-q8-b4", "moe_stage3"): 36_430_644,
-    ("qwen3.6-35b-a3b-q4-prefill512", "gate_up"): 347_003_996,
-    ("qwen3.6-35b-a3b-q4-prefill512", "down"): 209_619_225,
+    ("qwen3.6-35b-a3b-q4-prefill512", "gate_up"): 344_679_983,
+    ("qwen3.6-35b-a3b-q4-prefill512", "down"): 209_619_859,
 }
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
