@@ -322,24 +322,31 @@ __device__ __forceinline__ void down_slots(const MoEArgs &a, const Slots &sl, in
     }
 }
 
-// The shared expert's down tile for every token b: part[P + b][row - r0].
+// The shared expert's down rows [r0, r0 + rows3) for every token b:
+// part[P + b][row - r0].  rows3 is the routed down matrix's tile height; the
+// shared matrix's plan (a longer row: fewer rows per tile) may need several
+// of its tiles for it.
 template <int XDT, int BITS, int CPL, int ES, int XF>
 __device__ __forceinline__ void down_shared(const MoEArgs &a, int r0, float (*part)[kRows3], int lane) {
     static_assert(XDT == SWQ_F32 && CPL == 1, "down rows read fp32 activations, one chunk per lane");
     const LaneMap lm = lane_map(a.sh_down.lpr_log2, lane);
     const int end = min(r0 + a.rows3, a.H);
-    RowTile<BITS, 1, ES> t;
-    load_tile(t, a.sh_down, 0, lm, r0, end);
-    XRaw<SWQ_F32, BITS, 1> xa, xb;
-    load_xraw<SWQ_F32>(xa, a.sh_down, lm, a.h_sh, 0);
     const int P = a.B * a.K;
+    constexpr int RI = RowTile<BITS, 1, ES>::kRI;
 #pragma unroll 1
-    for (int b = 0; b < a.B; b += 2) {
-        if (b + 1 < a.B) load_xraw<SWQ_F32>(xb, a.sh_down, lm, a.h_sh, static_cast<int64_t>(b + 1) * a.Is);
-        down_tile_row<BITS, ES, XF>(a.sh_down, lm, t, xa, r0, end, part[P + b]);
-        if (b + 1 >= a.B) break;
-        if (b + 2 < a.B) load_xraw<SWQ_F32>(xa, a.sh_down, lm, a.h_sh, static_cast<int64_t>(b + 2) * a.Is);
-        down_tile_row<BITS, ES, XF>(a.sh_down, lm, t, xb, r0, end, part[P + b + 1]);
+    for (int rp = r0; rp < end; rp += RI * lm.rpw) {
+        RowTile<BITS, 1, ES> t;
+        load_tile(t, a.sh_down, 0, lm, rp, end);
+        XRaw<SWQ_F32, BITS, 1> xa, xb;
+        load_xraw<SWQ_F32>(xa, a.sh_down, lm, a.h_sh, 0);
+#pragma unroll 1
+        for (int b = 0; b < a.B; b += 2) {
+            if (b + 1 < a.B) load_xraw<SWQ_F32>(xb, a.sh_down, lm, a.h_sh, static_cast<int64_t>(b + 1) * a.Is);
+            down_tile_row<BITS, ES, XF>(a.sh_down, lm, t, xa, rp, end, part[P + b] + (rp - r0));
+            if (b + 1 >= a.B) break;
+            if (b + 2 < a.B) load_xraw<SWQ_F32>(xa, a.sh_down, lm, a.h_sh, static_cast<int64_t>(b + 2) * a.Is);
+            down_tile_row<BITS, ES, XF>(a.sh_down, lm, t, xb, rp, end, part[P + b + 1] + (rp - r0));
+        }
     }
 }
 

@@ -175,6 +175,33 @@ def test_fused_batch_equals_staged(name, batch):
     _check_against_oracle(shape, synth.bf16_to_f32(xb), of, i_f.cpu().numpy(), w_f.cpu().numpy())
 
 
+@pytest.mark.parametrize("bits,Is", [(4, 2048), (8, 1024)])
+@pytest.mark.parametrize("batch", [1, 2, 4])
+def test_fused_wide_intermediates(bits, Is, batch):
+    """Routed intermediates of 1024 rows and shared ones of 2048 (4-bit: the
+    compiled maximum) or 1024 (8-bit: the widest one-chunk-per-lane down
+    row): a wave's share of the owned slots' and of every token's shared
+    activations takes several polling rounds (one round covers 128 routed and
+    256 shared pairs per wave), on the single and the batched launches; equal
+    bit for bit to the three launches and within the bar of the oracle.  The
+    three launches' shared down rows then need several of that matrix's
+    tiles per workgroup (its rows are longer than the routed down rows)."""
+    import torch
+    shape = synth.MoEShape("wide-inter", 256, 64, 8, 1024, Is, expert_bits=bits, router_bits=8, group=64,
+                           norm_topk_prob=True)
+    print(f"wide intermediates: bits {bits} batch {batch}", flush=True)
+    gpu = moe.synth_layer(shape, 91, 0)
+    xb = synth.activations_bf16(92 + batch, batch, shape.hidden)
+    x = helpers.bf16_bits_to_torch(xb)
+    ws_f, ws_s = gpu.new_workspace(batch), gpu.new_workspace(batch)
+    (of, i_f, w_f), (os_, i_s, w_s) = _pair(gpu, shape, x, "f32", ws_f, ws_s)
+    from swiftlet_amd import _lib
+    assert gpu.workspace_status(ws_f) == _lib.SWQ_OK
+    assert torch.equal(i_f, i_s) and torch.equal(w_f, w_s)
+    assert torch.equal(of, os_)
+    _check_against_oracle(shape, synth.bf16_to_f32(xb), of, i_f.cpu().numpy(), w_f.cpu().numpy(), seed=91)
+
+
 def test_fused_epochs_across_calls():
     """One workspace, alternating layers and fresh inputs: each call consumes
     only what it produced itself (stale words of earlier calls carry older
