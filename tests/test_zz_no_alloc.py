@@ -5,8 +5,9 @@ second with a smaller input (batch 4 on the three launches, then batch 1 on
 the single launch), then a different, smaller layer sharing the same array,
 then the first layer again; f32 activations, bf16 outputs and the
 accumulate flag; calls between swq_moe_decode_norm calls; the entry point
-captured in a HIP graph and replayed.  Every test ends with the array's stall
-record clear.  A layer whose workspace exceeds the array is refused before
+captured in a HIP graph and replayed; in a fresh process, a first call made
+under capture is refused and the next one outside capture recovers.  Every
+test ends with the array's stall record clear.  A layer whose workspace exceeds the array is refused before
 any launch."""
 
 import ctypes
@@ -168,3 +169,55 @@ def test_noalloc_replays_under_graph_capture():
         assert torch.equal(w, ref_w)
         assert torch.equal(out, ref)
     assert _status(lib) == _lib.SWQ_OK
+
+
+_FIRST_UNDER_CAPTURE = r"""
+import ctypes, sys
+import torch
+from swiftlet_amd import _lib, moe, synth
+from tests import helpers
+lib = _lib.load()
+layer = moe.synth_layer(synth.SHAPES["qwen3.6-35b-a3b-q4"], helpers.SEED, 0)
+H, K = layer.hidden, layer.top_k
+x = helpers.bf16_bits_to_torch(synth.activations_bf16(helpers.SEED + 80, 1, H))
+out = torch.empty((1, H), dtype=torch.float32, device="cuda")
+ids = torch.empty((1, K), dtype=torch.int32, device="cuda")
+w = torch.empty((1, K), dtype=torch.float32, device="cuda")
+def call(stream=None):
+    return lib.swq_moe_decode_noalloc(ctypes.byref(layer._c), x.data_ptr(), _lib.SWQ_BF16, 1, out.data_ptr(),
+                                      _lib.SWQ_F32, ids.data_ptr(), w.data_ptr(), 0, stream)
+torch.cuda.synchronize()
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.stream(side):
+    with torch.cuda.graph(graph, stream=side):
+        out.add_(0.0)
+        st = call(ctypes.c_void_p(side.cuda_stream))
+assert st == _lib.SWQ_ERR_INVALID_ARGUMENT, st   # the first call, under capture: refused, nothing latched
+_lib.check(call(), "noalloc after capture")       # the set-up runs now
+torch.cuda.synchronize()
+ref, ref_ids, ref_w = layer.decode(x)
+torch.cuda.synchronize()
+assert torch.equal(out, ref) and torch.equal(ids, ref_ids) and torch.equal(w, ref_w)
+layer.decode(x, path="fused")                     # the device still takes the single launch
+assert lib.swq_moe_workspace_status(None, 0, 1, None) == _lib.SWQ_OK
+print("first-under-capture: ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_recovers():
+    """In a fresh process, the very first no-alloc call made under stream
+    capture is refused without latching anything: the next call outside
+    capture sets the array up and equals swq_moe_decode, and the device
+    still takes the single launch (the set-up's probe ran then)."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, PYTHONPATH=root + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    print("fresh process: first no-alloc call under capture", flush=True)
+    r = subprocess.run([sys.executable, "-c", _FIRST_UNDER_CAPTURE], cwd=root, env=env, capture_output=True,
+                       text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "first-under-capture: ok" in r.stdout
