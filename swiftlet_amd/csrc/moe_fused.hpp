@@ -342,6 +342,74 @@ __device__ __forceinline__ void fetch_acts(const uint64_t *src, int p0, int p1, 
     }
 }
 
+// poll_words split in two: issue() sends the first round of loads, finish()
+// checks them and polls on for the words still stale, so that other work
+// can run while the first round is in flight.
+template <int N>
+struct EarlyPoll {
+    const uint64_t *p[N];
+    bool pend[N];
+    uint64_t w[N];
+    __device__ __forceinline__ void issue() {
+#pragma unroll
+        for (int c = 0; c < N; ++c) w[c] = pend[c] ? get_pair(p[c]) : 0;
+    }
+    __device__ __forceinline__ void finish(uint32_t g, float (&v)[N], uint32_t *err, uint32_t bit) {
+#pragma unroll
+        for (int c = 0; c < N; ++c) v[c] = 0.f;
+        for (uint32_t it = 0;; ++it) {
+            bool any = false;
+#pragma unroll
+            for (int c = 0; c < N; ++c) {
+                if (pend[c] && static_cast<uint32_t>(w[c] >> 32) == g) {
+                    v[c] = __uint_as_float(static_cast<uint32_t>(w[c]));
+                    pend[c] = false;
+                }
+                any = any || pend[c];
+            }
+            if (__ballot(any) == 0) return;
+            if (it > kSpinLimit) {
+                if ((threadIdx.x & 63) == 0) record_stall(err, bit);
+                return;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            issue();
+        }
+    }
+};
+
+// Pairs [p0, p1) of NS slots' words (at src[i], none where live_slot[i] is
+// false) into buf[i], and pairs [s0, s1) of the words at ssrc into sbuf, all
+// in each polling round: one pair of each per lane and round.
+template <int DB, int NS>
+__device__ __forceinline__ void fetch_acts_multi(const uint64_t *const (&src)[NS], uint32_t *const (&buf)[NS],
+                                                 const bool (&live_slot)[NS], int p0, int p1, const uint64_t *ssrc,
+                                                 int s0, int s1, uint32_t *sbuf, uint32_t g, int lane,
+                                                 uint32_t *err) {
+    for (int r = 0; p0 + r < p1 || s0 + r < s1; r += kWave) {
+        constexpr int N = 2 * NS + 2;
+        const uint64_t *pp[N];
+        bool live[N];
+        const int pr = p0 + r + lane, sr = s0 + r + lane;
+        const int pc = min(pr, max(p1 - 1, p0)), sc = min(sr, max(s1 - 1, s0));
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            live[2 * i] = live[2 * i + 1] = live_slot[i] && pr < p1;
+            pp[2 * i] = src[i] + pair_first<DB>(pc);
+            pp[2 * i + 1] = src[i] + pair_second<DB>(pc);
+        }
+        live[2 * NS] = live[2 * NS + 1] = sr < s1;
+        pp[2 * NS] = ssrc + pair_first<DB>(sc);
+        pp[2 * NS + 1] = ssrc + pair_second<DB>(sc);
+        float v[N];
+        poll_words<N>(pp, live, g, v, err, 1u);
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+            if (live[2 * i]) store_pair_lds<DB>(buf[i], pr, v[2 * i], v[2 * i + 1]);
+        if (live[2 * NS]) store_pair_lds<DB>(sbuf, sr, v[2 * NS], v[2 * NS + 1]);
+    }
+}
+
 // Pairs [p0, p1) of the words at src into buf and [s0, s1) of those at ssrc
 // into sbuf, each at most a wave's 64, polled together in one round per
 // lane (the second set is ready earlier: it rides the first's wait).
@@ -420,6 +488,9 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     __shared__ float s_w[SWQ_MAX_TOPK];
     __shared__ __attribute__((aligned(16))) uint32_t s_hb[kMaxInterFused];   // a routed slot's activations
     __shared__ __attribute__((aligned(16))) uint32_t s_hsh[kMaxInterFused];  // the shared expert's
+    // two split slots' activations (512 experts and more)
+    __shared__ __attribute__((aligned(16))) uint32_t s_hb2[M >= 8 ? kMaxInterFused : 4];
+    __shared__ __attribute__((aligned(16))) uint32_t s_hb3[M >= 8 ? kMaxInterFused : 4];
     __shared__ float s_cmb[SWQ_MAX_TOPK * kMaxCombineRows];
     __shared__ float s_shd[kMaxCombineRows];  // shared-expert down rows of the combine rows
     __shared__ float s_sg;                    // shared-expert gate logit
@@ -592,7 +663,9 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
         rounds_init(rd, v, a.E, lane);
         // the rounds up to this group's last owned slot; the rest after the
         // routed work
-        const int own_last = a.K > grp ? grp + kGroups * ((a.K - 1 - grp) / kGroups) : -1;
+        int own_last = a.K > grp ? grp + kGroups * ((a.K - 1 - grp) / kGroups) : -1;
+        // (512 experts and more: picks past the eighth are every group's)
+        if constexpr (M >= 8) own_last = a.K > kGroups ? a.K - 1 : own_last;
         rounds_run(rd, own_last + 1, lane, s_ids);
         SWQ_STAMP(3);
     }
@@ -671,72 +744,164 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
                 if (s + kGroups < a.K) __syncthreads();
             }
         } else {
-            // 512 experts and more: the layers whose top-k exceeds the eight
-            // groups (a group then owns two slots) run the gate/up rows of
-            // every owned slot first, then each slot's activations and down
-            // rows, so that the second slot's gate/up rows need not wait for
-            // the first slot's activation round trip (80B step 21.5 -> 20.7
-            // us; the one-slot groups of the smaller layers lose 0.4 us this
-            // way, so they keep the slot-major loop)
-            for (int s = grp; s < a.K; s += kGroups) {
-                const int64_t e = min(wait_lds_nonneg(&s_ids[s], a.err), a.E - 1);
-                RowTile<GB, GC, 2, GRI> tg, tu;
-                for (int t = t0; t < a.gu_tpe; t += NPG * kFusedWaves) {
-                    const int row0 = t * GRI * lmg.rpw;
-                    load_tile(tg, a.gate, e, lmg, row0, a.I);
-                    load_tile(tu, a.up, e, lmg, row0, a.I);
-                    float rg[GRI], ru[GRI];
-                    dot_rows2(rg, ru, tg, tu, a.gate, a.up, xg, lmg);
-                    if (lmg.j == lmg.lpr - 1) {
-    #pragma unroll
-                        for (int i = 0; i < GRI; ++i) {
-                            const int row = row0 + i * lmg.rpw + lmg.q;
-                            if (row < a.I)
-                                put_pair_group(a.h_x + static_cast<int64_t>(s) * a.I + row, swiglu(rg[i], ru[i]), g,
-                                               a.local);
-                        }
+            // 512 experts and more: picks past the eighth (the 80B layer's
+            // top-10) are split over every workgroup instead of falling to
+            // groups 0 and 1 as a second slot.  Split slot j's gate/up and
+            // down tiles go one per workgroup to wave 1 + j (its tiles
+            // issued with the wave's own slot's, so that they are in when the
+            // own slot's dot products end); its activations cross XCDs, two
+            // split slots' in one polling round once the own slot's down rows
+            // are done.
+            const int nsplit = max(a.K - kGroups, 0);
+            const int js = (wave + kFusedWaves - 1) % kFusedWaves;  // this wave's split slot
+            const bool own = grp < a.K;
+            const bool spl = js < nsplit;
+            // that slot's tiles on this wave: b, b + NB, ... (one wave of
+            // every workgroup takes each split slot)
+            const int t_sp = b, sp_step = NB;
+            auto gate_up_rows = [&](int s, int64_t e, int row0, int local, const RowTile<GB, GC, 2, GRI> &tg,
+                                    const RowTile<GB, GC, 2, GRI> &tu) {
+                float rg[GRI], ru[GRI];
+                dot_rows2(rg, ru, tg, tu, a.gate, a.up, xg, lmg);
+                if (lmg.j == lmg.lpr - 1) {
+#pragma unroll
+                    for (int i = 0; i < GRI; ++i) {
+                        const int row = row0 + i * lmg.rpw + lmg.q;
+                        if (row < a.I)
+                            put_pair_group(a.h_x + static_cast<int64_t>(s) * a.I + row, swiglu(rg[i], ru[i]), g,
+                                           local);
                     }
                 }
-                SWQ_STAMP(4);
-            }
-            for (int s = grp; s < a.K; s += kGroups) {
-                const int64_t e = min(wait_lds_nonneg(&s_ids[s], a.err), a.E - 1);
-                RowTile<DB, 1, 2, DRI> dt0;
-                // the first down tile: its loads issued once the gate/up bytes,
-                // which the step waits for first, are in; used after the
-                // activations' round trip
-                if (t0 < a.dn_tpe) load_tile(dt0, a.down, e, lmd, t0 * DRI * lmd.rpw, a.H);
-                // Without this the compiler may sink the loads below the polls
-                // and the barrier that follow (allowed across an acquire), so they
-                // would start only once the activations are in.
-                asm volatile("" ::: "memory");
-                // the slot's activations: each wave polls an eighth into LDS
-                if (sh_early && s == grp)
-                    fetch_acts_with<DB>(a.h_x + static_cast<int64_t>(s) * a.I, min(np_r, wave * q_r),
-                                        min(np_r, (wave + 1) * q_r), s_hb, a.hsh_x, min(np_s, wave * q_s),
-                                        min(np_s, (wave + 1) * q_s), s_hsh, g, lane, a.err);
-                else
-                    fetch_acts<DB>(a.h_x + static_cast<int64_t>(s) * a.I, min(np_r, wave * q_r),
-                                   min(np_r, (wave + 1) * q_r), g, s_hb, lane, a.err);
-                __syncthreads();
-                SWQ_STAMP(5);
-                for (int t = t0; t < a.dn_tpe; t += NPG * kFusedWaves) {
+            };
+            auto down_rows = [&](int s, int64_t e, RowTile<DB, 1, 2, DRI> &dt0, int t_first, int t_step,
+                                 const uint32_t *hb) {
+                for (int t = t_first; t < a.dn_tpe; t += t_step) {
                     const int row0 = t * DRI * lmd.rpw;
-                    if (t != t0) load_tile(dt0, a.down, e, lmd, row0, a.H);
+                    if (t != t_first) load_tile(dt0, a.down, e, lmd, row0, a.H);
                     float res[DRI];
-                    down_dot<DB, DRI>(res, dt0, a.down, lmd, s_hb);
+                    down_dot<DB, DRI>(res, dt0, a.down, lmd, hb);
                     if (lmd.j == lmd.lpr - 1) {
-    #pragma unroll
+#pragma unroll
                         for (int i = 0; i < DRI; ++i) {
                             const int row = row0 + i * lmd.rpw + lmd.q;
                             if (row < a.H) put_pair(a.part_x + static_cast<int64_t>(s) * a.H + row, res[i], g);
                         }
                     }
                 }
+            };
+            int64_t e_own = 0, e_sp = 0;
+            {
+                RowTile<GB, GC, 2, GRI> tg, tu, tgs, tus;
+                if (own) {
+                    e_own = min(wait_lds_nonneg(&s_ids[grp], a.err), a.E - 1);
+                    if (t0 < a.gu_tpe) {
+                        load_tile(tg, a.gate, e_own, lmg, t0 * GRI * lmg.rpw, a.I);
+                        load_tile(tu, a.up, e_own, lmg, t0 * GRI * lmg.rpw, a.I);
+                    }
+                }
+                if (spl) {
+                    e_sp = min(wait_lds_nonneg(&s_ids[kGroups + js], a.err), a.E - 1);
+                    if (t_sp < a.gu_tpe) {
+                        load_tile(tgs, a.gate, e_sp, lmg, t_sp * GRI * lmg.rpw, a.I);
+                        load_tile(tus, a.up, e_sp, lmg, t_sp * GRI * lmg.rpw, a.I);
+                    }
+                }
+                asm volatile("" ::: "memory");
+                if (own) {
+                    for (int t = t0; t < a.gu_tpe; t += NPG * kFusedWaves) {
+                        const int row0 = t * GRI * lmg.rpw;
+                        if (t != t0) {
+                            load_tile(tg, a.gate, e_own, lmg, row0, a.I);
+                            load_tile(tu, a.up, e_own, lmg, row0, a.I);
+                        }
+                        gate_up_rows(grp, e_own, row0, a.local, tg, tu);
+                    }
+                    SWQ_STAMP(4);
+                }
+                if (spl) {
+                    for (int t = t_sp; t < a.gu_tpe; t += sp_step) {
+                        const int row0 = t * GRI * lmg.rpw;
+                        if (t != t_sp) {
+                            load_tile(tgs, a.gate, e_sp, lmg, row0, a.I);
+                            load_tile(tus, a.up, e_sp, lmg, row0, a.I);
+                        }
+                        gate_up_rows(kGroups + js, e_sp, row0, 0, tgs, tus);
+                    }
+                }
+                SWQ_STAMP(22);
+            }
+            // split slots 0 and 1: when a wave's share of their activations
+            // fits one polling round, its loads go out before the own slot's
+            // down rows and are checked after them
+            const int pr0 = min(np_r, wave * q_r), pr1 = min(np_r, (wave + 1) * q_r);
+            const bool early = nsplit > 0 && q_r <= kWave;
+            EarlyPoll<4> ep;
+            {
+                const int pr = pr0 + lane;
+                const int pc = min(pr, max(pr1 - 1, pr0));
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const uint64_t *src = a.h_x + static_cast<int64_t>(kGroups + u) * a.I;
+                    ep.pend[2 * u] = ep.pend[2 * u + 1] = early && u < nsplit && pr < pr1;
+                    ep.p[2 * u] = src + pair_first<DB>(pc);
+                    ep.p[2 * u + 1] = src + pair_second<DB>(pc);
+                }
+            }
+            if (own) {
+                RowTile<DB, 1, 2, DRI> dt0;
+                // the first down tile, issued before the activation polls
+                if (t0 < a.dn_tpe) load_tile(dt0, a.down, e_own, lmd, t0 * DRI * lmd.rpw, a.H);
+                // Without this the compiler may sink the loads below the polls
+                // and the barrier that follow (allowed across an acquire), so they
+                // would start only once the activations are in.
+                asm volatile("" ::: "memory");
+                // the slot's activations: each wave polls an eighth into LDS
+                if (sh_early)
+                    fetch_acts_with<DB>(a.h_x + static_cast<int64_t>(grp) * a.I, min(np_r, wave * q_r),
+                                        min(np_r, (wave + 1) * q_r), s_hb, a.hsh_x, min(np_s, wave * q_s),
+                                        min(np_s, (wave + 1) * q_s), s_hsh, g, lane, a.err);
+                else
+                    fetch_acts<DB>(a.h_x + static_cast<int64_t>(grp) * a.I, min(np_r, wave * q_r),
+                                   min(np_r, (wave + 1) * q_r), g, s_hb, lane, a.err);
+                __syncthreads();
+                SWQ_STAMP(5);
+                if (early) ep.issue();
+                asm volatile("" ::: "memory");
+                down_rows(grp, e_own, dt0, t0, NPG * kFusedWaves, s_hb);
                 SWQ_STAMP(6);
-                // s_hb is rewritten by the next slot; after the group's last one
-                // each wave goes on to the tail as soon as its own rows are done
-                if (s + kGroups < a.K) __syncthreads();
+            } else if (early) {
+                ep.issue();
+            }
+            // split slots two at a time: their activations in one polling
+            // round into s_hb2 and s_hb3 (the first round needs no barrier
+            // before it: the own slot's down rows read s_hb), then each down
+            // row of a split slot on the wave that owns the slot
+            for (int j0 = 0; j0 < nsplit; j0 += 2) {
+                const bool two = j0 + 1 < nsplit;
+                const bool mine = spl && (js == j0 || js == j0 + 1);
+                RowTile<DB, 1, 2, DRI> dts;
+                if (mine && t_sp < a.dn_tpe) load_tile(dts, a.down, e_sp, lmd, t_sp * DRI * lmd.rpw, a.H);
+                asm volatile("" ::: "memory");
+                if (j0 > 0) __syncthreads();  // s_hb2 and s_hb3 held the previous split slots' activations
+                if (j0 == 0 && early) {
+                    float v[4];
+                    ep.finish(g, v, a.err, 1u);
+                    const int pr = pr0 + lane;
+                    if (pr < pr1) {
+                        store_pair_lds<DB>(s_hb2, pr, v[0], v[1]);
+                        if (two) store_pair_lds<DB>(s_hb3, pr, v[2], v[3]);
+                    }
+                } else {
+                    const uint64_t *h0 = a.h_x + static_cast<int64_t>(kGroups + j0) * a.I;
+                    const uint64_t *src[2] = {h0, h0 + a.I};
+                    uint32_t *const buf[2] = {s_hb2, s_hb3};
+                    const bool lv[2] = {true, two};
+                    fetch_acts_multi<DB, 2>(src, buf, lv, pr0, pr1, a.hsh_x, 0, 0, s_hsh, g, lane, a.err);
+                }
+                __syncthreads();
+                SWQ_STAMP(23);
+                if (mine) down_rows(kGroups + js, e_sp, dts, t_sp, sp_step, js == j0 ? s_hb2 : s_hb3);
+                SWQ_STAMP(24);
             }
         }
     }
