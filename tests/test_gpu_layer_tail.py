@@ -118,8 +118,11 @@ def test_tiny_q4_model_with_device_layer_tails_matches_mlx(eng):
     assert np.argmax(got, axis=-1).tolist() == want
 
 
-@pytest.mark.parametrize("with_residual,shared", [(True, True), (False, True), (True, False)])
-def test_moe_decode_with_folded_norm(eng, with_residual, shared):
+@pytest.mark.parametrize("name,with_residual,shared", [
+    ("qwen3.6-35b-a3b-q4", True, True), ("qwen3.6-35b-a3b-q4", False, True), ("qwen3.6-35b-a3b-q4", True, False),
+    ("qwen3-next-80b-a3b-q4", True, True),  # top-10 of 512: the picks past the eighth as split slots
+])
+def test_moe_decode_with_folded_norm(eng, name, with_residual, shared):
     """swq_moe_decode_norm: the residual add and the post-attention RMSNorm in
     the MoE step's launch.  out - (h + r) is the MoE output of the
     normalised input: the oracle's expert ids exactly (the input's top-k
@@ -130,7 +133,8 @@ def test_moe_decode_with_folded_norm(eng, with_residual, shared):
     import torch
     from swiftlet_amd import moe, synth
     from tests import helpers
-    shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
+    shape = synth.SHAPES[name]
+    print(f"folded norm: {name} residual {with_residual} shared {shared}", flush=True)
     if not shared:  # has_shared = 0 (QwenCPUModel.swift:559-566 skips the shared expert)
         shape = synth.MoEShape("no-shared", 2048, 256, 8, 512, 0, 4)
     layer = moe.synth_layer(shape, helpers.SEED, 0, "cuda")
