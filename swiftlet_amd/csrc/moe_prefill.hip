@@ -290,15 +290,20 @@ __device__ __forceinline__ void load_bias_bs(BiasBS<ST> &bi, const uint8_t *cons
                                              int kg) {
     constexpr int W = ST == SWQ_F32 ? 8 : 4;
     constexpr int EB = ST == SWQ_F32 ? 4 : 2;
+    // scale words first: the K loop reads them (see the register pass after
+    // the first ring wait), the bias words only after it
+    auto gi = [&](int i) {
+        // group index of the word, clamped into the row (rows hold an even number of groups)
+        return min(8 * kg + (ST == SWQ_F32 ? i : 2 * i), NG - (ST == SWQ_F32 ? 1 : 2));
+    };
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < W; ++i) {
-            // group index of the word, clamped into the row (rows hold an even number of groups)
-            const int gi = min(8 * kg + (ST == SWQ_F32 ? i : 2 * i), NG - (ST == SWQ_F32 ? 1 : 2));
-            bi.b[j][i] = *reinterpret_cast<const uint32_t *>(bbase[j] + (srow[j] + gi) * EB);
-            bi.s[j][i] = *reinterpret_cast<const uint32_t *>(sbase[j] + (srow[j] + gi) * EB);
-        }
+        for (int i = 0; i < W; ++i) bi.s[j][i] = *reinterpret_cast<const uint32_t *>(sbase[j] + (srow[j] + gi(i)) * EB);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < W; ++i) bi.b[j][i] = *reinterpret_cast<const uint32_t *>(bbase[j] + (srow[j] + gi(i)) * EB);
 }
 
 // bias_term from preloaded biases/scales and the lane's group sums xv[mt]
@@ -1022,10 +1027,21 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4)))
     constexpr auto w2 = [](int n) constexpr { return (DA - 4) * n + 2 * (n + LB); };
     constexpr auto wl = [](int n) constexpr { return LB + (DA - 2) * (n + LB); };
     constexpr auto cl = [](int n) constexpr { return n < LA ? n : LA; };
-    if (0 < NG) {
-        ring_wait_sel<w0(0), w0(cl(1)), w0(cl(2)), w0(cl(3)), w0(cl(4))>(nl);
-        step(0, 0, 0);
-    }
+    if (0 < NG) ring_wait_sel<w0(0), w0(cl(1)), w0(cl(2)), w0(cl(3)), w0(cl(4))>(nl);
+    // The scale words were loaded before every ring load, so the wait above
+    // has landed them; the compiler cannot know that (it does not count the
+    // DMA loads) and would wait for them at their first use in the loop, on
+    // every pass and with a count that ignores the ring: vmcnt(0) for the
+    // last words loaded, a drain of the whole ring every other pair of
+    // groups.  Passing them through an empty asm here makes its outputs the
+    // values the loop reads, so the compiler's one wait for them is here,
+    // with a count of eight (the bias words were loaded after them).
+    if constexpr (!kScaleDma)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(bi.s[j][i]));
+    if (0 < NG) step(0, 0, 0);
     if constexpr (DA >= 3)
         if (1 < NG) {
             ring_wait_sel<w1(0), w1(cl(1)), w1(cl(2)), w1(cl(3)), w1(cl(4))>(nl);
