@@ -119,8 +119,10 @@ def test_prefill_f32_x_bf16_out():
 
 def test_prefill_skewed_512_tokens():
     """The benchmark workload: 512 tokens, Zipf(1.1)-skewed expert load.
-    Routing checked for every token, outputs for a sample against the oracle,
-    and every row against a smaller call holding only that row's token."""
+    Routing checked for every token, and every row whose k-th / (k+1)-th
+    logit gap exceeds 1e-3 (510 of the 512) against the oracle; rows also
+    equal those of a smaller call holding only some of the tokens.  The
+    oracle's pass over the rows takes ~15 s on one core."""
     import torch
     shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
     gpu = moe.synth_layer(shape, helpers.SEED, 0)
@@ -144,8 +146,11 @@ def test_prefill_skewed_512_tokens():
             p = R.softmax_row(logits[t].astype(np.float32))
             picks = R.topk_insertion(p, 8)
             assert list(ids_np[t]) == [e for e, _ in picks], t
-    # outputs of a sample
-    _check(shape, xf, out, ids_np, w_np, rows=[0, 255, 511], bias=bias, ref_layer=ref_layer)
+    # outputs of every margin-safe row
+    safe = [t for t in range(512) if margin[t] > MARGIN]
+    assert len(safe) >= 500
+    print(f"oracle over {len(safe)} rows", flush=True)
+    _check(shape, xf, out, ids_np, w_np, rows=safe, bias=bias, ref_layer=ref_layer)
     # repeat: identical
     out2, ids2, w2 = gpu.prefill(x, ws=ws, logit_bias=bias_t)
     torch.cuda.synchronize()
