@@ -230,6 +230,56 @@ __device__ __forceinline__ void poll_words(const uint64_t *const (&p)[N], const 
     }
 }
 
+// poll_words whose first round runs mid() between issuing its loads and
+// checking them: loads mid() issues then travel with the poll's instead of
+// ahead of it (loads complete in issue order, so a poll issued behind them
+// would wait for them too).  The compiler barriers keep mid()'s loads
+// between the two.
+template <int N, typename F>
+__device__ __forceinline__ void poll_words_mid(const uint64_t *const (&p)[N], const bool (&live)[N], uint32_t g,
+                                               float (&v)[N], uint32_t *err, uint32_t bit, F &&mid) {
+    bool pend[N];
+    {
+        uint64_t w[N];
+#pragma unroll
+        for (int c = 0; c < N; ++c) {
+            pend[c] = live[c];
+            v[c] = 0.f;
+            w[c] = pend[c] ? get_pair(p[c]) : 0;
+        }
+        asm volatile("" ::: "memory");
+        mid();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int c = 0; c < N; ++c)
+            if (pend[c] && static_cast<uint32_t>(w[c] >> 32) == g) {
+                v[c] = __uint_as_float(static_cast<uint32_t>(w[c]));
+                pend[c] = false;
+            }
+    }
+    // later rounds as poll_words (the words of a round die with it)
+    for (uint32_t it = 0;; ++it) {
+        bool any = false;
+#pragma unroll
+        for (int c = 0; c < N; ++c) any = any || pend[c];
+        if (__ballot(any) == 0) return;
+        if (it > kSpinLimit) {
+            if ((threadIdx.x & 63) == 0) record_stall(err, bit);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        uint64_t w[N];
+#pragma unroll
+        for (int c = 0; c < N; ++c) w[c] = pend[c] ? get_pair(p[c]) : 0;
+#pragma unroll
+        for (int c = 0; c < N; ++c)
+            if (pend[c] && static_cast<uint32_t>(w[c] >> 32) == g) {
+                v[c] = __uint_as_float(static_cast<uint32_t>(w[c]));
+                pend[c] = false;
+            }
+    }
+}
+
 // Bounded wait until the LDS word becomes non-negative; returns it (0 if the
 // wait ran out).
 __device__ __forceinline__ int32_t wait_lds_nonneg(int32_t *p, uint32_t *err) {

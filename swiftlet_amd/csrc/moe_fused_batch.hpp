@@ -26,15 +26,17 @@ constexpr int kFusedMaxSlots = 4;  // slots per XCD group: B K <= 32
 // pairs [f0, f1) of the shared expert's activations of all tokens laid end to
 // end (rows of Is words at hs, nps pairs each) into hsh: each polling round
 // takes 2 routed and NS shared pairs per lane, so the usual shapes need one
-// round trip for everything.
-template <int DB, int NS>
+// round trip for everything.  mid() runs once, between the first round's
+// loads and their check (with no pairs at all, before returning).
+template <int DB, int NS, typename F>
 __device__ __forceinline__ void fetch_slots(const uint64_t *hx, int I, int grp, int j0, int j1, int p0, int p1,
                                             uint32_t (*hbb)[kMaxInterFused], const uint64_t *hs, int Is, int nps,
                                             int f0, int f1, uint32_t (*hsh)[kMaxInterFused], uint32_t g, int lane,
-                                            uint32_t *err) {
+                                            uint32_t *err, F &&mid) {
     constexpr int N = 4 + 2 * NS;
     const int c = p1 - p0, nr = c > 0 && j1 > j0 ? (j1 - j0) * c : 0;
     const int ns = NS > 0 ? max(f1 - f0, 0) : 0;
+    if (nr <= 0 && ns <= 0) mid();
     for (int q = 0, qs = 0; q < nr || qs < ns; q += 2 * kWave, qs += NS * kWave) {
         const uint64_t *pp[N];
         bool live[N];
@@ -65,7 +67,8 @@ __device__ __forceinline__ void fetch_slots(const uint64_t *hx, int I, int grp, 
             pp[5 + 2 * u] = row + pair_second<DB>(sq[u]);
         }
         float v[N];
-        poll_words<N>(pp, live, g, v, err, 1u);
+        if (q == 0) poll_words_mid<N>(pp, live, g, v, err, 1u, mid);
+        else poll_words<N>(pp, live, g, v, err, 1u);
 #pragma unroll
         for (int u = 0; u < 2; ++u)
             if (live[2 * u]) store_pair_lds<DB>(hbb[rj[u]], rp[u], v[2 * u], v[2 * u + 1]);
@@ -314,15 +317,31 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
         }
     }
     {
-        if (nsl > 0 && dn1) {
-            load_tile(dt0, a.down, ex[0], lmd, t0 * DRI * lmd.rpw, a.H);
-            if (nsl > 1) load_tile(dt1, a.down, ex[1], lmd, t0 * DRI * lmd.rpw, a.H);
+        // The first two slots' down tiles (and on the waves from B on the
+        // shared down tile).  4-bit down rows: issued between the activation
+        // poll's loads and their check (issued first, they would hold the
+        // poll's round trip behind their own: 35B q4 at batch 4 38.8 ->
+        // 35.8 us, the 80B layer at batch 2 37.5 -> 31.3).  8-bit rows go out
+        // before the poll (between its loads and check they measured 41.6 us
+        // at batch 4 against 36.9 this way).
+        auto tiles = [&]() __attribute__((always_inline)) {
+            if (nsl > 0 && dn1) {
+                load_tile(dt0, a.down, ex[0], lmd, t0 * DRI * lmd.rpw, a.H);
+                if (nsl > 1) load_tile(dt1, a.down, ex[1], lmd, t0 * DRI * lmd.rpw, a.H);
+            }
+            if (wave >= B && sp0 < sh_passes) load_tile(sdt, a.sh_down, 0, lms, r0 + sp0 * lms.rpw, r0 + nr);
+        };
+        constexpr bool kTilesMid = DB == 4;
+        if constexpr (!kTilesMid) {
+            tiles();
+            // Without this the compiler may sink the down tiles' loads below
+            // the polls and the barrier that follow (allowed across an
+            // acquire), so they would start only once the activations are in.
+            asm volatile("" ::: "memory");
         }
-        if (wave >= B && sp0 < sh_passes) load_tile(sdt, a.sh_down, 0, lms, r0 + sp0 * lms.rpw, r0 + nr);
-        // Without this the compiler may sink the down tiles' loads below the
-        // polls and the barrier that follow (allowed across an acquire), so
-        // they would start only once the activations are in.
-        asm volatile("" ::: "memory");
+        auto mid = [&]() __attribute__((always_inline)) {
+            if constexpr (kTilesMid) tiles();
+        };
         // The activations of every owned slot but the last (an eighth polled
         // by each wave) and, on the waves from B on, a share of the shared
         // expert's activations of every token (written in phase A), in one
@@ -333,10 +352,10 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
         if (wave >= B && sh_rows) {
             const int nf = B * np_s, q3 = (nf + nsw - 1) / nsw;
             fetch_slots<DB, 4>(a.h_x, a.I, grp, 0, jl, pr0, pr1, s_hbb, a.hsh_x, a.Is, np_s, min(nf, sp0 * q3),
-                               min(nf, (sp0 + 1) * q3), s_hsh, g, lane, a.err);
+                               min(nf, (sp0 + 1) * q3), s_hsh, g, lane, a.err, mid);
         } else {
             fetch_slots<DB, 0>(a.h_x, a.I, grp, 0, jl, pr0, pr1, s_hbb, a.hsh_x, a.Is, np_s, 0, 0, s_hsh, g, lane,
-                               a.err);
+                               a.err, mid);
         }
         __syncthreads();
         SWQ_STAMP(5);
@@ -346,7 +365,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
                 const int s = grp + kGroups * j;
                 if (j == jl) {  // nsl is the same on every wave
                     fetch_slots<DB, 0>(a.h_x, a.I, grp, jl, jl + 1, pr0, pr1, s_hbb, a.hsh_x, a.Is, np_s, 0, 0,
-                                       s_hsh, g, lane, a.err);
+                                       s_hsh, g, lane, a.err, [] {});
                     __syncthreads();
                 }
                 DTile &dt = (j & 1) ? dt1 : dt0;
