@@ -384,8 +384,10 @@ def decode_measure(args, torch, lib, name, R=None, K=None, W=None, path="auto", 
     """µs per MoE-layer decode step of workload `name` on R resident seeded
     layers (all experts each), cycled with a distinct input per layer.
 
-    K steps are captured in one HIP graph (step i runs layer i mod R).  The
-    first timed replay, bracketed by a synchronize on both sides, gives
+    K steps are captured in one HIP graph (step i runs layer i mod R; by
+    default 480: a replay carries a fixed start-up cost, ~60-100 us on the
+    first timed replay, which 96-step graphs spread into ~1 us per step).
+    The first timed replay, bracketed by a synchronize on both sides, gives
     `value` (K steps exactly); further replays of the same graph, at least
     100 steps in all and at least 11 replays, give the distribution of the
     per-step time over replays (median, p10, p90).  Algorithmic bytes count
@@ -396,7 +398,7 @@ def decode_measure(args, torch, lib, name, R=None, K=None, W=None, path="auto", 
     shape_key, batch = CONFIGS[name]
     shape = synth.SHAPES[shape_key]
     R = R or DEFAULT_REPLICAS.get(name, 48)
-    K = K or max(R, 96)
+    K = K or max(R, 480)
     W = W if W is not None else R
     path = path if path != "auto" else auto_path(batch)
     mask = _lib.SWQ_STAGES_FUSED if path == "fused" else 7
