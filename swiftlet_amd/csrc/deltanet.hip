@@ -95,6 +95,27 @@ __global__ __launch_bounds__(kDnThreads) void deltanet_step_kernel(const DnArgs 
     const int hv = blockIdx.x, hk = hv / a.rep, ri = hv % a.rep;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
 
+    // the state rows of the recurrence's first pass, loaded before the conv
+    // step: they depend on nothing the step computes, and their round trip
+    // then overlaps its loads and the norms
+    const int gl = lane % G;
+    float *st_head = a.state + static_cast<int64_t>(hv) * a.dv * DK;
+    const int row_first = wave * RPW + lane / G;
+    float4 s0[CPL];
+    if (row_first < a.dv) {
+        const float4 *sr = reinterpret_cast<const float4 *>(st_head + static_cast<int64_t>(row_first) * DK);
+#pragma unroll
+        for (int m = 0; m < CPL; ++m) s0[m] = sr[gl + G * m];
+    }
+    // and the gated norm's inputs of this thread's first output (z and the
+    // norm weight), which would otherwise cost a round trip at the end
+    float z0 = 0.f, nw0 = 0.f;
+    if (tid < a.dv) {
+        z0 = z_in(a, hv, tid);
+        nw0 = a.norm_w[tid];
+    }
+    asm volatile("" ::: "memory");
+
     // 1. conv step + silu (acc += w[c][j] * row_j, j = 0..K-1, the newest
     // row last; multiply and add rounded separately as the reference does)
     const int nch = 2 * DK + a.dv;
@@ -148,7 +169,6 @@ __global__ __launch_bounds__(kDnThreads) void deltanet_step_kernel(const DnArgs 
 
     // 3. recurrence: lane group of G lanes per row, chunk m of lane j is
     // chunk j + G*m of the row (G consecutive 16-byte chunks per load)
-    const int gl = lane % G;
     float4 qv[CPL], kv[CPL];
 #pragma unroll
     for (int m = 0; m < CPL; ++m) {
@@ -157,12 +177,11 @@ __global__ __launch_bounds__(kDnThreads) void deltanet_step_kernel(const DnArgs 
                             s_q[e + 3] * scq * (inv * inv));
         kv[m] = make_float4(s_k[e] * sck * inv, s_k[e + 1] * sck * inv, s_k[e + 2] * sck * inv, s_k[e + 3] * sck * inv);
     }
-    float *st_head = a.state + static_cast<int64_t>(hv) * a.dv * DK;
-    for (int row = wave * RPW + lane / G; row < a.dv; row += kDnWaves * RPW) {
+    for (int row = row_first; row < a.dv; row += kDnWaves * RPW) {
         float4 *sr = reinterpret_cast<float4 *>(st_head + static_cast<int64_t>(row) * DK);
         float4 s[CPL];
 #pragma unroll
-        for (int m = 0; m < CPL; ++m) s[m] = sr[gl + G * m];
+        for (int m = 0; m < CPL; ++m) s[m] = row == row_first ? s0[m] : sr[gl + G * m];
         float mem = 0.f;
 #pragma unroll
         for (int m = 0; m < CPL; ++m) {
@@ -195,8 +214,8 @@ __global__ __launch_bounds__(kDnThreads) void deltanet_step_kernel(const DnArgs 
     sso = block_sum(sso, s_part);
     const float sc = 1.0f / __fsqrt_rn(sso / static_cast<float>(a.dv) + a.eps);
     for (int i = tid; i < a.dv; i += kDnThreads) {
-        const float y = s_o[i] * (sc * a.norm_w[i]);
-        a.out[hv * a.dv + i] = y * silu_acc(z_in(a, hv, i));
+        const float y = s_o[i] * (sc * (i == tid ? nw0 : a.norm_w[i]));
+        a.out[hv * a.dv + i] = y * silu_acc(i == tid ? z0 : z_in(a, hv, i));
     }
 }
 
