@@ -15,8 +15,9 @@ namespace swq {
 // The instantiation for this layer's formats, or nullptr: routed and shared
 // gate/up rows in one format, 4- or 8-bit down rows, an 8-bit router and
 // shared-expert gate.  M = ceil(E / 64), as the staged path's routing wave.
+// `one`: the one-expert launch (moe_fused_one.hpp) in the same formats.
 static FusedKernel fused_kernel_for(const QMat &router, const QMat &gate, const QMat &down, int x_dtype, int E,
-                                    bool prenorm, bool batched) {
+                                    bool prenorm, bool batched, bool one) {
     if (router.bits != 8) return nullptr;
     const int m = (E + kWave - 1) / kWave;
     const int M = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
@@ -31,6 +32,7 @@ static FusedKernel fused_kernel_for(const QMat &router, const QMat &gate, const 
         gfmt = gate.cpl == 2 ? kFusedQ8C2 : kFusedQ8C1;
     }
     if (gfmt < 0) return nullptr;
+    if (one) return fused_select_one(x_dtype, gfmt, rc2);
     if (prenorm) return x_dtype == SWQ_F32 && !batched ? fused_select_pn(gfmt, rc2, M) : nullptr;
     if (batched) return x_dtype == SWQ_BF16 ? fused_select_bf16_batch(gfmt, rc2, M) : fused_select_f32_batch(gfmt, rc2, M);
     return x_dtype == SWQ_BF16 ? fused_select_bf16(gfmt, rc2, M) : fused_select_f32(gfmt, rc2, M);
@@ -132,7 +134,10 @@ static FusedKernel fused_plan(const swq_moe_layer *layer, int x_dtype, int batch
     if (layer->moe_intermediate > kMaxInterFused || layer->moe_intermediate % 2 != 0) return nullptr;
     if (prenorm && layer->hidden > kPrenormMaxHidden) return nullptr;
     if (layer->hidden > kFusedMaxHidden || layer->num_experts > kMaxExperts) return nullptr;
-    FusedKernel kern = fused_kernel_for(a.router, a.gate, a.down, x_dtype, layer->num_experts, prenorm, batch > 1);
+    // one routed expert and no shared expert at batch 1: the one-expert launch
+    const bool one = batch == 1 && !prenorm && layer->num_experts == 1 && !layer->has_shared;
+    FusedKernel kern =
+        fused_kernel_for(a.router, a.gate, a.down, x_dtype, layer->num_experts, prenorm, batch > 1, one);
     if (!kern) return nullptr;
     const int blocks = fused_blocks(kern, dev);
     if (blocks <= 0) return nullptr;

@@ -1083,5 +1083,8 @@ FusedKernel fused_select_pn(int gfmt, bool rc2, int M);
 // the same for 2 or 4 tokens (kernels holding kFusedMaxBatch)
 FusedKernel fused_select_bf16_batch(int gfmt, bool rc2, int M);
 FusedKernel fused_select_f32_batch(int gfmt, bool rc2, int M);
+// the one-expert launch (moe_fused_one.hpp; batch 1, one routed expert, no
+// shared expert) for bf16 or f32 activations
+FusedKernel fused_select_one(int x_dtype, int gfmt, bool rc2);
 
 }  // namespace swq
