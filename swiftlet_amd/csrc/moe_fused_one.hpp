@@ -8,9 +8,10 @@
 // rows come back through a second exchange hop, this kernel
 // - computes the router's one logit in every workgroup (on its last wave) and
 //   the weight from it by the same rounds, so no logit crosses workgroups;
-// - spreads the gate/up tiles over every wave of the grid (tile t on wave
-//   t / NB of workgroup t mod NB), each activation published as one (value,
-//   epoch) word for every XCD;
+// - spreads the gate/up tiles over wave pairs of the grid (tile t on pair
+//   t / NB of workgroup t mod NB: its gate rows on the even wave, its up rows
+//   on the odd one, handed over in LDS for the SwiGLU), each activation
+//   published as one (value, epoch) word for every XCD;
 // - has every workgroup poll all the activations into LDS and compute its own
 //   output rows whole, so no partial output crosses workgroups.
 // Tiles, lane maps and reduction orders are moe_fused's, so the results equal
@@ -26,6 +27,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     __shared__ __attribute__((aligned(16))) uint32_t s_hb[kMaxInterFused];  // the expert's activations
     __shared__ int32_t s_ids[1];
     __shared__ float s_w;
+    __shared__ float s_up[kFusedWaves / 2][2 * kWave];  // up rows of each wave pair's tile (at most 2 x 64)
 
     static_assert(sizeof(FusedArgs) <= 1024, "kernel arguments");
     SWQ_TRACE_DECL;
@@ -41,20 +43,21 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     const LaneMap lmd = lane_map(a.down.lpr_log2, lane);
     const LaneMap lmr = lane_map(a.router.lpr_log2, lane);
 
-    // Loads in the order they are needed: the first gate/up tile and its x
-    // slice, the epoch, this wave's first pass of the workgroup's down rows,
-    // then (last wave) the router row and its x slice, whose logit is needed
-    // only for the output.
-    const int t0 = b + NB * wave;  // first gate/up tile of this wave
+    // gate/up tile t on the wave pair t / NB of workgroup t mod NB: its gate
+    // rows on the even wave, its up rows on the odd one
+    const int pair = wave >> 1, is_up = wave & 1;
+    const int t0 = b + NB * pair;
+    const int gu_iters = (a.gu_tpe + NB * (kFusedWaves / 2) - 1) / (NB * (kFusedWaves / 2));  // uniform
     const bool has_g = t0 < a.gu_tpe;
     const bool rwave = wave == kFusedWaves - 1;
     const int passes = (nr + lmd.rpw - 1) / lmd.rpw;  // passes of this workgroup's down rows, pass p on wave p
     const bool has_d = wave < passes;
-    RowTile<GB, GC, 2, GRI> tg, tu;
-    if (has_g) {
-        load_tile(tg, a.gate, 0, lmg, t0 * GRI * lmg.rpw, a.I);
-        load_tile(tu, a.up, 0, lmg, t0 * GRI * lmg.rpw, a.I);
-    }
+    // Loads in the order they are needed: the wave's gate or up rows and their
+    // x slice, the epoch, this wave's first pass of the workgroup's down rows,
+    // then (last wave) the router row and its x slice, whose logit is needed
+    // only for the output.
+    RowTile<GB, GC, 2, GRI> tg;
+    if (has_g) load_tile(tg, is_up ? a.up : a.gate, 0, lmg, t0 * GRI * lmg.rpw, a.I);
     XRaw<XDT, GB, GC> xgr;
     if (has_g) load_xraw<XDT>(xgr, a.gate, lmg, a.x, 0);
     asm volatile("" ::: "memory");
@@ -70,25 +73,32 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     }
     asm volatile("" ::: "memory");
 
-    // ---- gate/up + SwiGLU: the grid's waves, wave-major ----------------------
-    if (has_g) {
+    // ---- gate/up + SwiGLU: wave pairs over the grid ------------------------
+    {
         XSlice<GB, GC, GX> xg;
-        xslice_convert(xg, xgr);
-        for (int t = t0; t < a.gu_tpe; t += NB * kFusedWaves) {
+        if (has_g) xslice_convert(xg, xgr);
+        for (int it = 0; it < gu_iters; ++it) {
+            const int t = t0 + it * NB * (kFusedWaves / 2);
+            const bool live = t < a.gu_tpe;
             const int row0 = t * GRI * lmg.rpw;
-            if (t != t0) {
-                load_tile(tg, a.gate, 0, lmg, row0, a.I);
-                load_tile(tu, a.up, 0, lmg, row0, a.I);
+            float r[GRI];
+            if (live) {
+                if (it > 0) load_tile(tg, is_up ? a.up : a.gate, 0, lmg, row0, a.I);
+                dot_rows(r, tg, is_up ? a.up : a.gate, xg, lmg);
+                if (is_up && lmg.j == lmg.lpr - 1) {
+#pragma unroll
+                    for (int i = 0; i < GRI; ++i) s_up[pair][i * lmg.rpw + lmg.q] = r[i];
+                }
             }
-            float rg[GRI], ru[GRI];
-            dot_rows2(rg, ru, tg, tu, a.gate, a.up, xg, lmg);
-            if (lmg.j == lmg.lpr - 1) {
+            __syncthreads();  // s_up
+            if (live && !is_up && lmg.j == lmg.lpr - 1) {
 #pragma unroll
                 for (int i = 0; i < GRI; ++i) {
                     const int row = row0 + i * lmg.rpw + lmg.q;
-                    if (row < a.I) put_pair(a.h_x + row, swiglu(rg[i], ru[i]), g);
+                    if (row < a.I) put_pair(a.h_x + row, swiglu(r[i], s_up[pair][i * lmg.rpw + lmg.q]), g);
                 }
             }
+            if (it + 1 < gu_iters) __syncthreads();  // s_up is rewritten
         }
         SWQ_STAMP(4);
     }
