@@ -11,10 +11,10 @@
 //      of 4 groups; its first column block also writes x in the layout
 //      gate/up reads (bf16 planes) and the group sums of x;
 //   2. route: softmax, top-k (ties to the lower id), renormalisation and
-//      the shared-expert gate logit per token; the last workgroup to finish
-//      counts the pairs per expert and builds the sorted pair order and the
-//      table of 64-row tiles (routed experts, then the shared expert over
-//      all tokens), and leaves its arrival counter at zero for the next call;
+//      the shared-expert gate logit per token;
+//   2b. group: one workgroup of 1024 threads counts the pairs per expert and
+//      builds the sorted pair order and the table of 64-row tiles (routed
+//      experts, then the shared expert over all tokens);
 //   3. gate/up GEMM over the tile table with the SwiGLU epilogue: h in
 //      sorted pair order, as bf16 hi + lo planes;
 //   4. down GEMM over the same tiles: y rows (f32) in sorted pair order;
@@ -51,7 +51,7 @@ constexpr int kMaxGroups = 64;   // inputs per row <= 4096
 constexpr int kXsPitch = kMaxGroups + 36;  // a K slice's bias term reads up to 31 groups past its first
 constexpr int kTileRows = 64;    // rows of a routed / shared tile
 constexpr int kRouterRows = 16;  // rows of a router tile
-constexpr int kRouteWaves = 4;   // tokens per route workgroup
+constexpr int kRouteWaves = 1;   // tokens per route workgroup, one wave each (512 workgroups at 512 tokens)
 constexpr int kXcds = 8;         // XCDs of the device: workgroup b runs on XCD b % 8
 
 // Workgroups covering `tiles` tiles of `nblk` column blocks under the XCD
@@ -1094,7 +1094,6 @@ struct RouteArgs {
     int32_t *user_ids;
     float *user_w;
     float *sg;                // [T]
-    uint32_t *done;           // finished workgroups: zero on entry; left zero
     int32_t *pos;             // [T, K]: sorted index of pair (t, k)
     int32_t *tok;             // [P + T]: token of each sorted row
     Tile *tiles;
@@ -1152,39 +1151,41 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
     return v;
 }
 
-// The last workgroup: per-expert pair counts (LDS atomics over the ids),
-// exclusive scans of the pair counts and of the tile counts, the tile table
-// (by decreasing row count), and the sorted pair order (a second pass hands
-// out the slots; the order of pairs within an expert does not matter, every
-// row is computed on its own).  The first kHeldIds * 256 ids are loaded at
-// once and kept in registers for the second pass.
+// The grouping workgroup (NT threads): per-expert pair counts (LDS atomics
+// over the ids), exclusive scans of the pair counts and of the tile counts,
+// the tile table (by decreasing row count), and the sorted pair order (a
+// second pass hands out the slots; the order of pairs within an expert does
+// not matter, every row is computed on its own).  The first kHeldIds * NT
+// ids are loaded at once and kept in registers for the second pass.
+template <int NT>
 __device__ void group_pairs(const RouteArgs &a) {
     __shared__ int32_t s_cnt[kMaxExperts];  // counts, then the next free slot
-    __shared__ int32_t s_wsum[2][kPfThreads / kWave];
+    __shared__ int32_t s_wsum[2][NT / kWave];
     __shared__ int32_t s_rows[kTileRows + 1];  // tiles of each row count, then their next slot
-    constexpr int kHeldIds = 16;
+    static_assert(NT <= kMaxExperts && NT <= 4096, "at least one expert and one held id per thread");
+    constexpr int kHeldIds = 4096 / NT;  // every id of 512 tokens x top-8
     constexpr int kBatch = 8;  // ids per thread per pass past the held ones, all in flight at once
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int P = a.T * a.K;
     int held[kHeldIds];
 #pragma unroll
-    for (int u = 0; u < kHeldIds; ++u) held[u] = a.ids[min(tid + u * kPfThreads, P - 1)];
-    for (int e = tid; e < a.E; e += kPfThreads) s_cnt[e] = 0;
-    for (int r = tid; r <= kTileRows; r += kPfThreads) s_rows[r] = 0;
+    for (int u = 0; u < kHeldIds; ++u) held[u] = a.ids[min(tid + u * NT, P - 1)];
+    for (int e = tid; e < a.E; e += NT) s_cnt[e] = 0;
+    for (int r = tid; r <= kTileRows; r += NT) s_rows[r] = 0;
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < kHeldIds; ++u)
-        if (tid + u * kPfThreads < P) atomicAdd(&s_cnt[held[u]], 1);
-    for (int p0 = tid + kHeldIds * kPfThreads; p0 < P; p0 += kBatch * kPfThreads) {
+        if (tid + u * NT < P) atomicAdd(&s_cnt[held[u]], 1);
+    for (int p0 = tid + kHeldIds * NT; p0 < P; p0 += kBatch * NT) {
         int e[kBatch];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) e[u] = a.ids[min(p0 + u * kPfThreads, P - 1)];
+        for (int u = 0; u < kBatch; ++u) e[u] = a.ids[min(p0 + u * NT, P - 1)];
 #pragma unroll
         for (int u = 0; u < kBatch; ++u)
-            if (p0 + u * kPfThreads < P) atomicAdd(&s_cnt[e[u]], 1);
+            if (p0 + u * NT < P) atomicAdd(&s_cnt[e[u]], 1);
     }
     __syncthreads();
-    constexpr int EPT = kMaxExperts / kPfThreads;  // experts per thread
+    constexpr int EPT = kMaxExperts / NT;  // experts per thread
     int cnt[EPT], tl[EPT];
     int csum = 0, tsum = 0;
 #pragma unroll
@@ -1220,7 +1221,7 @@ __device__ void group_pairs(const RouteArgs &a) {
     __syncthreads();
     int c0 = cinc - csum, routed_tiles = 0;
 #pragma unroll
-    for (int w = 0; w < kPfThreads / kWave; ++w) {
+    for (int w = 0; w < NT / kWave; ++w) {
         if (w < wave) c0 += s_wsum[0][w];
         routed_tiles += s_wsum[1][w];
     }
@@ -1244,31 +1245,28 @@ __device__ void group_pairs(const RouteArgs &a) {
         }
         c0 += cnt[i];
     }
-    for (int q = tid; q < sh_tiles; q += kPfThreads) {
+    for (int q = tid; q < sh_tiles; q += NT) {
         const int rows = min(kTileRows, a.T - q * kTileRows);
         a.tiles[atomicAdd(&s_rows[rows], 1)] = Tile{a.E, P + q * kTileRows, rows, 0};
     }
-    if (tid == 0) {
-        *a.n_tiles = routed_tiles + sh_tiles;
-        *a.done = 0u;
-    }
+    if (tid == 0) *a.n_tiles = routed_tiles + sh_tiles;
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < kHeldIds; ++u) {
-        const int p = tid + u * kPfThreads;
+        const int p = tid + u * NT;
         if (p < P) {
             const int q = atomicAdd(&s_cnt[held[u]], 1);
             a.pos[p] = q;
             a.tok[q] = p / a.K;
         }
     }
-    for (int p0 = tid + kHeldIds * kPfThreads; p0 < P; p0 += kBatch * kPfThreads) {
+    for (int p0 = tid + kHeldIds * NT; p0 < P; p0 += kBatch * NT) {
         int e[kBatch];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) e[u] = a.ids[min(p0 + u * kPfThreads, P - 1)];
+        for (int u = 0; u < kBatch; ++u) e[u] = a.ids[min(p0 + u * NT, P - 1)];
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
-            const int p = p0 + u * kPfThreads;
+            const int p = p0 + u * NT;
             if (p >= P) continue;
             const int q = atomicAdd(&s_cnt[e[u]], 1);
             a.pos[p] = q;
@@ -1276,7 +1274,7 @@ __device__ void group_pairs(const RouteArgs &a) {
         }
     }
     if (a.has_shared)
-        for (int t = tid; t < a.T; t += kPfThreads) a.tok[P + t] = t;
+        for (int t = tid; t < a.T; t += NT) a.tok[P + t] = t;
 }
 
 // One token's routing on one wave: the logits of the lane's experts
@@ -1360,9 +1358,8 @@ __device__ __forceinline__ void route_token(const RouteArgs &a, int t, int lane,
 }
 
 template <int XDT>
-__global__ __launch_bounds__(kPfThreads) void pf_route(const RouteArgs a) {
+__global__ __launch_bounds__(kRouteWaves * kWave) void pf_route(const RouteArgs a) {
     __shared__ int32_t s_pick[kRouteWaves][SWQ_MAX_TOPK];
-    __shared__ int s_last;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t = blockIdx.x * kRouteWaves + wave;
     if (t < a.T) {
@@ -1373,20 +1370,13 @@ __global__ __launch_bounds__(kPfThreads) void pf_route(const RouteArgs a) {
         else if (M <= 8) route_token<XDT, 8>(a, t, lane, s_pick[wave]);
         else route_token<XDT, 16>(a, t, lane, s_pick[wave]);
     }
-    // the last workgroup to arrive groups the pairs: the barrier orders this
-    // workgroup's stores before thread 0's release, the release before its
-    // count, the last arrival's acquire before its loads
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        const uint32_t prev = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    group_pairs(a);
 }
+
+// The pairs grouped by expert once every token is routed: its own launch, so
+// the kernel boundary orders the routing's stores before the grouping's
+// loads (an arrival count with a release per routing workgroup cost more).
+constexpr int kGroupThreads = 1024;
+__global__ __launch_bounds__(kGroupThreads) void pf_group(const RouteArgs a) { group_pairs<kGroupThreads>(a); }
 
 // ---------------------------------------------------------------------------
 // combine
@@ -1467,7 +1457,7 @@ PfLayout pf_layout(const swq_moe_layer *l, int T) {
     w.max_tiles = static_cast<int>((P + static_cast<size_t>(kTileRows - 1) * U) / kTileRows) +
                   (l->has_shared ? (T + kTileRows - 1) / kTileRows : 0);
     w.Ih = std::max(l->moe_intermediate, l->has_shared ? l->shared_intermediate : 0);
-    w.header = take(256);  // [0] finished route workgroups, [1] tile count
+    w.header = take(256);  // [1] tile count
     w.kslices = router_kslices(l->hidden);
     w.logits = take(static_cast<size_t>(w.kslices) * T * l->num_experts * 4);  // [slice][T][E] partial logits
     w.sg = take(static_cast<size_t>(T) * 4);
@@ -1700,7 +1690,6 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         r.user_ids = topk_ids;
         r.user_w = topk_weights;
         r.sg = sg;
-        r.done = header;
         r.pos = pos;
         r.tok = tok;
         r.tiles = tiles;
@@ -1712,8 +1701,10 @@ int prefill_impl(const swq_moe_layer *layer, const void *x, int x_dtype, int T, 
         r.norm = layer->norm_topk_prob ? 1 : 0;
         r.has_shared = layer->has_shared ? 1 : 0;
         const int blocks = (T + kRouteWaves - 1) / kRouteWaves;
-        if (bf16x) hipLaunchKernelGGL(pf_route<SWQ_BF16>, dim3(blocks), dim3(kPfThreads), 0, s, r);
-        else hipLaunchKernelGGL(pf_route<SWQ_F32>, dim3(blocks), dim3(kPfThreads), 0, s, r);
+        if (bf16x) hipLaunchKernelGGL(pf_route<SWQ_BF16>, dim3(blocks), dim3(kRouteWaves * kWave), 0, s, r);
+        else hipLaunchKernelGGL(pf_route<SWQ_F32>, dim3(blocks), dim3(kRouteWaves * kWave), 0, s, r);
+        if ((st = launch_status()) != SWQ_OK) return st;
+        hipLaunchKernelGGL(pf_group, dim3(1), dim3(kGroupThreads), 0, s, r);
         if ((st = launch_status()) != SWQ_OK) return st;
     }
     // 3. gate/up + SwiGLU over the tiles
