@@ -3,7 +3,8 @@ static device array inside the library, against swq_moe_decode itself (a
 workspace of its own per layer): equal bit for bit on two calls in a row, the
 second with a smaller input (batch 4 on the three launches, then batch 1 on
 the single launch), then a different, smaller layer sharing the same array,
-then the first layer again; f32 activations, bf16 outputs and the
+a layer of one routed expert (its own single launch on the same array), then
+the first layer again; f32 activations, bf16 outputs and the
 accumulate flag; calls between swq_moe_decode_norm calls; the entry point
 captured in a HIP graph and replayed; in a fresh process, a first call made
 under capture is refused and the next one outside capture recovers.  Every
@@ -58,7 +59,10 @@ def test_noalloc_matches_decode():
                                            norm_topk_prob=False), 77, 0)
     _compare(lib, small, 1, 78)
     _compare(lib, small, 3, 79)
+    one = moe.synth_layer(synth.SHAPES["single-expert-q4"], helpers.SEED, 0)
+    _compare(lib, one, 1, 80)  # the one-expert launch
     _compare(lib, big, 1, helpers.SEED + 43)
+    _compare(lib, one, 1, 81)
     assert _status(lib) == _lib.SWQ_OK
 
 
