@@ -107,6 +107,22 @@ def test_prefill_without_shared_expert():
     _check(shape, xf, out, ids.cpu().numpy(), w.cpu().numpy(), rows=[0, 11, 23])
 
 
+@pytest.mark.parametrize("T", [1, 7, 100])
+def test_prefill_single_expert_layer(T):
+    """One routed expert and no shared expert (the single-expert workload): a
+    one-column router, every pair on expert 0 with weight 1, and tiles of one
+    expert over all the tokens."""
+    import torch
+    shape = synth.SHAPES["single-expert-q4"]
+    print(f"prefill of the single-expert layer, T={T}", flush=True)
+    gpu = moe.synth_layer(shape, helpers.SEED, 0)
+    x, xf = _x(helpers.SEED + 5 + T, T, shape.hidden)
+    out, ids, w = gpu.prefill(x)
+    torch.cuda.synchronize()
+    assert (ids.cpu().numpy() == 0).all() and (w.cpu().numpy() == 1.0).all()
+    _check(shape, xf, out, ids.cpu().numpy(), w.cpu().numpy())
+
+
 def test_prefill_f32_x_bf16_out():
     import torch
     shape = synth.SHAPES["qwen3.6-35b-a3b-q4"]
